@@ -1,0 +1,147 @@
+/*
+ * awq_w4a16.h -- C ABI of the MI355X (gfx950) W4A16 AWQ GEMM library.
+ *
+ * The library replaces the GEMM behind kernels/awq_gemm.py::awq_gemm_forward
+ * (kernels/awq_gemm.py:237-284) of Qwen2-7B-Triton_Engine.  Operand formats
+ * are the reference's, unchanged:
+ *
+ *   x        fp16  [M, K]      row-major, contiguous
+ *   qweight  int32 [K, N/8]    8 int4 codes per word; logical column n of a
+ *                              word sits in nibble ORD[n % 8], ORD =
+ *                              {0,4,1,5,2,6,3,7} (kernels/awq_gemm.py:5-6)
+ *   qzeros   int32 [K/G, N/8]  zero codes, packed the same way
+ *   scales   fp16  [K/G, N]
+ *   out      fp16  [M, N]      out = x @ W, W[k,n] = fp16((q - z) * s),
+ *                              accumulated in fp32, rounded once to fp16
+ *
+ * All pointers are device pointers.  `stream` is a hipStream_t (NULL = the
+ * legacy default stream).  No entry point allocates device memory,
+ * synchronises the host or keeps mutable global state, so every call is
+ * reentrant and can be captured into a HIP graph.  Every entry point returns
+ * AWQ_OK (0) or a negative awq_w4a16_status.
+ */
+#ifndef AWQ_W4A16_H
+#define AWQ_W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AWQ_W4A16_ABI_VERSION 1
+
+typedef enum awq_w4a16_status {
+    AWQ_OK = 0,
+    AWQ_ERR_NULL_POINTER = -1,   /* a required pointer is NULL                        */
+    AWQ_ERR_BAD_DIMS = -2,       /* M < 0, N <= 0, K <= 0, N % 8 != 0 or K % G != 0    */
+    AWQ_ERR_GROUP_SIZE = -3,     /* group size other than 128                          */
+    AWQ_ERR_MISALIGNED = -4,     /* x/out/scales not 16-byte, qweight/qzeros not 4-byte aligned */
+    AWQ_ERR_WORKSPACE = -5,      /* workspace NULL or smaller than required            */
+    AWQ_ERR_LAUNCH = -6,         /* the HIP runtime rejected a kernel launch           */
+    AWQ_ERR_PATH = -7,           /* unknown kernel path, or path cannot serve this M   */
+    AWQ_ERR_TOO_LARGE = -8       /* a dimension > 2^30, or an operand > 2^31-1 bytes   */
+} awq_w4a16_status;
+
+/* Kernel paths.  AUTO lets the shape dispatcher choose (the reference's own
+ * choice is by M alone, kernels/awq_gemm.py:251); the others force one
+ * kernel family, for tests and measurements. */
+typedef enum awq_w4a16_path {
+    AWQ_PATH_AUTO = 0,
+    AWQ_PATH_SKINNY = 1,         /* decode: MFMA GEMV / skinny-M streaming kernel (M <= 64) */
+    AWQ_PATH_TILE = 2            /* prefill: LDS-tiled MFMA GEMM                            */
+} awq_w4a16_path;
+
+/* What the dispatcher will launch for a shape (host-side description). */
+typedef struct awq_w4a16_plan {
+    int32_t path;                /* AWQ_PATH_SKINNY or AWQ_PATH_TILE                       */
+    int32_t variant;             /* kernel variant inside the path                          */
+    int32_t tile_m;              /* rows of x per work unit (skinny: 16, 32 or 64)          */
+    int32_t tile_n;              /* output columns per work unit                            */
+    int32_t rows_per_wave;       /* skinny: K rows per wavefront (32, 64 or 128*q)          */
+    int32_t k_waves;             /* skinny: wavefronts per workgroup along K (1, 2, 4)      */
+    int32_t split_k;             /* workgroups along K; > 1 uses the fp32 workspace         */
+    int32_t block_threads;       /* threads per workgroup                                   */
+    int64_t grid;                /* workgroups in the main launch                           */
+    uint64_t workspace_bytes;    /* fp32 split-K partials [split_k, M, N]; 0 if split_k==1  */
+    uint64_t lds_bytes;          /* dynamic LDS per workgroup                               */
+} awq_w4a16_plan;
+
+/* ABI version of the loaded library (AWQ_W4A16_ABI_VERSION).  No reference
+ * counterpart; lets a binding refuse a mismatched library. */
+int awq_w4a16_abi_version(void);
+
+/* Static text for a status code.  No reference counterpart (the reference
+ * raises no errors for bad operands, kernels/awq_gemm.py:237-284). */
+const char* awq_w4a16_error_string(int status);
+
+/* Host-only: fill *plan with what awq_w4a16_gemm_ex would launch for this
+ * shape and path, after validating the dimensions.  Touches no GPU.
+ * Replaces the M-based dispatch of kernels/awq_gemm.py:251 (M <= 4 ->
+ * dequant + cuBLAS, else the autotuned Triton GEMM of :152-164). */
+int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                       int32_t path, awq_w4a16_plan* plan);
+
+/* Host-only: a skinny-path plan with explicit tuning values (rows_per_wave:
+ * 32, 64 or a multiple of 128 not above K; k_waves: 1, 2 or 4), with the
+ * derived fields (split_k, grid, workspace and LDS bytes) filled in.  For
+ * sweeps; AWQ_ERR_PATH if the values cannot serve the shape. */
+int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                          int32_t rows_per_wave, int32_t k_waves, awq_w4a16_plan* plan);
+
+/* Host-only: bytes of workspace awq_w4a16_gemm needs for this shape
+ * (0 if none).  Replaces the module-global _dequant_buffer of
+ * kernels/awq_gemm.py:234,255-262, which holds K*N fp16 values; the
+ * workspace here holds only fp32 split-K partials.  Returns 0 for invalid
+ * dimensions as well; awq_w4a16_plan_for reports the reason. */
+size_t awq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size);
+size_t awq_w4a16_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                    int32_t path);
+
+/* Host-only: the checks awq_w4a16_gemm_ex performs before launching
+ * (pointers, dimensions, alignment, workspace size), without launching. */
+int awq_w4a16_validate(const void* x, const void* qweight, const void* qzeros,
+                       const void* scales, const void* out, int64_t M, int64_t N,
+                       int64_t K, int32_t group_size, const void* workspace,
+                       size_t workspace_bytes, int32_t path);
+
+/* out[M,N] = x[M,K] @ dequant(qweight, qzeros, scales).
+ * Replaces awq_gemm_forward (kernels/awq_gemm.py:237-284) for a flattened
+ * x (:244-246); the caller allocates `out` (the reference allocates it,
+ * :249) and, when awq_w4a16_workspace_bytes() > 0, `workspace`.
+ * M == 0 is a valid no-op. */
+int awq_w4a16_gemm(const void* x, const int32_t* qweight, const int32_t* qzeros,
+                   const void* scales, void* out, int64_t M, int64_t N, int64_t K,
+                   int32_t group_size, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* As awq_w4a16_gemm, with the kernel path forced (AWQ_PATH_*).  The
+ * workspace must be at least awq_w4a16_workspace_bytes_ex(..., path). */
+int awq_w4a16_gemm_ex(const void* x, const int32_t* qweight, const int32_t* qzeros,
+                      const void* scales, void* out, int64_t M, int64_t N, int64_t K,
+                      int32_t group_size, void* workspace, size_t workspace_bytes,
+                      int32_t path, void* stream);
+
+/* As awq_w4a16_gemm_ex, launching a caller-supplied plan: one from
+ * awq_w4a16_plan_for, or one filled by awq_w4a16_plan_skinny with other
+ * tuning values.  The plan is checked against the
+ * shape first (AWQ_ERR_PATH if inconsistent).  Replaces the per-(M,N,K)
+ * autotuning of kernels/awq_gemm.py:152-164 with an explicit, stateless
+ * choice the caller can sweep. */
+int awq_w4a16_gemm_planned(const void* x, const int32_t* qweight, const int32_t* qzeros,
+                           const void* scales, void* out, int64_t M, int64_t N, int64_t K,
+                           int32_t group_size, void* workspace, size_t workspace_bytes,
+                           const awq_w4a16_plan* plan, void* stream);
+
+/* w[K,N] fp16 = fp16((q - z) * s), the dense dequantised weight, bit-exact.
+ * Replaces _dequant_to_fp16 / _dequant_awq_kernel (kernels/awq_gemm.py:14-87);
+ * it runs the same unpack/dequant device code as the GEMM kernels. */
+int awq_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                      void* w_out, int64_t N, int64_t K, int32_t group_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AWQ_W4A16_H */

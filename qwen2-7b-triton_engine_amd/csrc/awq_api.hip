@@ -1,0 +1,281 @@
+// C ABI of the W4A16 AWQ GEMM library: validation, shape dispatch, launches.
+// Declarations and the reference interfaces they replace: include/awq_w4a16.h.
+#include <limits.h>
+#include <stdint.h>
+
+#include "../../include/awq_w4a16.h"
+#include "awq_kernels.h"
+
+using namespace awq;
+
+namespace {
+
+// Active waves the decode dispatcher aims for: 256 CUs x 4 SIMDs x 2.
+constexpr int64_t kSkinnyTargetWaves = 2048;
+// Largest M the skinny path serves (4 MFMA blocks of 16 rows).
+constexpr int64_t kSkinnyMaxM = 64;
+// M above which AUTO picks the tile kernel.
+constexpr int64_t kAutoSkinnyMaxM = 64;
+// LDS the skinny dispatcher allows one workgroup for its K reduction.
+constexpr uint64_t kSkinnyLdsBudget = 64 * 1024;
+
+constexpr int64_t kIndexLimit = (int64_t)1 << 30;
+// Byte-size limit of any one operand (buffer descriptors carry 32-bit sizes).
+constexpr int64_t kBytesLimit = ((int64_t)1 << 31) - 1;
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int check_dims(int64_t M, int64_t N, int64_t K, int32_t G) {
+    if (G != kGroup) return AWQ_ERR_GROUP_SIZE;
+    if (M < 0 || N <= 0 || K <= 0 || N % 8 != 0 || K % G != 0) return AWQ_ERR_BAD_DIMS;
+    if (M > kIndexLimit || N > kIndexLimit || K > kIndexLimit) return AWQ_ERR_TOO_LARGE;
+    if (K * (N / 2) > kBytesLimit || M * K * 2 > kBytesLimit || M * N * 2 > kBytesLimit)
+        return AWQ_ERR_TOO_LARGE;
+    return AWQ_OK;
+}
+
+bool valid_rows_per_wave(int64_t r, int64_t K) {
+    if (r == 32 || r == 64) return true;
+    return r > 0 && r % kGroup == 0 && r <= K;
+}
+
+int m_blocks_for(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+
+// Fills every field of a skinny plan from (rows_per_wave, k_waves).
+int fill_skinny(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t k_waves, awq_w4a16_plan* p) {
+    if (M > kSkinnyMaxM) return AWQ_ERR_PATH;
+    if (!valid_rows_per_wave(rows_per_wave, K)) return AWQ_ERR_PATH;
+    if (!(k_waves == 1 || k_waves == 2 || k_waves == 4)) return AWQ_ERR_PATH;
+    const int mb = m_blocks_for(M);
+    const int64_t rows_per_block = rows_per_wave * k_waves;
+    p->path = AWQ_PATH_SKINNY;
+    p->variant = 1;
+    p->tile_m = 16 * mb;
+    p->tile_n = kSkinnyCols;
+    p->rows_per_wave = (int32_t)rows_per_wave;
+    p->k_waves = (int32_t)k_waves;
+    p->split_k = (int32_t)((K + rows_per_block - 1) / rows_per_block);
+    p->block_threads = (int32_t)(128 * k_waves);
+    p->grid = skinny_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
+    p->workspace_bytes = p->split_k > 1 ? (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    p->lds_bytes = skinny_lds_bytes((int)M, mb, (int)k_waves);
+    if (p->lds_bytes > kSkinnyLdsBudget) return AWQ_ERR_PATH;
+    return AWQ_OK;
+}
+
+int skinny_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    if (M > kSkinnyMaxM) return AWQ_ERR_PATH;
+    const int mb = m_blocks_for(M);
+    // Most waves along K whose LDS reduction fits the budget.
+    int64_t kw = 4;
+    while (kw > 1 && skinny_lds_bytes((int)M, mb, (int)kw) > kSkinnyLdsBudget) kw /= 2;
+    // Longest K range per wave that still gives the target number of active waves.
+    const int64_t n_ct = (N + kSkinnyCols - 1) / kSkinnyCols;
+    int64_t best = 32;
+    auto waves = [&](int64_t r) { return n_ct * ((K + r - 1) / r); };
+    if (waves(64) >= kSkinnyTargetWaves) best = 64;
+    for (int64_t r = kGroup; r <= K; r += kGroup) {
+        if (waves(r) >= kSkinnyTargetWaves) best = r;
+        else break;
+    }
+    return fill_skinny(M, N, K, best, kw, p);
+}
+
+int tile_plan(int64_t M, int64_t N, int64_t /*K*/, awq_w4a16_plan* p) {
+    p->path = AWQ_PATH_TILE;
+    p->variant = 1;
+    p->tile_m = 128;
+    p->tile_n = 128;
+    p->rows_per_wave = 0;
+    p->k_waves = 1;
+    p->split_k = 1;
+    p->block_threads = 256;
+    p->grid = ((M + 127) / 128) * ((N + 127) / 128);
+    p->workspace_bytes = 0;
+    p->lds_bytes = 0;
+    return AWQ_OK;
+}
+
+// Checks a caller-supplied plan against the shape: it must be exactly what
+// the planner derives from its tuning values.
+int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
+    awq_w4a16_plan q;
+    if (p->path == AWQ_PATH_SKINNY) {
+        if (p->variant != 1) return AWQ_ERR_PATH;
+        const int st = fill_skinny(M, N, K, p->rows_per_wave, p->k_waves, &q);
+        if (st != AWQ_OK) return st;
+    } else if (p->path == AWQ_PATH_TILE) {
+        tile_plan(M, N, K, &q);
+        if (p->variant != q.variant) return AWQ_ERR_PATH;
+    } else {
+        return AWQ_ERR_PATH;
+    }
+    if (p->tile_m != q.tile_m || p->tile_n != q.tile_n || p->split_k != q.split_k ||
+        p->block_threads != q.block_threads || p->grid != q.grid ||
+        p->workspace_bytes != q.workspace_bytes || p->lds_bytes != q.lds_bytes)
+        return AWQ_ERR_PATH;
+    return AWQ_OK;
+}
+
+int check_pointers(const void* x, const void* qweight, const void* qzeros, const void* scales,
+                   const void* out, int64_t M) {
+    if (!qweight || !qzeros || !scales) return AWQ_ERR_NULL_POINTER;
+    if (M > 0 && (!x || !out)) return AWQ_ERR_NULL_POINTER;
+    if (!aligned(qweight, 4) || !aligned(qzeros, 4) || !aligned(scales, 16)) return AWQ_ERR_MISALIGNED;
+    if (M > 0 && (!aligned(x, 16) || !aligned(out, 16))) return AWQ_ERR_MISALIGNED;
+    return AWQ_OK;
+}
+
+int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const void* scales,
+             void* out, int64_t M, int64_t N, int64_t K, void* workspace, const awq_w4a16_plan& p,
+             void* stream) {
+    if (M == 0) return AWQ_OK;
+    GemmArgs a;
+    a.x = static_cast<const half_t*>(x);
+    a.qweight = reinterpret_cast<const uint32_t*>(qweight);
+    a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
+    a.scales = static_cast<const half_t*>(scales);
+    a.out = static_cast<half_t*>(out);
+    a.partials = static_cast<float*>(workspace);
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (p.path == AWQ_PATH_SKINNY) {
+        SkinnyConfig cfg;
+        cfg.m_blocks = p.tile_m / 16;
+        cfg.rows_per_wave = p.rows_per_wave;
+        cfg.kw_count = p.k_waves;
+        cfg.split_k = p.split_k;
+        e = launch_skinny(a, cfg, s);
+        if (e == hipSuccess && p.split_k > 1) e = launch_splitk_reduce(a.partials, a.out, M * N, p.split_k, s);
+    } else {
+        TileConfig cfg;
+        cfg.variant = p.variant;
+        cfg.tile_m = p.tile_m;
+        cfg.tile_n = p.tile_n;
+        e = launch_tile(a, cfg, s);
+    }
+    return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int awq_w4a16_abi_version(void) { return AWQ_W4A16_ABI_VERSION; }
+
+const char* awq_w4a16_error_string(int status) {
+    switch (status) {
+        case AWQ_OK: return "ok";
+        case AWQ_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case AWQ_ERR_BAD_DIMS: return "bad dimensions: need M >= 0, N > 0, K > 0, N % 8 == 0, K % group_size == 0";
+        case AWQ_ERR_GROUP_SIZE: return "unsupported group size (only 128 is served)";
+        case AWQ_ERR_MISALIGNED: return "misaligned pointer: x, out, scales need 16-byte, qweight/qzeros 4-byte alignment";
+        case AWQ_ERR_WORKSPACE: return "workspace missing or too small";
+        case AWQ_ERR_LAUNCH: return "HIP kernel launch failed";
+        case AWQ_ERR_PATH: return "kernel path or plan cannot serve this shape";
+        case AWQ_ERR_TOO_LARGE: return "a dimension exceeds 2^30, or an operand exceeds 2^31-1 bytes";
+        default: return "unknown status";
+    }
+}
+
+int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
+                          int32_t k_waves, awq_w4a16_plan* plan) {
+    if (!plan) return AWQ_ERR_NULL_POINTER;
+    const int d = check_dims(M, N, K, group_size);
+    if (d != AWQ_OK) return d;
+    return fill_skinny(M, N, K, rows_per_wave, k_waves, plan);
+}
+
+int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t path,
+                       awq_w4a16_plan* plan) {
+    if (!plan) return AWQ_ERR_NULL_POINTER;
+    const int d = check_dims(M, N, K, group_size);
+    if (d != AWQ_OK) return d;
+    switch (path) {
+        case AWQ_PATH_AUTO:
+            return M <= kAutoSkinnyMaxM ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);
+        case AWQ_PATH_SKINNY: return skinny_plan(M, N, K, plan);
+        case AWQ_PATH_TILE: return tile_plan(M, N, K, plan);
+        default: return AWQ_ERR_PATH;
+    }
+}
+
+size_t awq_w4a16_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t path) {
+    awq_w4a16_plan p;
+    if (awq_w4a16_plan_for(M, N, K, group_size, path, &p) != AWQ_OK) return 0;
+    return (size_t)p.workspace_bytes;
+}
+
+size_t awq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size) {
+    return awq_w4a16_workspace_bytes_ex(M, N, K, group_size, AWQ_PATH_AUTO);
+}
+
+int awq_w4a16_validate(const void* x, const void* qweight, const void* qzeros, const void* scales,
+                       const void* out, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                       const void* workspace, size_t workspace_bytes, int32_t path) {
+    awq_w4a16_plan p;
+    int st = awq_w4a16_plan_for(M, N, K, group_size, path, &p);
+    if (st != AWQ_OK) return st;
+    st = check_pointers(x, qweight, qzeros, scales, out, M);
+    if (st != AWQ_OK) return st;
+    if (M > 0 && p.workspace_bytes > 0) {
+        if (!workspace || workspace_bytes < p.workspace_bytes) return AWQ_ERR_WORKSPACE;
+        if (!aligned(workspace, 16)) return AWQ_ERR_MISALIGNED;
+    }
+    return AWQ_OK;
+}
+
+int awq_w4a16_gemm_ex(const void* x, const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                      void* out, int64_t M, int64_t N, int64_t K, int32_t group_size, void* workspace,
+                      size_t workspace_bytes, int32_t path, void* stream) {
+    const int st = awq_w4a16_validate(x, qweight, qzeros, scales, out, M, N, K, group_size, workspace,
+                                      workspace_bytes, path);
+    if (st != AWQ_OK) return st;
+    awq_w4a16_plan p;
+    awq_w4a16_plan_for(M, N, K, group_size, path, &p);
+    return run_plan(x, qweight, qzeros, scales, out, M, N, K, workspace, p, stream);
+}
+
+int awq_w4a16_gemm(const void* x, const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                   void* out, int64_t M, int64_t N, int64_t K, int32_t group_size, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+    return awq_w4a16_gemm_ex(x, qweight, qzeros, scales, out, M, N, K, group_size, workspace,
+                             workspace_bytes, AWQ_PATH_AUTO, stream);
+}
+
+int awq_w4a16_gemm_planned(const void* x, const int32_t* qweight, const int32_t* qzeros,
+                           const void* scales, void* out, int64_t M, int64_t N, int64_t K,
+                           int32_t group_size, void* workspace, size_t workspace_bytes,
+                           const awq_w4a16_plan* plan, void* stream) {
+    if (!plan) return AWQ_ERR_NULL_POINTER;
+    int st = check_dims(M, N, K, group_size);
+    if (st != AWQ_OK) return st;
+    st = check_plan(M, N, K, plan);
+    if (st != AWQ_OK) return st;
+    st = check_pointers(x, qweight, qzeros, scales, out, M);
+    if (st != AWQ_OK) return st;
+    if (M > 0 && plan->workspace_bytes > 0) {
+        if (!workspace || workspace_bytes < plan->workspace_bytes) return AWQ_ERR_WORKSPACE;
+        if (!aligned(workspace, 16)) return AWQ_ERR_MISALIGNED;
+    }
+    return run_plan(x, qweight, qzeros, scales, out, M, N, K, workspace, *plan, stream);
+}
+
+int awq_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, void* w_out,
+                      int64_t N, int64_t K, int32_t group_size, void* stream) {
+    int st = check_dims(0, N, K, group_size);
+    if (st != AWQ_OK) return st;
+    if (!qweight || !qzeros || !scales || !w_out) return AWQ_ERR_NULL_POINTER;
+    if (!aligned(qweight, 4) || !aligned(qzeros, 4) || !aligned(scales, 16) || !aligned(w_out, 16))
+        return AWQ_ERR_MISALIGNED;
+    const hipError_t e = launch_dequant(reinterpret_cast<const uint32_t*>(qweight),
+                                        reinterpret_cast<const uint32_t*>(qzeros),
+                                        static_cast<const half_t*>(scales), static_cast<half_t*>(w_out),
+                                        (int)N, (int)K, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
+}
+
+}  // extern "C"

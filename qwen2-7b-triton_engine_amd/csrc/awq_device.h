@@ -1,0 +1,137 @@
+// Device helpers shared by the W4A16 AWQ kernels (gfx950 / CDNA4).
+//
+// AWQ packing (kernels/awq_gemm.py:5-6): logical column c of a packed int32
+// word sits in nibble ORD[c], ORD = {0,4,1,5,2,6,3,7}.  Equivalently the low
+// 16 bits of a word hold columns 0,2,4,6 (nibbles 0..3) and the high 16 bits
+// hold columns 1,3,5,7 (nibbles 4..7).  So `(w >> 4t) & 0x000F000F` puts
+// column 2t in the low half-word and column 2t+1 in the high half-word: the
+// order is made for packed 16-bit arithmetic.
+//
+// int4 -> fp16 without conversion instructions: 0x6400 is fp16 1024.0, whose
+// unit in the last place is exactly 1, so OR-ing a code c (0..15) into the
+// low mantissa bits gives the fp16 value 1024 + c (Kim et al., 2022, "Who Says
+// Elephants Can't Run").  (1024 + q) - (1024 + z) = q - z is then exact in
+// fp16, and one fp16 multiply by the scale rounds once, to nearest even: the
+// reference's fp16((q - z) * s) bit for bit (kernels/awq_gemm.py:59,223).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace awq {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGroup = 128;          // AWQ group size served by the kernels
+constexpr uint32_t kMagic2 = 0x64006400u;  // fp16 pair (1024.0, 1024.0)
+
+__device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ __forceinline__ uint32_t as_u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Nibble shift of logical column c (0..7): 4 * ORD[c].
+__device__ __forceinline__ constexpr int col_shift(int c) { return 4 * ((c >> 1) + (c & 1) * 4); }
+
+// (1024 + code) of logical columns (2t, 2t+1) of one word, as an fp16 pair.
+__device__ __forceinline__ uint32_t pair_magic(uint32_t w, int t) {
+    return ((w >> (4 * t)) & 0x000F000Fu) | kMagic2;
+}
+
+// fp16 pair (1024 + z, 1024 + z) for logical column c of a packed zero word.
+__device__ __forceinline__ uint32_t zero_splat(uint32_t zw, int c) {
+    const uint32_t z = (zw >> col_shift(c)) & 0xFu;
+    return kMagic2 | z | (z << 16);
+}
+
+// Exact dequant of one packed word: out[c] = fp16((q_c - z_c) * s_c) in
+// logical column order c = 0..7.
+__device__ __forceinline__ half8_t dequant_word(uint32_t w, uint32_t zw, half8_t s) {
+    half8_t out;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const half2_t d = as_h2(pair_magic(w, t)) - as_h2(pair_magic(zw, t));  // exact q - z
+        const half2_t s2 = {s[2 * t], s[2 * t + 1]};
+        const half2_t r = d * s2;                                             // one RNE rounding
+        out[2 * t] = r.x;
+        out[2 * t + 1] = r.y;
+    }
+    return out;
+}
+
+// k-pairs of two words a (row r) and b (row r + 1) of the same packed column:
+// kp[c] = fp16 pair (1024 + q[r][c], 1024 + q[r+1][c]) for logical column c.
+// v_perm_b32 gathers the low (high) half-words of a and b into one register,
+// so each column's two rows land in the two halves of one 32-bit value.
+__device__ __forceinline__ void kpairs_magic(uint32_t a, uint32_t b, uint32_t kp[8]) {
+    const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);  // a[15:0] | b[15:0] << 16
+    const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);  // a[31:16] | b[31:16] << 16
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        kp[2 * u] = ((lo >> (4 * u)) & 0x000F000Fu) | kMagic2;      // column 2u (nibble u)
+        kp[2 * u + 1] = ((hi >> (4 * u)) & 0x000F000Fu) | kMagic2;  // column 2u+1 (nibble u+4)
+    }
+}
+
+// (x & mask) | magic in one VALU op.  gfx9 VOP3 encodings cannot carry two
+// literal constants, so the compiler splits this into v_and + v_or; spelling
+// v_and_or_b32 with the mask in an SGPR and the magic in a VGPR keeps it one.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(magic));
+    return r;
+}
+
+// As kpairs_magic, but without the shifts by 4: nibbles 1 and 3 of each
+// half-word are masked in place (mask 0x00F000F0), which yields the fp16
+// value 1024 + 16*q.  Columns 2, 3, 6, 7 (c with bit 1 set) therefore come
+// out scaled by 16; the matching zero splat is (1024 + 16*z), the difference
+// 16*(q - z) is still exact in fp16, and the caller folds 1/16 into the scale.
+__device__ __forceinline__ void kpairs_magic_x16(uint32_t a, uint32_t b, uint32_t kp[8]) {
+    const uint32_t magic = kMagic2;
+    const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
+    const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
+    const uint32_t lo8 = lo >> 8;
+    const uint32_t hi8 = hi >> 8;
+    kp[0] = and_or(lo, 0x000F000Fu, magic);
+    kp[2] = and_or(lo, 0x00F000F0u, magic);
+    kp[4] = and_or(lo8, 0x000F000Fu, magic);
+    kp[6] = and_or(lo8, 0x00F000F0u, magic);
+    kp[1] = and_or(hi, 0x000F000Fu, magic);
+    kp[3] = and_or(hi, 0x00F000F0u, magic);
+    kp[5] = and_or(hi8, 0x000F000Fu, magic);
+    kp[7] = and_or(hi8, 0x00F000F0u, magic);
+}
+
+// Whether kpairs_magic_x16 returns logical column c scaled by 16.
+__device__ __forceinline__ constexpr bool x16_column(int c) { return (c >> 1) & 1; }
+
+// Zero splat matching kpairs_magic_x16 for logical column c.
+__device__ __forceinline__ uint32_t zero_splat_x16(uint32_t zw, int c) {
+    const uint32_t z = (zw >> col_shift(c)) & 0xFu;
+    const uint32_t zz = x16_column(c) ? (z << 4) : z;
+    return kMagic2 | zz | (zz << 16);
+}
+
+__device__ __forceinline__ floatx4 mfma16x16x32(half8_t a, half8_t b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Raw buffer resources (gfx9 descriptor word 3 = 0x00020000).  Reads whose
+// VGPR offset lies at or beyond num_bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ half8_t buf_load_h8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+}  // namespace awq

@@ -1,0 +1,129 @@
+"""ctypes binding of ``lib/libawq_w4a16.so`` (C ABI: ``include/awq_w4a16.h``).
+
+Loading fails loudly when the library is missing: there is no fallback path.
+Build it with ``python qwen2-7b-triton_engine_amd/build.py``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libawq_w4a16.so")
+
+ABI_VERSION = 1
+
+AWQ_OK = 0
+AWQ_ERR_NULL_POINTER = -1
+AWQ_ERR_BAD_DIMS = -2
+AWQ_ERR_GROUP_SIZE = -3
+AWQ_ERR_MISALIGNED = -4
+AWQ_ERR_WORKSPACE = -5
+AWQ_ERR_LAUNCH = -6
+AWQ_ERR_PATH = -7
+AWQ_ERR_TOO_LARGE = -8
+
+PATH_AUTO = 0
+PATH_SKINNY = 1
+PATH_TILE = 2
+PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile"}
+
+
+class Plan(ctypes.Structure):
+    """Mirror of ``awq_w4a16_plan``."""
+
+    _fields_ = [
+        ("path", ctypes.c_int32),
+        ("variant", ctypes.c_int32),
+        ("tile_m", ctypes.c_int32),
+        ("tile_n", ctypes.c_int32),
+        ("rows_per_wave", ctypes.c_int32),
+        ("k_waves", ctypes.c_int32),
+        ("split_k", ctypes.c_int32),
+        ("block_threads", ctypes.c_int32),
+        ("grid", ctypes.c_int64),
+        ("workspace_bytes", ctypes.c_uint64),
+        ("lds_bytes", ctypes.c_uint64),
+    ]
+
+    def as_dict(self) -> dict:
+        d = {name: getattr(self, name) for name, _ in self._fields_}
+        d["path_name"] = PATH_NAMES.get(self.path, "?")
+        return d
+
+
+# Every symbol include/awq_w4a16.h declares, with its ctypes signature.
+_VP = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+SIGNATURES = {
+    "awq_w4a16_abi_version": (ctypes.c_int, []),
+    "awq_w4a16_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "awq_w4a16_plan_for": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_skinny": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
+    "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
+    "awq_w4a16_validate": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
+                                          ctypes.c_size_t, _I32]),
+    "awq_w4a16_gemm": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
+                                      ctypes.c_size_t, _VP]),
+    "awq_w4a16_gemm_ex": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
+                                         ctypes.c_size_t, _I32, _VP]),
+    "awq_w4a16_gemm_planned": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
+                                              ctypes.c_size_t, ctypes.POINTER(Plan), _VP]),
+    "awq_w4a16_dequant": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I32, _VP]),
+}
+
+_lib = None
+
+
+class AwqNativeError(RuntimeError):
+    """A nonzero status from the HIP library."""
+
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: status {status}: {error_string(status)}")
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"W4A16 AWQ HIP library not found at {LIB_PATH}; build it with "
+                "`python qwen2-7b-triton_engine_amd/build.py` (there is no fallback path)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        if L.awq_w4a16_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {L.awq_w4a16_abi_version()}, expected {ABI_VERSION}")
+        _lib = L
+    return _lib
+
+
+def error_string(status: int) -> str:
+    return lib().awq_w4a16_error_string(status).decode()
+
+
+def check(status: int, where: str) -> None:
+    if status != AWQ_OK:
+        raise AwqNativeError(status, where)
+
+
+def plan_for(M: int, N: int, K: int, group_size: int = 128, path: int = PATH_AUTO) -> Plan:
+    p = Plan()
+    check(lib().awq_w4a16_plan_for(M, N, K, group_size, path, ctypes.byref(p)), "awq_w4a16_plan_for")
+    return p
+
+
+def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, group_size: int = 128) -> Plan:
+    p = Plan()
+    check(lib().awq_w4a16_plan_skinny(M, N, K, group_size, rows_per_wave, k_waves, ctypes.byref(p)),
+          "awq_w4a16_plan_skinny")
+    return p
+
+
+def workspace_bytes(M: int, N: int, K: int, group_size: int = 128, path: int = PATH_AUTO) -> int:
+    return int(lib().awq_w4a16_workspace_bytes_ex(M, N, K, group_size, path))

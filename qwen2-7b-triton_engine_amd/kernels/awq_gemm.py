@@ -1,0 +1,161 @@
+"""W4A16 AWQ GEMM/GEMV: drop-in for ``kernels/awq_gemm.py`` of
+Qwen2-7B-Triton_Engine, running hand-written gfx950 HIP kernels through the C
+ABI of ``lib/libawq_w4a16.so`` (``include/awq_w4a16.h``).
+
+Same entry point, argument meaning and result as the reference
+(``kernels/awq_gemm.py:237-284``)::
+
+    awq_gemm_forward(x, qweight, qzeros, scales, group_size=128) -> Tensor
+
+* ``x``        fp16 ``[..., K]`` (any leading shape; flattened to ``[M, K]``)
+* ``qweight``  int32 ``[K, N/8]``, AWQ nibble order (column n in nibble
+  ``[0,4,1,5,2,6,3,7][n % 8]``)
+* ``qzeros``   int32 ``[K/G, N/8]``, same packing
+* ``scales``   fp16 ``[K/G, N]``; ``N = scales.shape[1]`` as in the reference
+* returns a new fp16 ``[..., N]`` = ``x @ dequant(W)``, fp32 accumulation.
+
+Differences from the reference, all on the error side: operands are checked
+and a bad call raises ``ValueError`` (the reference launches anyway and lets
+Triton's masks hide out-of-range reads); only ``group_size == 128`` is served
+(the value the reference always uses, ``model/config.py:22``).  The work runs
+on the caller's current stream; the split-K workspace comes from torch's
+caching allocator, so the call is capturable into a CUDA/HIP graph.  There is
+no Triton, no torch dequant and no other fallback: without the HIP library
+the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+
+__all__ = ["awq_gemm_forward", "awq_gemm_forward_ex", "_dequant_to_fp16", "plan"]
+
+
+def _check_operands(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
+                    scales: torch.Tensor, group_size: int):
+    """Shape/dtype checks shared by every entry point; returns (K, N)."""
+    if x.dtype != torch.float16:
+        raise ValueError(f"x must be float16, got {x.dtype}")
+    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
+        raise ValueError(f"qweight/qzeros must be int32, got {qweight.dtype}/{qzeros.dtype}")
+    if scales.dtype != torch.float16:
+        raise ValueError(f"scales must be float16, got {scales.dtype}")
+    if qweight.dim() != 2 or qzeros.dim() != 2 or scales.dim() != 2 or x.dim() < 1:
+        raise ValueError("qweight, qzeros and scales must be 2-D and x at least 1-D")
+    if group_size != 128:
+        raise ValueError(f"group_size {group_size} is not served (only 128)")
+    K = x.shape[-1]
+    N = scales.shape[1]
+    if N % 8 != 0 or N == 0:
+        raise ValueError(f"N = scales.shape[1] = {N} must be a positive multiple of 8")
+    if K == 0 or K % group_size != 0:
+        raise ValueError(f"K = {K} must be a positive multiple of group_size {group_size}")
+    if tuple(qweight.shape) != (K, N // 8):
+        raise ValueError(f"qweight shape {tuple(qweight.shape)} != (K, N/8) = {(K, N // 8)}")
+    if tuple(qzeros.shape) != (K // group_size, N // 8):
+        raise ValueError(f"qzeros shape {tuple(qzeros.shape)} != (K/G, N/8) = {(K // group_size, N // 8)}")
+    if tuple(scales.shape) != (K // group_size, N):
+        raise ValueError(f"scales shape {tuple(scales.shape)} != (K/G, N) = {(K // group_size, N)}")
+    return K, N
+
+
+def _check_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"operands must be on a ROCm device, got {dev}")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"all operands must be on {dev}, got {t.device}")
+    return dev
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _prepare(x, qweight, qzeros, scales, group_size):
+    K, N = _check_operands(x, qweight, qzeros, scales, group_size)
+    dev = _check_device(x, qweight, qzeros, scales)
+    in_shape = x.shape
+    x_flat = x.reshape(-1, K).contiguous()          # kernels/awq_gemm.py:244-246
+    # The reference passes strides to Triton; the C ABI takes dense operands.
+    qweight = qweight.contiguous()
+    qzeros = qzeros.contiguous()
+    scales = scales.contiguous()
+    return in_shape, x_flat, qweight, qzeros, scales, K, N, dev
+
+
+def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=None, plan_obj=None):
+    L = _native.lib()
+    if plan_obj is not None:
+        ws_bytes = int(plan_obj.workspace_bytes)
+    else:
+        ws_bytes = _native.workspace_bytes(M, N, K, group_size, _native.PATH_AUTO if path is None else path)
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes else None
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    args = (_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out), M, N, K, group_size,
+            _ptr(ws), ws_bytes)
+    with torch.cuda.device(dev):
+        if plan_obj is not None:
+            st = L.awq_w4a16_gemm_planned(*args, ctypes.byref(plan_obj), stream)
+            where = "awq_w4a16_gemm_planned"
+        elif path is None:
+            st = L.awq_w4a16_gemm(*args, stream)
+            where = "awq_w4a16_gemm"
+        else:
+            st = L.awq_w4a16_gemm_ex(*args, path, stream)
+            where = "awq_w4a16_gemm_ex"
+    _native.check(st, where)
+
+
+def awq_gemm_forward(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
+                     scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """``x @ dequant(qweight, qzeros, scales)`` in fp16 (kernels/awq_gemm.py:237-284)."""
+    in_shape, x_flat, qweight, qzeros, scales, K, N, dev = _prepare(x, qweight, qzeros, scales, group_size)
+    M = x_flat.shape[0]
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev)
+    return out.view(*in_shape[:-1], N)
+
+
+def awq_gemm_forward_ex(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
+                        scales: torch.Tensor, group_size: int = 128, path: int | None = None,
+                        plan_obj: "_native.Plan | None" = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``awq_gemm_forward`` with the kernel path forced (``_native.PATH_*``) or an
+    explicit plan (``_native.plan_skinny`` / ``plan``), optionally into ``out``."""
+    in_shape, x_flat, qweight, qzeros, scales, K, N, dev = _prepare(x, qweight, qzeros, scales, group_size)
+    M = x_flat.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    elif out.dtype != torch.float16 or tuple(out.shape) != (M, N) or not out.is_contiguous() or out.device != dev:
+        raise ValueError("out must be a contiguous fp16 [M, N] tensor on the operands' device")
+    _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=path, plan_obj=plan_obj)
+    return out.view(*in_shape[:-1], N)
+
+
+def _dequant_to_fp16(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+                     out_buf: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Dense fp16 ``[K, N]`` weight ``(q - z) * s`` into ``out_buf``, bit-exact
+    (kernels/awq_gemm.py:66-87)."""
+    K = qweight.shape[0]
+    N = scales.shape[1]
+    dummy_x = torch.empty((0, K), dtype=torch.float16, device=qweight.device)
+    _check_operands(dummy_x, qweight, qzeros, scales, group_size)
+    dev = _check_device(qweight, qzeros, scales, out_buf)
+    if out_buf.dtype != torch.float16 or tuple(out_buf.shape) != (K, N) or not out_buf.is_contiguous():
+        raise ValueError(f"out_buf must be a contiguous fp16 tensor of shape {(K, N)}")
+    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    with torch.cuda.device(dev):
+        st = _native.lib().awq_w4a16_dequant(_ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out_buf),
+                                             N, K, group_size, stream)
+    _native.check(st, "awq_w4a16_dequant")
+    return out_buf
+
+
+def plan(M: int, N: int, K: int, group_size: int = 128, path: int = _native.PATH_AUTO) -> dict:
+    """What the shape dispatcher launches for ``[M, K] x [K, N]`` (host only)."""
+    return _native.plan_for(M, N, K, group_size, path).as_dict()
