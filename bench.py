@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W4A16 AWQ GEMM (one GPU).
+
+Headline workload (the decode sweep over Qwen2-7B linear shapes): one step is
+every AWQ GEMM of one decode token of a 28-layer Qwen2-7B stack, called as
+the reference engine calls them -- fused QKV (3584->4608), o_proj
+(3584->3584), fused gate||up (3584->37888), down_proj (18944->3584)
+(model/qwen2.py:104,156,183,196) -- at M = 1, 4 and 16 rows: 3 x 28 x 4 =
+336 GEMMs over 28 distinct layers of random-init AWQ weights (3.4 GB, far
+beyond the 256 MB MALL), captured once into a HIP graph and replayed.
+``value`` = algorithmic bytes of the step / step time (GB/s).
+
+Also reported (not part of ``value``): per-GEMM times of every per-layer
+shape at M in {1, 4, 16}, the prefill gate||up GEMM at M = 2048 (TFLOP/s), the
+down_proj M-sweep, the roofline of the dominant kernel, and the reference's
+CPU dequant + matmul timed on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "qwen2-7b-triton_engine_amd")
+for _p in (PKG, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "W4A16 AWQ GEMM: decode HBM GB/s vs peak; prefill TFLOPS vs MFMA peak"
+LAYERS = 28
+HIDDEN, INTER = 3584, 18944
+ENGINE_SHAPES = (("qkv_proj", HIDDEN, 4608), ("o_proj", HIDDEN, HIDDEN),
+                 ("gate_up_proj", HIDDEN, 2 * INTER), ("down_proj", INTER, HIDDEN))
+DECODE_M = (1, 4, 16)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_weights(torch, dev, k, n, seed):
+    """Random AWQ operands: uniform int4 codes and zeros, scales U[0.002, 0.02]."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    qw = torch.randint(-2**31, 2**31 - 1, (k, n // 8), generator=g, device=dev, dtype=torch.int32)
+    qz = torch.randint(-2**31, 2**31 - 1, (k // 128, n // 8), generator=g, device=dev, dtype=torch.int32)
+    sc = (torch.rand((k // 128, n), generator=g, device=dev) * 0.018 + 0.002).half()
+    return qw, qz, sc
+
+
+def graph_of(torch, fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    return g
+
+
+def time_graph(torch, g, reps):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def kernel_family(_native, m, n, k):
+    return _native.PATH_NAMES[_native.plan_for(m, n, k).path]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of timed CPU work")
+    ap.add_argument("--no-extras", action="store_true", help="headline only (for profiling runs)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "this build has no multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from kernels import _native
+    from kernels.awq_gemm import awq_gemm_forward
+    from kernels.awq_roofline import (HBM_PEAK_BPS, MFMA_F16_DENSE_PEAK_FLOPS, QWEN2_7B_LINEARS,
+                                      algorithmic_bytes, flops)
+
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device {props.name} CUs={props.multi_processor_count}")
+
+    # ---- synthetic operands: 28 layers x 4 fused projections ---------------
+    t0 = time.time()
+    layers = []
+    for li in range(LAYERS):
+        layers.append({name: make_weights(torch, dev, k, n, 1000 * li + j)
+                       for j, (name, k, n) in enumerate(ENGINE_SHAPES)})
+    gx = torch.Generator(device=dev)
+    gx.manual_seed(7)
+    xs = {(m, k): torch.randn((m, k), generator=gx, device=dev).half() for m in DECODE_M for k in (HIDDEN, INTER)}
+    torch.cuda.synchronize()
+    log(f"operands ready in {time.time() - t0:.1f}s")
+
+    def step():
+        outs = []
+        for m in DECODE_M:
+            for li in range(LAYERS):
+                for name, k, n in ENGINE_SHAPES:
+                    outs.append(awq_gemm_forward(xs[(m, k)], *layers[li][name]))
+        return outs
+
+    step()  # eager: sizes the shared workspace before capture
+    torch.cuda.synchronize()
+    g = graph_of(torch, step)
+    step_bytes = sum(algorithmic_bytes(m, n, k) for m in DECODE_M for _ in range(LAYERS)
+                     for _, k, n in ENGINE_SHAPES)
+    step_flops = sum(flops(m, n, k) for m in DECODE_M for _ in range(LAYERS) for _, k, n in ENGINE_SHAPES)
+
+    # ---- timed region: exactly `steps` steps ------------------------------
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t_step = e0.elapsed_time(e1) / 1e3 / args.steps
+    value = step_bytes / t_step / 1e9
+    log(f"decode step: {t_step * 1e3:.3f} ms, {value:.1f} GB/s ({value / (HBM_PEAK_BPS / 1e9):.3f} of HBM peak)")
+    del g
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 activations x int4 weights, fp32 accumulate",
+        "data": "synthetic: random-init AWQ int4 weights (uniform codes/zeros, scales U[0.002,0.02]), x~N(0,1)",
+        "config": {
+            "workload": "Qwen2-7B decode sweep: 28 layers x {qkv 3584->4608, o 3584->3584, gate_up 3584->37888, "
+                        "down 18944->3584} x M in {1,4,16}, one HIP graph per step",
+            "layers": LAYERS, "M": list(DECODE_M), "group_size": 128,
+            "gemms_per_step": len(DECODE_M) * LAYERS * len(ENGINE_SHAPES),
+            "bytes_per_step": step_bytes, "flops_per_step": step_flops,
+        },
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+    # ---- per-GEMM times: each (M, shape) over the 28 layers in one graph ---
+    def per_launch(m, k, n, weights):
+        x = xs[(m, k)] if (m, k) in xs else torch.randn((m, k), device=dev).half()
+        awq_gemm_forward(x, *weights[0])
+        torch.cuda.synchronize()
+        gg = graph_of(torch, lambda: [awq_gemm_forward(x, *w) for w in weights])
+        gg.replay()
+        t = min(time_graph(torch, gg, 3) for _ in range(3)) / len(weights)
+        del gg
+        return t
+
+    per_gemm = []
+    family_time, family_bytes, family_launches = {}, {}, {}
+    for m in DECODE_M:
+        for name, k, n in ENGINE_SHAPES:
+            t = per_launch(m, k, n, [layers[li][name] for li in range(LAYERS)])
+            b = algorithmic_bytes(m, n, k)
+            fam = kernel_family(_native, m, n, k)
+            per_gemm.append({"shape": name, "M": m, "K": k, "N": n, "us": round(t * 1e6, 2), "kernel": fam,
+                             "GBps": round(b / t / 1e9, 1), "hbm_frac": round(b / t / HBM_PEAK_BPS, 3)})
+            family_time[fam] = family_time.get(fam, 0.0) + t * LAYERS
+            family_bytes[fam] = family_bytes.get(fam, 0) + b * LAYERS
+            family_launches[fam] = family_launches.get(fam, 0) + LAYERS
+    dom = max(family_time, key=family_time.get)
+    avg_t = family_time[dom] / family_launches[dom]
+    avg_b = family_bytes[dom] / family_launches[dom]
+    achieved = avg_b / avg_t / 1e9
+    result["roofline"] = {
+        "bound": "hbm",
+        "kernel": {"gemv": "awq_gemv_kernel", "skinny": "awq_skinny_kernel", "tile": "awq_tile_kernel"}[dom],
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_BPS / 1e9,
+        "unit": "GB/s",
+        "frac": round(achieved / (HBM_PEAK_BPS / 1e9), 4),
+        "traffic": None,
+        "bytes_per_launch": round(avg_b),
+        "avg_launch_us": round(avg_t * 1e6, 3),
+        "launches_per_step": family_launches[dom],
+        "share_of_step_time": round(family_time[dom] / sum(family_time.values()), 3),
+    }
+    result["per_gemm_engine_shapes"] = per_gemm
+
+    if not args.no_extras:
+        # unfused per-layer shapes of the decode sweep (q/k/v/o, gate/up, down)
+        sweep = []
+        for name, k, n in QWEN2_7B_LINEARS:
+            if name in ("v_proj", "up_proj", "o_proj"):
+                continue  # same shape as k_proj / gate_proj / q_proj
+            copies = max(2, min(LAYERS, int(640e6 // (k * n // 2)) + 1))
+            ws = [make_weights(torch, dev, k, n, 50000 + c) for c in range(copies)]
+            for m in DECODE_M:
+                t = per_launch(m, k, n, ws)
+                b = algorithmic_bytes(m, n, k)
+                sweep.append({"shape": name, "M": m, "K": k, "N": n, "us": round(t * 1e6, 2),
+                              "kernel": kernel_family(_native, m, n, k),
+                              "GBps": round(b / t / 1e9, 1), "hbm_frac": round(b / t / HBM_PEAK_BPS, 3)})
+            del ws
+        result["per_gemm_unfused_shapes"] = sweep
+
+        # prefill gate||up at M = 2048 and the down_proj M-sweep
+        def mfma_point(m, k, n, copies):
+            ws = [make_weights(torch, dev, k, n, 70000 + c) for c in range(copies)]
+            t = per_launch(m, k, n, ws)
+            f = flops(m, n, k)
+            b = algorithmic_bytes(m, n, k)
+            del ws
+            return {"M": m, "K": k, "N": n, "us": round(t * 1e6, 2), "kernel": kernel_family(_native, m, n, k),
+                    "TFLOPs": round(f / t / 1e12, 1), "mfma_frac": round(f / t / MFMA_F16_DENSE_PEAK_FLOPS, 4),
+                    "GBps": round(b / t / 1e9, 1), "hbm_frac": round(b / t / HBM_PEAK_BPS, 3)}
+
+        result["prefill_gate_up"] = mfma_point(2048, HIDDEN, 2 * INTER, 4)
+        result["down_m_sweep"] = [mfma_point(m, INTER, HIDDEN, 4 if m >= 512 else 16) for m in (1, 8, 64, 512, 2048)]
+
+    # ---- CPU baseline: the reference's dequant + matmul on the host --------
+    if not args.no_cpu_baseline:
+        from oracle.cpu_baseline import time_cpu_baseline  # reported baseline, not the product
+
+        threads = min(16, os.cpu_count() or 1)
+        total_b = total_t = 0.0
+        spent = 0.0
+        done = []
+        for j, (name, k, n) in enumerate(ENGINE_SHAPES):
+            if spent >= args.cpu_budget:
+                break
+            qw, qz, sc = (t.cpu() for t in layers[0][name])
+            x = xs[(1, k)].cpu()
+            r = time_cpu_baseline(x, qw, qz, sc, reps=3, warmup=1, threads=threads,
+                                  budget_s=max(1.0, args.cpu_budget - spent))
+            spent += r["median_s"] * (r["reps"] + 1)
+            total_b += algorithmic_bytes(1, n, k)
+            total_t += r["median_s"]
+            done.append(name)
+        result["cpu_baseline"] = {
+            "value": round(total_b / total_t / 1e9, 3),
+            "unit": "GB/s",
+            "cores": r["threads"],
+            "kind": "port",
+            "sample": f"layer 0 GEMMs {'+'.join(done)} at M=1 (torch-CPU restatement of the reference's "
+                      f"dequant+matmul, test/compare_benchmark.py:72-95), 1 warm-up + median of up to 3",
+            "cpu_model": r["cpu_model"],
+            "os_cpu_count": r["os_cpu_count"],
+            "seconds_per_step_equiv": round(total_t / total_b * step_bytes, 3),
+        }
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

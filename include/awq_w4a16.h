@@ -41,7 +41,7 @@ typedef enum awq_w4a16_status {
     AWQ_ERR_WORKSPACE = -5,      /* workspace NULL or smaller than required            */
     AWQ_ERR_LAUNCH = -6,         /* the HIP runtime rejected a kernel launch           */
     AWQ_ERR_PATH = -7,           /* unknown kernel path, or path cannot serve this M   */
-    AWQ_ERR_TOO_LARGE = -8       /* a dimension > 2^30, or an operand > 2^31-1 bytes   */
+    AWQ_ERR_TOO_LARGE = -8       /* M, K > 2^30, N > 2^20 or an operand > 2^31-1 bytes */
 } awq_w4a16_status;
 
 /* Kernel paths.  AUTO lets the shape dispatcher choose (the reference's own
@@ -49,8 +49,9 @@ typedef enum awq_w4a16_status {
  * kernel family, for tests and measurements. */
 typedef enum awq_w4a16_path {
     AWQ_PATH_AUTO = 0,
-    AWQ_PATH_SKINNY = 1,         /* decode: MFMA GEMV / skinny-M streaming kernel (M <= 64) */
-    AWQ_PATH_TILE = 2            /* prefill: LDS-tiled MFMA GEMM                            */
+    AWQ_PATH_SKINNY = 1,         /* decode: MFMA skinny-M streaming kernel (M <= 64)         */
+    AWQ_PATH_TILE = 2,           /* prefill: LDS-tiled MFMA GEMM                            */
+    AWQ_PATH_GEMV = 3            /* decode: VALU dot2 GEMV (M <= 2)                         */
 } awq_w4a16_path;
 
 /* What the dispatcher will launch for a shape (host-side description). */
@@ -63,8 +64,10 @@ typedef struct awq_w4a16_plan {
     int32_t k_waves;             /* skinny: wavefronts per workgroup along K (1, 2, 4)      */
     int32_t split_k;             /* workgroups along K; > 1 uses the fp32 workspace         */
     int32_t block_threads;       /* threads per workgroup                                   */
-    int64_t grid;                /* workgroups in the main launch                           */
-    uint64_t workspace_bytes;    /* fp32 split-K partials [split_k, M, N]; 0 if split_k==1  */
+    int32_t factored_scale;      /* skinny: 1 = scale applied per group sum, 0 = per weight */
+    int32_t reserved;            /* zero                                                    */
+    int64_t grid;                /* workgroups in the one launch                            */
+    uint64_t workspace_bytes;    /* split_k > 1: arrival counters + fp32 partials; else 0   */
     uint64_t lds_bytes;          /* dynamic LDS per workgroup                               */
 } awq_w4a16_plan;
 
@@ -84,17 +87,30 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size,
                        int32_t path, awq_w4a16_plan* plan);
 
 /* Host-only: a skinny-path plan with explicit tuning values (rows_per_wave:
- * 32, 64 or a multiple of 128 not above K; k_waves: 1, 2 or 4), with the
- * derived fields (split_k, grid, workspace and LDS bytes) filled in.  For
- * sweeps; AWQ_ERR_PATH if the values cannot serve the shape. */
+ * 32, 64 or a multiple of 128 not above K; k_waves: 1, 2 or 4; variant: 1
+ * pipelined or 2 plain main loop; factored_scale: 0 or 1), with the derived
+ * fields (split_k, grid, workspace and LDS bytes) filled in.  For sweeps;
+ * AWQ_ERR_PATH if the values cannot serve the shape. */
 int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
-                          int32_t rows_per_wave, int32_t k_waves, awq_w4a16_plan* plan);
+                          int32_t rows_per_wave, int32_t k_waves, int32_t variant,
+                          int32_t factored_scale, awq_w4a16_plan* plan);
+
+/* Host-only: a GEMV-path plan (M <= 2) with explicit tuning values
+ * (rows_per_wave: 16, 32 or 64; k_waves: 1, 2, 4 or 8). */
+int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                        int32_t rows_per_wave, int32_t k_waves, awq_w4a16_plan* plan);
 
 /* Host-only: bytes of workspace awq_w4a16_gemm needs for this shape
  * (0 if none).  Replaces the module-global _dequant_buffer of
  * kernels/awq_gemm.py:234,255-262, which holds K*N fp16 values; the
- * workspace here holds only fp32 split-K partials.  Returns 0 for invalid
- * dimensions as well; awq_w4a16_plan_for reports the reason. */
+ * workspace here holds, for split-K launches, a block of uint32 arrival
+ * counters (first awq_w4a16_counter_bytes() bytes) followed by the fp32
+ * partial sums.  The counter block must be zero-filled before the
+ * workspace is first used; every call leaves it zero again, so one zeroed
+ * workspace serves any number of calls, as long as calls that share it do
+ * not run concurrently.  Returns 0 for invalid dimensions as well;
+ * awq_w4a16_plan_for reports the reason. */
+size_t awq_w4a16_counter_bytes(void);
 size_t awq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size);
 size_t awq_w4a16_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int32_t group_size,
                                     int32_t path);

@@ -19,6 +19,9 @@ constexpr int64_t kAutoSkinnyMaxM = 64;
 // LDS the skinny dispatcher allows one workgroup for its K reduction.
 constexpr uint64_t kSkinnyLdsBudget = 64 * 1024;
 
+// Compute units of an MI355X.
+constexpr int64_t kCUs = 256;
+
 constexpr int64_t kIndexLimit = (int64_t)1 << 30;
 // Byte-size limit of any one operand (buffer descriptors carry 32-bit sizes).
 constexpr int64_t kBytesLimit = ((int64_t)1 << 31) - 1;
@@ -28,7 +31,7 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 int check_dims(int64_t M, int64_t N, int64_t K, int32_t G) {
     if (G != kGroup) return AWQ_ERR_GROUP_SIZE;
     if (M < 0 || N <= 0 || K <= 0 || N % 8 != 0 || K % G != 0) return AWQ_ERR_BAD_DIMS;
-    if (M > kIndexLimit || N > kIndexLimit || K > kIndexLimit) return AWQ_ERR_TOO_LARGE;
+    if (M > kIndexLimit || N > kMaxN || K > kIndexLimit) return AWQ_ERR_TOO_LARGE;
     if (K * (N / 2) > kBytesLimit || M * K * 2 > kBytesLimit || M * N * 2 > kBytesLimit)
         return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
@@ -41,44 +44,88 @@ bool valid_rows_per_wave(int64_t r, int64_t K) {
 
 int m_blocks_for(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 
-// Fills every field of a skinny plan from (rows_per_wave, k_waves).
-int fill_skinny(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t k_waves, awq_w4a16_plan* p) {
+// Fills every field of a skinny plan from its tuning values.
+int fill_skinny(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t k_waves, int64_t variant,
+                int64_t factored, awq_w4a16_plan* p) {
     if (M > kSkinnyMaxM) return AWQ_ERR_PATH;
     if (!valid_rows_per_wave(rows_per_wave, K)) return AWQ_ERR_PATH;
     if (!(k_waves == 1 || k_waves == 2 || k_waves == 4)) return AWQ_ERR_PATH;
     const int mb = m_blocks_for(M);
+    // Kernel instances that exist: see launch_skinny.
+    if (variant == 1) {
+        if (mb != 1) return AWQ_ERR_PATH;
+    } else if (variant == 2) {
+        if (mb == 4 && factored) return AWQ_ERR_PATH;
+    } else {
+        return AWQ_ERR_PATH;
+    }
+    if (factored != 0 && factored != 1) return AWQ_ERR_PATH;
     const int64_t rows_per_block = rows_per_wave * k_waves;
     p->path = AWQ_PATH_SKINNY;
-    p->variant = 1;
+    p->variant = (int32_t)variant;
     p->tile_m = 16 * mb;
     p->tile_n = kSkinnyCols;
     p->rows_per_wave = (int32_t)rows_per_wave;
     p->k_waves = (int32_t)k_waves;
     p->split_k = (int32_t)((K + rows_per_block - 1) / rows_per_block);
     p->block_threads = (int32_t)(128 * k_waves);
+    p->factored_scale = (int32_t)factored;
+    p->reserved = 0;
     p->grid = skinny_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
-    p->workspace_bytes = p->split_k > 1 ? (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    p->workspace_bytes =
+        p->split_k > 1 ? skinny_counter_bytes() + (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
     p->lds_bytes = skinny_lds_bytes((int)M, mb, (int)k_waves);
     if (p->lds_bytes > kSkinnyLdsBudget) return AWQ_ERR_PATH;
+    if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
 }
 
+// Defaults measured on MI355X (K range per wave x waves per workgroup swept
+// per shape): two waves along K per workgroup; 512 rows per wave for the long
+// K of down_proj, 256 otherwise; the chunk-pipelined main loop for one row
+// block, the plain loop (smaller register file, more waves) for more.
 int skinny_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (M > kSkinnyMaxM) return AWQ_ERR_PATH;
     const int mb = m_blocks_for(M);
-    // Most waves along K whose LDS reduction fits the budget.
-    int64_t kw = 4;
+    int64_t kw = 2;
     while (kw > 1 && skinny_lds_bytes((int)M, mb, (int)kw) > kSkinnyLdsBudget) kw /= 2;
-    // Longest K range per wave that still gives the target number of active waves.
-    const int64_t n_ct = (N + kSkinnyCols - 1) / kSkinnyCols;
-    int64_t best = 32;
-    auto waves = [&](int64_t r) { return n_ct * ((K + r - 1) / r); };
-    if (waves(64) >= kSkinnyTargetWaves) best = 64;
-    for (int64_t r = kGroup; r <= K; r += kGroup) {
-        if (waves(r) >= kSkinnyTargetWaves) best = r;
-        else break;
-    }
-    return fill_skinny(M, N, K, best, kw, p);
+    int64_t r = K >= 8192 ? 512 : 256;
+    while (r > K) r /= 2;
+    if (r < kGroup) r = r >= 64 ? 64 : 32;
+    const int64_t variant = mb == 1 ? 1 : 2;
+    return fill_skinny(M, N, K, r, kw, variant, mb == 4 ? 0 : 1, p);
+}
+
+// Largest M the GEMV path serves.
+constexpr int64_t kGemvMaxM = 2;
+
+int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t k_waves, awq_w4a16_plan* p) {
+    if (M > kGemvMaxM) return AWQ_ERR_PATH;
+    if (!(rows_per_wave == 16 || rows_per_wave == 32 || rows_per_wave == 64)) return AWQ_ERR_PATH;
+    if (!(k_waves == 1 || k_waves == 2 || k_waves == 4 || k_waves == 8)) return AWQ_ERR_PATH;
+    const int64_t rows_per_block = rows_per_wave * k_waves;
+    p->path = AWQ_PATH_GEMV;
+    p->variant = 1;
+    p->tile_m = (int32_t)kGemvMaxM;
+    p->tile_n = 512;
+    p->rows_per_wave = (int32_t)rows_per_wave;
+    p->k_waves = (int32_t)k_waves;
+    p->split_k = (int32_t)((K + rows_per_block - 1) / rows_per_block);
+    p->block_threads = (int32_t)(64 * k_waves);
+    p->factored_scale = 1;
+    p->reserved = 0;
+    p->grid = gemv_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
+    p->workspace_bytes =
+        p->split_k > 1 ? skinny_counter_bytes() + (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    p->lds_bytes = 0;
+    if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
+    return AWQ_OK;
+}
+
+// Measured default: 64 rows per wave, 8 waves per workgroup along K (the
+// fewest split-K workgroups, whose cross-workgroup reduction is the cost).
+int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    return fill_gemv(M, N, K, 64, 8, p);
 }
 
 int tile_plan(int64_t M, int64_t N, int64_t /*K*/, awq_w4a16_plan* p) {
@@ -90,6 +137,8 @@ int tile_plan(int64_t M, int64_t N, int64_t /*K*/, awq_w4a16_plan* p) {
     p->k_waves = 1;
     p->split_k = 1;
     p->block_threads = 256;
+    p->factored_scale = 0;
+    p->reserved = 0;
     p->grid = ((M + 127) / 128) * ((N + 127) / 128);
     p->workspace_bytes = 0;
     p->lds_bytes = 0;
@@ -101,12 +150,14 @@ int tile_plan(int64_t M, int64_t N, int64_t /*K*/, awq_w4a16_plan* p) {
 int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
     awq_w4a16_plan q;
     if (p->path == AWQ_PATH_SKINNY) {
-        if (p->variant != 1) return AWQ_ERR_PATH;
-        const int st = fill_skinny(M, N, K, p->rows_per_wave, p->k_waves, &q);
+        const int st = fill_skinny(M, N, K, p->rows_per_wave, p->k_waves, p->variant, p->factored_scale, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_TILE) {
         tile_plan(M, N, K, &q);
         if (p->variant != q.variant) return AWQ_ERR_PATH;
+    } else if (p->path == AWQ_PATH_GEMV) {
+        const int st = fill_gemv(M, N, K, p->rows_per_wave, p->k_waves, &q);
+        if (st != AWQ_OK) return st;
     } else {
         return AWQ_ERR_PATH;
     }
@@ -136,7 +187,7 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
     a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
     a.scales = static_cast<const half_t*>(scales);
     a.out = static_cast<half_t*>(out);
-    a.partials = static_cast<float*>(workspace);
+    a.partials = nullptr;
     a.M = (int)M;
     a.N = (int)N;
     a.K = (int)K;
@@ -148,8 +199,22 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         cfg.rows_per_wave = p.rows_per_wave;
         cfg.kw_count = p.k_waves;
         cfg.split_k = p.split_k;
-        e = launch_skinny(a, cfg, s);
-        if (e == hipSuccess && p.split_k > 1) e = launch_splitk_reduce(a.partials, a.out, M * N, p.split_k, s);
+        cfg.variant = p.variant;
+        cfg.factored = p.factored_scale != 0;
+        uint32_t* counters = static_cast<uint32_t*>(workspace);
+        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                              skinny_counter_bytes())
+                                   : nullptr;
+        e = launch_skinny(a, cfg, counters, s);
+    } else if (p.path == AWQ_PATH_GEMV) {
+        GemvConfig cfg;
+        cfg.rows_per_wave = p.rows_per_wave;
+        cfg.kw_count = p.k_waves;
+        cfg.split_k = p.split_k;
+        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                              skinny_counter_bytes())
+                                   : nullptr;
+        e = launch_gemv(a, cfg, static_cast<uint32_t*>(workspace), s);
     } else {
         TileConfig cfg;
         cfg.variant = p.variant;
@@ -176,17 +241,27 @@ const char* awq_w4a16_error_string(int status) {
         case AWQ_ERR_WORKSPACE: return "workspace missing or too small";
         case AWQ_ERR_LAUNCH: return "HIP kernel launch failed";
         case AWQ_ERR_PATH: return "kernel path or plan cannot serve this shape";
-        case AWQ_ERR_TOO_LARGE: return "a dimension exceeds 2^30, or an operand exceeds 2^31-1 bytes";
+        case AWQ_ERR_TOO_LARGE: return "M or K exceeds 2^30, N exceeds 2^20, or an operand exceeds 2^31-1 bytes";
         default: return "unknown status";
     }
 }
 
 int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
-                          int32_t k_waves, awq_w4a16_plan* plan) {
+                          int32_t k_waves, int32_t variant, int32_t factored_scale, awq_w4a16_plan* plan) {
     if (!plan) return AWQ_ERR_NULL_POINTER;
     const int d = check_dims(M, N, K, group_size);
     if (d != AWQ_OK) return d;
-    return fill_skinny(M, N, K, rows_per_wave, k_waves, plan);
+    return fill_skinny(M, N, K, rows_per_wave, k_waves, variant, factored_scale, plan);
+}
+
+size_t awq_w4a16_counter_bytes(void) { return skinny_counter_bytes(); }
+
+int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
+                        int32_t k_waves, awq_w4a16_plan* plan) {
+    if (!plan) return AWQ_ERR_NULL_POINTER;
+    const int d = check_dims(M, N, K, group_size);
+    if (d != AWQ_OK) return d;
+    return fill_gemv(M, N, K, rows_per_wave, k_waves, plan);
 }
 
 int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t path,
@@ -196,8 +271,10 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
     if (d != AWQ_OK) return d;
     switch (path) {
         case AWQ_PATH_AUTO:
+            if (M <= kGemvMaxM) return gemv_plan(M, N, K, plan);
             return M <= kAutoSkinnyMaxM ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);
         case AWQ_PATH_SKINNY: return skinny_plan(M, N, K, plan);
+        case AWQ_PATH_GEMV: return gemv_plan(M, N, K, plan);
         case AWQ_PATH_TILE: return tile_plan(M, N, K, plan);
         default: return AWQ_ERR_PATH;
     }

@@ -134,4 +134,17 @@ __device__ __forceinline__ half8_t buf_load_h8(__amdgpu_buffer_rsrc_t r, uint32_
     return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
+// Device-scope (cache policy SC1) 16-byte store and load: coherent across
+// the XCDs of the device without whole-L2 maintenance.
+constexpr int kCpolSC1 = 16;
+__device__ __forceinline__ void buf_store_f4_device(floatx4 v, __amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, 0, kCpolSC1);
+}
+__device__ __forceinline__ floatx4 buf_load_f4_device(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, kCpolSC1));
+}
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima): every vector
+// memory operation of this wave, stores included, has completed.
+__device__ __forceinline__ void wait_vm_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 }  // namespace awq

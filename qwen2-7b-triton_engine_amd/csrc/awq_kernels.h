@@ -24,6 +24,14 @@ struct SkinnyConfig {
     int rows_per_wave;       // K rows per wave: 32, 64 or a multiple of 128
     int kw_count;            // waves per workgroup along K (partials added in LDS): 1, 2 or 4
     int split_k;             // workgroups along K: ceil(K / (rows_per_wave * kw_count))
+    int variant;             // main loop: 1 chunked software pipeline, 2 plain loop
+    bool factored;           // scale applied to group sums (true) or to each weight (false)
+};
+
+struct GemvConfig {
+    int rows_per_wave;       // K rows per wave: 16, 32 or 64 (inside one 128-row group)
+    int kw_count;            // waves per workgroup along K: 1, 2, 4 or 8
+    int split_k;             // workgroups along K
 };
 
 struct TileConfig {
@@ -34,16 +42,26 @@ struct TileConfig {
 hipError_t launch_dequant(const uint32_t* qweight, const uint32_t* qzeros, const half_t* scales,
                           half_t* w, int N, int K, hipStream_t stream);
 
-hipError_t launch_skinny(const GemmArgs& a, const SkinnyConfig& cfg, hipStream_t stream);
+// counters: skinny_counter_bytes() of zero-filled uint32 arrival counters
+// (left zero on return); a.partials: split_k * M * N floats (split_k > 1).
+hipError_t launch_skinny(const GemmArgs& a, const SkinnyConfig& cfg, uint32_t* counters, hipStream_t stream);
 size_t skinny_lds_bytes(int M, int m_blocks, int kw_count);
+int64_t skinny_pairs(int N);
 int64_t skinny_blocks(int N, int K, int rows_per_wave, int kw_count);
+size_t skinny_counter_bytes();
 
-hipError_t launch_splitk_reduce(const float* partials, half_t* out, int64_t mn, int split_k,
-                                hipStream_t stream);
+// Same workspace contract as launch_skinny (counters, then partials).
+hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream);
+int64_t gemv_strips(int N);
+int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
 
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, hipStream_t stream);
 
 // Output columns per skinny wave.
 constexpr int kSkinnyCols = 128;
+// Arrival-counter block at the start of a split-K workspace: one uint32 per
+// pair of 128-column tiles, so N up to kCounterBytes / 4 * 256 columns.
+constexpr size_t kCounterBytes = 16384;
+constexpr int64_t kMaxN = (int64_t)(kCounterBytes / 4) * 2 * kSkinnyCols;
 
 }  // namespace awq

@@ -26,7 +26,8 @@ AWQ_ERR_TOO_LARGE = -8
 PATH_AUTO = 0
 PATH_SKINNY = 1
 PATH_TILE = 2
-PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile"}
+PATH_GEMV = 3
+PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile", PATH_GEMV: "gemv"}
 
 
 class Plan(ctypes.Structure):
@@ -41,6 +42,8 @@ class Plan(ctypes.Structure):
         ("k_waves", ctypes.c_int32),
         ("split_k", ctypes.c_int32),
         ("block_threads", ctypes.c_int32),
+        ("factored_scale", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("grid", ctypes.c_int64),
         ("workspace_bytes", ctypes.c_uint64),
         ("lds_bytes", ctypes.c_uint64),
@@ -60,7 +63,10 @@ SIGNATURES = {
     "awq_w4a16_abi_version": (ctypes.c_int, []),
     "awq_w4a16_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "awq_w4a16_plan_for": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(Plan)]),
-    "awq_w4a16_plan_skinny": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_skinny": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
+                                             ctypes.POINTER(Plan)]),
+    "awq_w4a16_counter_bytes": (ctypes.c_size_t, []),
+    "awq_w4a16_plan_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
     "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
     "awq_w4a16_validate": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
@@ -118,11 +124,25 @@ def plan_for(M: int, N: int, K: int, group_size: int = 128, path: int = PATH_AUT
     return p
 
 
-def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, group_size: int = 128) -> Plan:
+def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant: int = 2,
+                factored_scale: int | None = None, group_size: int = 128) -> Plan:
+    if factored_scale is None:
+        factored_scale = 0 if M > 32 else 1
     p = Plan()
-    check(lib().awq_w4a16_plan_skinny(M, N, K, group_size, rows_per_wave, k_waves, ctypes.byref(p)),
-          "awq_w4a16_plan_skinny")
+    check(lib().awq_w4a16_plan_skinny(M, N, K, group_size, rows_per_wave, k_waves, variant, factored_scale,
+                                      ctypes.byref(p)), "awq_w4a16_plan_skinny")
     return p
+
+
+def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, group_size: int = 128) -> Plan:
+    p = Plan()
+    check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, rows_per_wave, k_waves, ctypes.byref(p)),
+          "awq_w4a16_plan_gemv")
+    return p
+
+
+def counter_bytes() -> int:
+    return int(lib().awq_w4a16_counter_bytes())
 
 
 def workspace_bytes(M: int, N: int, K: int, group_size: int = 128, path: int = PATH_AUTO) -> int:

@@ -18,10 +18,19 @@ Differences from the reference, all on the error side: operands are checked
 and a bad call raises ``ValueError`` (the reference launches anyway and lets
 Triton's masks hide out-of-range reads); only ``group_size == 128`` is served
 (the value the reference always uses, ``model/config.py:22``).  The work runs
-on the caller's current stream; the split-K workspace comes from torch's
-caching allocator, so the call is capturable into a CUDA/HIP graph.  There is
-no Triton, no torch dequant and no other fallback: without the HIP library
-the call raises.
+on the caller's current stream, one kernel launch per call.  There is no
+Triton, no torch dequant and no other fallback: without the HIP library the
+call raises.
+
+Workspace: like the reference's module-global ``_dequant_buffer``
+(kernels/awq_gemm.py:234,255-262) the module keeps one buffer per device,
+grown on demand -- here it holds split-K partial sums and the kernels'
+arrival counters (zero-filled once; each call leaves them zero).  Calls that
+share a device must therefore not run concurrently on different streams, the
+same single-stream use the reference makes of its buffer.  The buffer is
+graph-capture safe once it is large enough: capture after one eager call of
+the largest shape, as the reference's engine warms up before capturing
+(inference/engine.py:43-52); growing it during a capture raises.
 """
 from __future__ import annotations
 
@@ -76,6 +85,26 @@ def _ptr(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
 
 
+# Per-device workspace buffers.  Earlier (smaller) buffers stay referenced so
+# that graphs captured with them keep valid memory.
+_workspaces: dict = {}
+_WS_ALIGN = 1 << 20
+
+
+def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    bufs = _workspaces.setdefault(dev.index, [])
+    if bufs and bufs[-1].numel() * 4 >= nbytes:
+        return bufs[-1]
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            f"awq_gemm workspace must grow to {nbytes} bytes during graph capture; run the "
+            "largest shape once eagerly before capturing")
+    size = (nbytes + _WS_ALIGN - 1) // _WS_ALIGN * _WS_ALIGN
+    buf = torch.zeros(size // 4, dtype=torch.float32, device=dev)
+    bufs.append(buf)
+    return buf
+
+
 def _prepare(x, qweight, qzeros, scales, group_size):
     K, N = _check_operands(x, qweight, qzeros, scales, group_size)
     dev = _check_device(x, qweight, qzeros, scales)
@@ -94,7 +123,9 @@ def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path
         ws_bytes = int(plan_obj.workspace_bytes)
     else:
         ws_bytes = _native.workspace_bytes(M, N, K, group_size, _native.PATH_AUTO if path is None else path)
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes else None
+    ws = _workspace(dev, ws_bytes) if ws_bytes else None
+    if ws is not None:
+        ws_bytes = ws.numel() * 4
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     args = (_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out), M, N, K, group_size,
             _ptr(ws), ws_bytes)

@@ -47,6 +47,8 @@ def _paths_for(m):
     paths = [_native.PATH_TILE]
     if m <= 64:
         paths.insert(0, _native.PATH_SKINNY)
+    if m <= 2:
+        paths.insert(0, _native.PATH_GEMV)
     return paths
 
 
@@ -143,12 +145,12 @@ _SHAPES = {name: (k, n) for name, k, n in QWEN2_7B_LINEARS + QWEN2_7B_FUSED}
 
 
 @pytest.mark.parametrize("name", ["q_proj", "k_proj", "gate_proj", "down_proj", "qkv_proj", "gate_up_proj"])
-@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("m", [1, 2, 4, 16])
 def test_gemm_decode_shapes(gpu, name, m):
     k, n = _SHAPES[name]
     x, qw, qz, s = O.make_inputs(m, k, n, seed=0)
     y_ref = x.astype(np.float64) @ O.dequant_awq_f32eval(qw, qz, s).astype(np.float64)
-    for path in (None, _native.PATH_SKINNY):
+    for path in (None, _native.PATH_SKINNY) + ((_native.PATH_GEMV,) if m <= 2 else ()):
         print(f"decode {name} M={m} path={path}", flush=True)
         y = _run(gpu, x, qw, qz, s, path=path)
         _assert_close(y, y_ref, f"{name} M={m} path={path}")
@@ -188,20 +190,57 @@ def test_gemm_prefill_gate_up(gpu):
 # Split-K plans, determinism, API behaviour
 # --------------------------------------------------------------------------
 
-@pytest.mark.parametrize("m", [1, 16, 32, 64])
+@pytest.mark.parametrize("m", [1, 3, 16, 20, 32, 64])
 def test_skinny_plans_agree(gpu, m):
-    k, n = 3584, 512
+    """Every skinny main-loop variant, scale mode, K range per wave and K
+    wave count gives the same result within tolerance (split-K included)."""
+    k, n = 3584, 520
     x, qw, qz, s = O.make_inputs(m, k, n, seed=4)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)
-    for rpw in (32, 64, 128, 256, 512, 3584):
-        for kw in (1, 2, 4):
-            try:
-                p = _native.plan_skinny(m, n, k, rpw, kw)
-            except _native.AwqNativeError:
-                continue
-            print(f"skinny plan M={m} rows_per_wave={rpw} k_waves={kw}", flush=True)
+    tried = 0
+    for variant in (1, 2):
+        for factored in (0, 1):
+            for rpw in (32, 64, 128, 256, 384, 3584):
+                for kw in (1, 2, 4):
+                    try:
+                        p = _native.plan_skinny(m, n, k, rpw, kw, variant, factored)
+                    except _native.AwqNativeError:
+                        continue
+                    print(f"skinny plan M={m} v={variant} f={factored} rows_per_wave={rpw} k_waves={kw}", flush=True)
+                    y = _run(gpu, x, qw, qz, s, plan_obj=p)
+                    _assert_close(y, y_ref, f"M={m} v={variant} f={factored} rpw={rpw} kw={kw}")
+                    tried += 1
+    assert tried >= 12
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_gemv_plans_agree(gpu, m):
+    """Every GEMV K range per wave and K wave count, split-K included."""
+    k, n = 3584, 1032
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=14)
+    y_ref = O.awq_gemm_oracle(x, qw, qz, s)
+    for rpw in (16, 32, 64):
+        for kw in (1, 2, 4, 8):
+            p = _native.plan_gemv(m, n, k, rpw, kw)
+            print(f"gemv plan M={m} rows_per_wave={rpw} k_waves={kw} split={p.split_k}", flush=True)
             y = _run(gpu, x, qw, qz, s, plan_obj=p)
-            _assert_close(y, y_ref, f"M={m} rpw={rpw} kw={kw}")
+            _assert_close(y, y_ref, f"gemv M={m} rpw={rpw} kw={kw}")
+
+
+def test_split_k_counters_left_zero(gpu):
+    """The in-kernel split-K reduction resets its arrival counters, so the
+    shared workspace is ready for the next call (and for graph replays)."""
+    from kernels import awq_gemm as G
+    k, n = 3584, 4608
+    x, qw, qz, s = O.make_inputs(1, k, n, seed=6)
+    p = _native.plan_for(1, n, k)
+    assert p.split_k > 1
+    y = _run(gpu, x, qw, qz, s)
+    ws = G._workspaces[gpu.index][-1]
+    cnt = ws[: _native.counter_bytes() // 4].view(torch.int32)
+    assert int(cnt.abs().sum().item()) == 0
+    y2 = _run(gpu, x, qw, qz, s)
+    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
 
 
 def test_deterministic(gpu):
