@@ -41,7 +41,7 @@ typedef enum awq_w4a16_status {
     AWQ_ERR_WORKSPACE = -5,      /* workspace NULL or smaller than required            */
     AWQ_ERR_LAUNCH = -6,         /* the HIP runtime rejected a kernel launch           */
     AWQ_ERR_PATH = -7,           /* unknown kernel path, or path cannot serve this M   */
-    AWQ_ERR_TOO_LARGE = -8       /* M, K > 2^30, N > 2^20 or an operand > 2^31-1 bytes */
+    AWQ_ERR_TOO_LARGE = -8       /* M > 2^30, K > 2^22, N > 2^20 or operand > 2^31-1 B */
 } awq_w4a16_status;
 
 /* Kernel paths.  AUTO lets the shape dispatcher choose (the reference's own
@@ -94,6 +94,14 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size,
 int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
                           int32_t rows_per_wave, int32_t k_waves, int32_t variant,
                           int32_t factored_scale, awq_w4a16_plan* plan);
+
+/* Host-only: a tile-path plan (variant 1: 128x128x32 tiles; variant 2:
+ * 128x128x64 tiles with prefetch; variant 3: 256x128x64 tiles, x streamed
+ * into a 3-stage LDS ring by direct loads; variants 2 and 3 take split_k >= 1
+ * workgroups along K).  For variants 2 and 3 the plan's rows_per_wave holds
+ * the K rows per split. */
+int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                        int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 
 /* Host-only: a GEMV-path plan (M <= 2) with explicit tuning values
  * (rows_per_wave: 16, 32 or 64; k_waves: 1, 2, 4 or 8). */

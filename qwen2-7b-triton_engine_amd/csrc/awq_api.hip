@@ -23,6 +23,9 @@ constexpr uint64_t kSkinnyLdsBudget = 64 * 1024;
 constexpr int64_t kCUs = 256;
 
 constexpr int64_t kIndexLimit = (int64_t)1 << 30;
+// K bound that keeps every 32-bit buffer offset in range, including the rows
+// past M that a 256-row tile reads as zeros: (M + 256) * K * 2 < 2^32.
+constexpr int64_t kMaxK = (int64_t)1 << 22;
 // Byte-size limit of any one operand (buffer descriptors carry 32-bit sizes).
 constexpr int64_t kBytesLimit = ((int64_t)1 << 31) - 1;
 
@@ -31,7 +34,7 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 int check_dims(int64_t M, int64_t N, int64_t K, int32_t G) {
     if (G != kGroup) return AWQ_ERR_GROUP_SIZE;
     if (M < 0 || N <= 0 || K <= 0 || N % 8 != 0 || K % G != 0) return AWQ_ERR_BAD_DIMS;
-    if (M > kIndexLimit || N > kMaxN || K > kIndexLimit) return AWQ_ERR_TOO_LARGE;
+    if (M > kIndexLimit || N > kMaxN || K > kMaxK) return AWQ_ERR_TOO_LARGE;
     if (K * (N / 2) > kBytesLimit || M * K * 2 > kBytesLimit || M * N * 2 > kBytesLimit)
         return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
@@ -128,21 +131,61 @@ int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_gemv(M, N, K, 64, 8, p);
 }
 
-int tile_plan(int64_t M, int64_t N, int64_t /*K*/, awq_w4a16_plan* p) {
+int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k, awq_w4a16_plan* p) {
     p->path = AWQ_PATH_TILE;
-    p->variant = 1;
+    p->variant = (int32_t)variant;
     p->tile_m = 128;
     p->tile_n = 128;
     p->rows_per_wave = 0;
     p->k_waves = 1;
-    p->split_k = 1;
     p->block_threads = 256;
     p->factored_scale = 0;
     p->reserved = 0;
-    p->grid = ((M + 127) / 128) * ((N + 127) / 128);
-    p->workspace_bytes = 0;
     p->lds_bytes = 0;
+    if (variant == 3) {
+        p->tile_m = 256;
+        p->block_threads = 512;
+    }
+    const int64_t tiles = tile_tiles((int)M, (int)N, (int)variant);
+    if (variant == 1) {
+        if (split_k != 1) return AWQ_ERR_PATH;
+        p->split_k = 1;
+        p->grid = tiles;
+        p->workspace_bytes = 0;
+        return AWQ_OK;
+    }
+    if ((variant != 2 && variant != 3) || split_k < 1) return AWQ_ERR_PATH;
+    // K range per split: a multiple of the 64-row k-step.
+    const int64_t steps = K / 64;
+    const int64_t per = (steps + split_k - 1) / split_k;
+    const int64_t s = (steps + per - 1) / per;
+    if (s != split_k) return AWQ_ERR_PATH;
+    if (split_k > 1 && tiles * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
+    p->split_k = (int32_t)split_k;
+    p->rows_per_wave = (int32_t)(per * 64);  // K rows per split
+    p->grid = tiles * split_k;
+    p->workspace_bytes =
+        split_k > 1 ? skinny_counter_bytes() + (uint64_t)split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
+}
+
+// Variant 3 (its LDS allows one workgroup per CU); split-K only when the tile
+// grid leaves CUs idle: as many splits as fit in one pass over the CUs, at
+// least 8 k-steps per split.
+int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    const int64_t tiles = tile_tiles((int)M, (int)N, 3);
+    int64_t split = 1;
+    if (tiles < kCUs && tiles * 4 <= (int64_t)kCounterBytes) {
+        split = kCUs / tiles;
+        const int64_t max_split = (K / 64) / 8;
+        if (split > max_split) split = max_split;
+        if (split < 1) split = 1;
+        const int64_t steps = K / 64;
+        const int64_t per = (steps + split - 1) / split;
+        split = (steps + per - 1) / per;
+    }
+    return fill_tile(M, N, K, 3, split, p);
 }
 
 // Checks a caller-supplied plan against the shape: it must be exactly what
@@ -153,8 +196,8 @@ int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
         const int st = fill_skinny(M, N, K, p->rows_per_wave, p->k_waves, p->variant, p->factored_scale, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_TILE) {
-        tile_plan(M, N, K, &q);
-        if (p->variant != q.variant) return AWQ_ERR_PATH;
+        const int st = fill_tile(M, N, K, p->variant, p->split_k, &q);
+        if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_GEMV) {
         const int st = fill_gemv(M, N, K, p->rows_per_wave, p->k_waves, &q);
         if (st != AWQ_OK) return st;
@@ -220,7 +263,12 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         cfg.variant = p.variant;
         cfg.tile_m = p.tile_m;
         cfg.tile_n = p.tile_n;
-        e = launch_tile(a, cfg, s);
+        cfg.split_k = p.split_k;
+        cfg.k_per_split = p.rows_per_wave;
+        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                              skinny_counter_bytes())
+                                   : nullptr;
+        e = launch_tile(a, cfg, static_cast<uint32_t*>(workspace), s);
     }
     return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
 }
@@ -241,7 +289,7 @@ const char* awq_w4a16_error_string(int status) {
         case AWQ_ERR_WORKSPACE: return "workspace missing or too small";
         case AWQ_ERR_LAUNCH: return "HIP kernel launch failed";
         case AWQ_ERR_PATH: return "kernel path or plan cannot serve this shape";
-        case AWQ_ERR_TOO_LARGE: return "M or K exceeds 2^30, N exceeds 2^20, or an operand exceeds 2^31-1 bytes";
+        case AWQ_ERR_TOO_LARGE: return "M exceeds 2^30, K exceeds 2^22, N exceeds 2^20, or an operand exceeds 2^31-1 bytes";
         default: return "unknown status";
     }
 }
@@ -255,6 +303,14 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size, i
 }
 
 size_t awq_w4a16_counter_bytes(void) { return skinny_counter_bytes(); }
+
+int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant, int32_t split_k,
+                        awq_w4a16_plan* plan) {
+    if (!plan) return AWQ_ERR_NULL_POINTER;
+    const int d = check_dims(M, N, K, group_size);
+    if (d != AWQ_OK) return d;
+    return fill_tile(M, N, K, variant, split_k, plan);
+}
 
 int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
                         int32_t k_waves, awq_w4a16_plan* plan) {

@@ -147,4 +147,80 @@ __device__ __forceinline__ floatx4 buf_load_f4_device(__amdgpu_buffer_rsrc_t r, 
 // memory operation of this wave, stores included, has completed.
 __device__ __forceinline__ void wait_vm_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Last-arriving workgroup of a split-K output range: for rows row0 ..
+// row0+nrows and columns col0 .. col0+ncols,
+// out[m, n] = fp16(sum over split of partials[split, m, n]) (partials of
+// shape [split, M, N]).  Every thread of the workgroup takes part and the
+// loads of many outputs are in flight together:
+//  * few outputs (fewer quads than threads): each output quad gets P threads
+//    that add the splits part, part+P, ... (8 loads at a time), combined
+//    through LDS in a fixed order;
+//  * many outputs: each thread keeps up to U quads in registers and adds
+//    split after split, U loads in flight per split (U is a template
+//    parameter so that callers that never have many outputs keep their
+//    register footprint).
+// Either way each element is summed in a fixed order, independent of timing.
+// `fin` holds blockDim.x float4.  Must be called by the whole workgroup.
+template <int U>
+__device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t* __restrict__ out, int M, int N,
+                                              int row0, int nrows, int col0, int ncols, int split_k,
+                                              floatx4* fin) {
+    const int quads = ncols / 4;
+    const int items = nrows * quads;
+    const int nt = blockDim.x;
+    const int t = threadIdx.x;
+    const uint32_t stride = (uint32_t)((size_t)M * N * 4);
+    auto item_off = [&](int item, int& m, int& n) {
+        const int r = item / quads;
+        m = row0 + r;
+        n = col0 + 4 * (item - r * quads);
+        return (uint32_t)(((size_t)m * N + n) * 4);
+    };
+    auto store = [&](int m, int n, floatx4 s) {
+        const half4_t h = {(half_t)s[0], (half_t)s[1], (half_t)s[2], (half_t)s[3]};
+        *reinterpret_cast<half4_t*>(out + (size_t)m * N + n) = h;
+    };
+    if (items < nt) {
+        const int P = min(8, nt / items);
+        const int part = t / items;
+        const int item = t - part * items;
+        const bool valid = part < P;
+        floatx4 s = {0.f, 0.f, 0.f, 0.f};
+        int m = 0, n = 0;
+        if (valid) {
+            const uint32_t off = item_off(item, m, n);
+#pragma unroll 8
+            for (int q = part; q < split_k; q += P) s += buf_load_f4_device(rp, off + (uint32_t)q * stride);
+        }
+        if (P > 1) {
+            if (valid) fin[t] = s;
+            __syncthreads();
+            if (valid && part == 0) {
+                for (int p = 1; p < P; ++p) s += fin[p * items + item];
+            }
+        }
+        if (valid && part == 0) store(m, n, s);
+        return;
+    }
+    for (int base = 0; base < items; base += U * nt) {
+        floatx4 s[U];
+        uint32_t off[U];
+        int mm[U], nn[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int item = base + u * nt + t;
+            s[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+            off[u] = item < items ? item_off(item, mm[u], nn[u]) : 0u;
+        }
+        for (int q = 0; q < split_k; ++q) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (base + u * nt + t < items) s[u] += buf_load_f4_device(rp, off[u] + (uint32_t)q * stride);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (base + u * nt + t < items) store(mm[u], nn[u], s[u]);
+    }
+}
+
 }  // namespace awq

@@ -33,6 +33,7 @@ __global__ __launch_bounds__(512) void awq_gemv_kernel(GemmArgs a, int kw_count,
                                                        uint32_t* counters) {
     __shared__ float red[7 * MR * 8 * 64];
     __shared__ int last_flag;
+    __shared__ floatx4 fin[512];
     const int lane = threadIdx.x & 63;
     const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pn = a.N >> 3;
@@ -141,18 +142,7 @@ __global__ __launch_bounds__(512) void awq_gemv_kernel(GemmArgs a, int kw_count,
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    const int col0 = strip * 512;
-    const int quads = min(512, a.N - col0) / 4;
-    const uint32_t stride = (uint32_t)((size_t)a.M * a.N * 4);
-    for (int idx = threadIdx.x; idx < a.M * quads; idx += blockDim.x) {
-        const int m = idx / quads;
-        const int n = col0 + 4 * (idx - m * quads);
-        const uint32_t off = (uint32_t)(((size_t)m * a.N + n) * 4);
-        floatx4 s = buf_load_f4_device(rp, off);
-        for (int q = 1; q < split_k; ++q) s += buf_load_f4_device(rp, off + q * stride);
-        const half4_t h = {(half_t)s[0], (half_t)s[1], (half_t)s[2], (half_t)s[3]};
-        *reinterpret_cast<half4_t*>(a.out + (size_t)m * a.N + n) = h;
-    }
+    splitk_finish<2>(rp, a.out, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
     if (threadIdx.x == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

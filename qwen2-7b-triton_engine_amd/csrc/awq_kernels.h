@@ -35,8 +35,10 @@ struct GemvConfig {
 };
 
 struct TileConfig {
-    int variant;             // tile kernel variant
+    int variant;             // 1: 128x128x32; 2: 128x128x64, prefetch, XCD order, split-K; 3: 256x128x64, x ring in LDS
     int tile_m, tile_n;
+    int split_k;             // variant 2: workgroups along K per tile
+    int k_per_split;         // variant 2: K rows per split (multiple of 64)
 };
 
 hipError_t launch_dequant(const uint32_t* qweight, const uint32_t* qzeros, const half_t* scales,
@@ -55,7 +57,10 @@ hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* count
 int64_t gemv_strips(int N);
 int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
 
-hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, hipStream_t stream);
+// Variant 2 with split_k > 1 uses the same workspace contract as launch_skinny
+// (counters: one per tile).
+hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream);
+int64_t tile_tiles(int M, int N, int variant);
 
 // Output columns per skinny wave.
 constexpr int kSkinnyCols = 128;

@@ -17,6 +17,8 @@
 // Two LDS buffers: the global loads for k-step t+1 are issued before the
 // MFMAs of step t and written to the other buffer after them; one barrier per
 // k-step.
+#include <type_traits>
+
 #include "awq_kernels.h"
 
 namespace awq {
@@ -157,14 +159,510 @@ __global__ __launch_bounds__(256) void awq_tile_kernel_v1(GemmArgs a) {
     }
 }
 
-hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, hipStream_t stream) {
-    if (cfg.variant != 1) return hipErrorInvalidValue;
-    const int64_t m_tiles = (a.M + BM - 1) / BM;
-    const int64_t n_tiles = (a.N + BN - 1) / BN;
-    const int64_t blocks = m_tiles * n_tiles;
-    if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(awq_tile_kernel_v1, dim3((unsigned)blocks), dim3(256), 0, stream, a);
-    return hipGetLastError();
+// ---------------------------------------------------------------------------
+// Variant 2: 128 x 128 x 64 tiles, register prefetch one k-step ahead,
+// XCD-aware tile order, optional split-K.
+//
+// * LDS rows are k-contiguous with a 144-byte pitch, which keeps the 16-byte
+//   fragment reads of 8 consecutive rows on distinct banks.
+// * Each thread dequantises 4 rows x 1 packed column per k-step (two k-pairs
+//   per logical column) and writes each column's 4 fp16 values as one 8-byte
+//   LDS store; 16 consecutive lanes cover 16 row quads, 128 contiguous bytes.
+// * Work order: workgroup b runs on XCD b % 8 (round-robin dispatch); the
+//   workgroups of one XCD take a contiguous range of the grouped-M tile order
+//   (8 M tiles per group), so concurrent workgroups of an XCD share x rows and
+//   weight columns in that XCD's L2.  Any other dispatch order only costs
+//   locality: the mapping is a bijection either way.
+// * split_k > 1 (small tile grids): each workgroup covers a K range and
+//   finishes like the decode kernels (device-scope partials, arrival counter,
+//   deterministic finish by the last workgroup of the tile).
+namespace {
+constexpr int T2_BM = 128;
+constexpr int T2_BN = 128;
+constexpr int T2_BK = 64;
+constexpr int T2_PITCH = T2_BK + 8;  // halves
+constexpr int T2_GM = 8;             // M tiles per group of the tile order
+}  // namespace
+
+__global__ __launch_bounds__(256, 2) void awq_tile_kernel_v2(GemmArgs a, int split_k, int k_per_split,
+                                                             uint32_t* counters) {
+    __shared__ __attribute__((aligned(16))) half_t As[2][T2_BM * T2_PITCH];
+    __shared__ __attribute__((aligned(16))) half_t Bs[2][T2_BN * T2_PITCH];
+    __shared__ floatx4 fin[256];
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave & 1;
+    const int wn = wave >> 1;
+    const int c16 = lane & 15;
+    const int kq = lane >> 4;
+
+    // ---- work item of this workgroup ----
+    const int m_tiles = (a.M + T2_BM - 1) / T2_BM;
+    const int n_tiles = (a.N + T2_BN - 1) / T2_BN;
+    const int total = (int)gridDim.x;  // m_tiles * n_tiles * split_k
+    const int xcd = blockIdx.x & 7;
+    const int xi = blockIdx.x >> 3;
+    const int per = (total + 7) >> 3;
+    const int rem = total & 7;
+    const int w = (rem == 0 || xcd < rem) ? xcd * per + xi : rem * per + (xcd - rem) * (per - 1) + xi;
+    const int tile = w / split_k;
+    const int split = w - tile * split_k;
+    const int in_group = T2_GM * n_tiles;
+    const int first_m = (tile / in_group) * T2_GM;
+    const int gm = min(m_tiles - first_m, T2_GM);
+    const int tm = first_m + (tile % in_group) % gm;
+    const int tn = (tile % in_group) / gm;
+    const int m0 = tm * T2_BM;
+    const int n0 = tn * T2_BN;
+    const int pn = a.N >> 3;
+    const int k_begin = split * k_per_split;
+    const int k_end = min(a.K, k_begin + k_per_split);
+    const int KT = (k_end - k_begin) / T2_BK;
+
+    // ---- loaders ----
+    int xrow[4], xkc[4];
+    bool xok[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int q = tid + 256 * r;
+        xrow[r] = q >> 3;
+        xkc[r] = q & 7;
+        xok[r] = m0 + xrow[r] < a.M;
+    }
+    const int rq = tid & 15;       // row quad: rows 4*rq .. 4*rq+3 of the k-step
+    const int jj = tid >> 4;       // packed column of the tile
+    const int jg = (n0 >> 3) + jj;
+    const bool wok = jg < pn;
+    const int jgc = wok ? jg : pn - 1;
+
+    half8_t xr[4];
+    uint32_t wr[4];
+    uint32_t zs[8], ss[8];
+
+    auto load_global = [&](int kt) {
+        const int kb = k_begin + kt * T2_BK;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (xok[r])
+                xr[r] = *reinterpret_cast<const half8_t*>(a.x + (size_t)(m0 + xrow[r]) * a.K + kb + 8 * xkc[r]);
+            else
+                xr[r] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        const uint32_t* wp = a.qweight + (size_t)(kb + 4 * rq) * pn + jgc;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wr[i] = wp[(size_t)i * pn];
+    };
+    auto load_group = [&](int kt) {
+        const int g = (k_begin + kt * T2_BK) / kGroup;
+        const uint32_t zw = a.qzeros[(size_t)g * pn + jgc];
+        const half8_t s8 = *reinterpret_cast<const half8_t*>(a.scales + (size_t)g * a.N + 8 * jgc);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            zs[c] = zero_splat(zw, c);
+            ss[c] = as_u32(half2_t{s8[c], s8[c]});
+        }
+    };
+    auto store_lds = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<half8_t*>(&As[buf][xrow[r] * T2_PITCH + 8 * xkc[r]]) = xr[r];
+        uint32_t k01[8], k23[8];
+        kpairs_magic(wr[0], wr[1], k01);
+        kpairs_magic(wr[2], wr[3], k23);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const half2_t lo = (as_h2(k01[c]) - as_h2(zs[c])) * as_h2(ss[c]);
+            const half2_t hi = (as_h2(k23[c]) - as_h2(zs[c])) * as_h2(ss[c]);
+            const u32x2 v = wok ? u32x2{as_u32(lo), as_u32(hi)} : u32x2{0u, 0u};
+            *reinterpret_cast<u32x2*>(&Bs[buf][(8 * jj + c) * T2_PITCH + 4 * rq]) = v;
+        }
+    };
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    if (KT > 0) {
+        load_group(0);
+        load_global(0);
+        store_lds(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int buf = kt & 1;
+        const bool has_next = kt + 1 < KT;
+        if (has_next) load_global(kt + 1);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            half8_t af[4], bfr[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+                af[x] = *reinterpret_cast<const half8_t*>(
+                    &Bs[buf][(64 * wn + 16 * x + c16) * T2_PITCH + 32 * s2 + 8 * kq]);
+#pragma unroll
+            for (int y = 0; y < 4; ++y)
+                bfr[y] = *reinterpret_cast<const half8_t*>(
+                    &As[buf][(64 * wm + 16 * y + c16) * T2_PITCH + 32 * s2 + 8 * kq]);
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+#pragma unroll
+                for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+        }
+        if (has_next) {
+            if ((k_begin + (kt + 1) * T2_BK) % kGroup == 0) load_group(kt + 1);
+            store_lds(buf ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // acc[x][y] lane value v: out^T[n = 16x + 4kq + v][m = 16y + c16] of this wave's 64 x 64.
+    if (split_k == 1) {
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            const int gm_ = m0 + 64 * wm + 16 * y + c16;
+            if (gm_ >= a.M) continue;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
+                if (gn >= a.N) continue;
+                const half4_t h = {(half_t)acc[x][y][0], (half_t)acc[x][y][1], (half_t)acc[x][y][2],
+                                   (half_t)acc[x][y][3]};
+                *reinterpret_cast<half4_t*>(a.out + (size_t)gm_ * a.N + gn) = h;
+            }
+        }
+        return;
+    }
+
+    const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, part_bytes);
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+        const int gm_ = m0 + 64 * wm + 16 * y + c16;
+        if (gm_ >= a.M) continue;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
+            if (gn >= a.N) continue;
+            buf_store_f4_device(acc[x][y], rp, (uint32_t)((((size_t)split * a.M + gm_) * a.N + gn) * 4));
+        }
+    }
+    wait_vm_stores();
+    __syncthreads();
+    if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)(split_k - 1);
+    __syncthreads();
+    if (!last_flag) return;
+    splitk_finish<16>(rp, a.out, a.M, a.N, m0, min(T2_BM, a.M - m0), n0, min(T2_BN, a.N - n0), split_k, fin);
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Variant 3: 256 x 128 x 64 tiles, 512 threads (8 waves of 64 x 64), every
+// operand streamed into LDS rings by direct global->LDS loads.
+//
+// buffer_load_dword[x4] ... lds writes each lane's 4 (16) bytes to
+// M0 + 4*lane (16*lane): a wave writes one contiguous LDS block per
+// instruction, and each lane chooses which global element lands in its slot.
+//   * x: 3-stage ring, rows of 128 B XOR-swizzled (16-byte chunk p of row r
+//     holds k-chunk p ^ (r & 7)), so the MFMA fragment reads of 8 consecutive
+//     rows hit 8 distinct chunk positions (all banks once).  Rows beyond M
+//     read as zeros (buffer out-of-range).
+//   * raw int4 words: 4-stage ring.  Block b (68 words, 4 of them padding)
+//     holds rows 4b .. 4b+3 of the 16 packed columns, word 4*jj + (r & 3):
+//     each load instruction reads 4 row segments of 64 bytes, and the thread
+//     that dequantises rows (2p, 2p+1) of packed column jj reads one 8-byte
+//     word pair; the padding spreads a wave's reads over all banks.
+//   * zero words and scales of the k-step's group: 4-stage ring; wave 0
+//     loads the zero words, every other wave the same 64 scale words (one
+//     load per wave keeps the per-wave load count uniform).
+// The dequantised weight (the reference's exact fp16 (q - z) * s) is written
+// to one of two W^T buffers one k-step ahead of its MFMAs.
+//
+// The loads are issued from inline assembly, 7 per wave per k-step (loads
+// past the last k-step re-read it, into free slots).  The compiler, which
+// cannot tell which LDS bytes a direct load writes, would otherwise wait for
+// every outstanding load before each LDS read; the kernel waits itself: the
+// barrier that ends k-step t is preceded by s_waitcnt vmcnt(7), so every load
+// issued up to k-step t-1 has landed.  Distances: x for step t+2 and raw
+// weights for step t+3 are issued in step t; step t+1's raw weights, issued
+// in step t-2, are dequantised in step t; step t+2's x is read in step t+2.
+namespace {
+constexpr int T3_BM = 256;
+constexpr int T3_BN = 128;
+constexpr int T3_BK = 64;
+constexpr int T3_XS = 3;              // x stages
+constexpr int T3_RS = 4;              // raw weight / zero+scale stages
+constexpr int T3_WPITCH = T3_BK + 8;  // halves per W^T row (144 B)
+constexpr int T3_GM = 4;              // M tiles per group of the tile order
+constexpr int T3_RAW_BLOCK = 68;                  // words per 4-row block (64 + padding)
+constexpr int T3_RAW_WORDS = 16 * T3_RAW_BLOCK;   // 64 rows x 16 packed columns
+constexpr int T3_ZS_WORDS = 128;      // 64 zero-word slots (16 used) + 64 scale words
+// s_waitcnt vmcnt(7), expcnt/lgkmcnt at their maxima (gfx9 encoding).
+constexpr int kWaitVm7 = 0x0F77;
+
+__device__ __forceinline__ void buffer_load_lds_x4(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %0, %1, %2 offen lds"
+        :
+        : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_base)
+        : "memory", "m0");
+}
+__device__ __forceinline__ void buffer_load_lds_x1(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %0, %1, %2 offen lds"
+        :
+        : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_base)
+        : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p);
+}
+
+__device__ __forceinline__ u32x4 raw_rsrc(const void* base, uint32_t num_bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, num_bytes, 0x00020000u};
+}
+}  // namespace
+
+__global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int split_k, int k_per_split,
+                                                             uint32_t* counters) {
+    __shared__ __attribute__((aligned(16))) half_t Xs[T3_XS][T3_BM * T3_BK];
+    __shared__ __attribute__((aligned(16))) half_t Ws[2][T3_BN * T3_WPITCH];
+    __shared__ __attribute__((aligned(16))) uint32_t Wr[T3_RS][T3_RAW_WORDS];
+    __shared__ __attribute__((aligned(16))) uint32_t Zs[T3_RS][T3_ZS_WORDS];
+    __shared__ int last_flag;
+    floatx4* fin = reinterpret_cast<floatx4*>(&Xs[0][0]);  // split-K finish, after the main loop
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 3;
+    const int wn = wave >> 2;
+    const int c16 = lane & 15;
+    const int kq = lane >> 4;
+
+    // ---- work item (same XCD-aware grouped order as variant 2) ----
+    const int m_tiles = (a.M + T3_BM - 1) / T3_BM;
+    const int n_tiles = (a.N + T3_BN - 1) / T3_BN;
+    const int total = (int)gridDim.x;
+    const int xcd = blockIdx.x & 7;
+    const int xi = blockIdx.x >> 3;
+    const int per = (total + 7) >> 3;
+    const int rem = total & 7;
+    const int w = (rem == 0 || xcd < rem) ? xcd * per + xi : rem * per + (xcd - rem) * (per - 1) + xi;
+    const int tile = w / split_k;
+    const int split = w - tile * split_k;
+    const int in_group = T3_GM * n_tiles;
+    const int first_m = (tile / in_group) * T3_GM;
+    const int gm = min(m_tiles - first_m, T3_GM);
+    const int tm = first_m + (tile % in_group) % gm;
+    const int tn = (tile % in_group) / gm;
+    const int m0 = tm * T3_BM;
+    const int n0 = tn * T3_BN;
+    const int pn = a.N >> 3;
+    const int j0 = n0 >> 3;
+    const int k_begin = split * k_per_split;
+    const int k_end = min(a.K, k_begin + k_per_split);
+    const int KT = (k_end - k_begin) / T3_BK;
+
+    // ---- per-lane source offsets of the direct loads ----
+    const u32x4 rx = raw_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
+    const u32x4 rw = raw_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
+    const u32x4 rz = raw_rsrc(a.qzeros, (uint32_t)((size_t)(a.K / kGroup) * pn * 4));
+    const u32x4 rs = raw_rsrc(a.scales, (uint32_t)((size_t)(a.K / kGroup) * a.N * 2));
+    // x: instruction i of wave w fills rows 8*(8i+w) .. +7 of the stage.
+    const int xr_in_blk = lane >> 3;
+    const int xkc = (lane & 7) ^ xr_in_blk;
+    uint32_t x_voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * (i * 8 + wave) + xr_in_blk;
+        x_voff[i] = (uint32_t)(((size_t)(m0 + r) * a.K + 8 * xkc) * 2);
+    }
+    // raw weights: instruction i of wave w fills block b = 2w + i; lane l reads
+    // qweight[kb + 4b + (l & 3)][j0 + (l >> 2)] (columns past the last clamp to it).
+    const uint32_t w_voff = (uint32_t)(((lane & 3) * pn + min(j0 + (lane >> 2), pn - 1)) * 4);
+    // zero words (wave 0, lane l: packed column j0 + l, clamped) and scales
+    // (other waves, lane l: columns n0 + 2l, n0 + 2l + 1; past N they read the
+    // next group's bytes or zeros, and are never used).
+    const bool zs_is_zero = wave == 0;  // wave-uniform
+    const uint32_t zs_voff =
+        zs_is_zero ? (uint32_t)(min(j0 + lane, pn - 1) * 4) : (uint32_t)((n0 + 2 * lane) * 2);
+
+    auto issue_x = [&](int kt, int xstage) {
+        const int kb = k_begin + kt * T3_BK;
+        const uint32_t xs_off = __builtin_amdgcn_readfirstlane((uint32_t)kb * 2u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            buffer_load_lds_x4(rx, x_voff[i], xs_off, lds_addr(&Xs[xstage][(i * 8 + wave) * 512]));
+    };
+    auto issue_raw = [&](int kt, int rstage) {
+        const int kb = k_begin + kt * T3_BK;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int b = 2 * wave + i;
+            buffer_load_lds_x1(rw, w_voff, __builtin_amdgcn_readfirstlane((uint32_t)(kb + 4 * b) * (uint32_t)pn * 4u),
+                               lds_addr(&Wr[rstage][b * T3_RAW_BLOCK]));
+        }
+        const int g = kb / kGroup;
+        if (zs_is_zero)
+            buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
+                               lds_addr(&Zs[rstage][0]));
+        else  // identical bytes from every wave
+            buffer_load_lds_x1(rs, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
+                               lds_addr(&Zs[rstage][64]));
+    };
+
+    // ---- dequant: thread = (packed column jj, row pair rp) ----
+    const int jj = tid >> 5;
+    const int rp = tid & 31;
+    const bool wok = j0 + jj < pn;
+    auto dequant = [&](int rstage, int wbuf) {
+        const u32x2 wpair =
+            *reinterpret_cast<const u32x2*>(&Wr[rstage][(rp >> 1) * T3_RAW_BLOCK + 4 * jj + 2 * (rp & 1)]);
+        const uint32_t zw = Zs[rstage][jj];
+        const half8_t s8 = *reinterpret_cast<const half8_t*>(&Zs[rstage][64 + 4 * jj]);
+        uint32_t kp[8];
+        kpairs_magic(wpair[0], wpair[1], kp);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const half2_t v = (as_h2(kp[c]) - as_h2(zero_splat(zw, c))) * half2_t{s8[c], s8[c]};
+            *reinterpret_cast<uint32_t*>(&Ws[wbuf][(8 * jj + c) * T3_WPITCH + 2 * rp]) = wok ? as_u32(v) : 0u;
+        }
+    };
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    if (KT > 0) {
+        const int last = KT - 1;
+        // Prologue: x for steps 0, 1; raw weights for steps 0, 1, 2.
+        issue_x(0, 0);
+        issue_x(min(1, last), 1);
+        issue_raw(0, 0);
+        issue_raw(min(1, last), 1);
+        issue_raw(min(2, last), 2);
+        wait_vm_stores();
+        __syncthreads();
+        dequant(0, 0);
+        __syncthreads();
+        for (int kt = 0; kt < KT; ++kt) {
+            // Both rings' target stages were last read before the previous barrier.
+            issue_x(min(kt + 2, last), (kt + 2) % T3_XS);
+            issue_raw(min(kt + 3, last), (kt + 3) % T3_RS);
+            const half_t* xs = Xs[kt % T3_XS];
+            const half_t* wsb = Ws[kt & 1];
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                half8_t af[4], bfr[4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    af[x] = *reinterpret_cast<const half8_t*>(
+                        &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
+#pragma unroll
+                for (int y = 0; y < 4; ++y) {
+                    const int r = 64 * wm + 16 * y + c16;
+                    const int phys = (4 * s2 + kq) ^ (r & 7);
+                    bfr[y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
+                }
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+#pragma unroll
+                    for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+            }
+            if (kt + 1 < KT) dequant((kt + 1) % T3_RS, (kt + 1) & 1);
+            __builtin_amdgcn_s_waitcnt(kWaitVm7);
+            __syncthreads();
+        }
+        wait_vm_stores();  // drain the re-read tail loads before the LDS is reused
+        __syncthreads();
+    }
+
+    // acc[x][y] lane value v: out^T[n = 16x + 4kq + v][m = 16y + c16] of this wave's 64 x 64.
+    if (split_k == 1) {
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            const int gm_ = m0 + 64 * wm + 16 * y + c16;
+            if (gm_ >= a.M) continue;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
+                if (gn >= a.N) continue;
+                const half4_t h = {(half_t)acc[x][y][0], (half_t)acc[x][y][1], (half_t)acc[x][y][2],
+                                   (half_t)acc[x][y][3]};
+                *reinterpret_cast<half4_t*>(a.out + (size_t)gm_ * a.N + gn) = h;
+            }
+        }
+        return;
+    }
+
+    const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
+    const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+        const int gm_ = m0 + 64 * wm + 16 * y + c16;
+        if (gm_ >= a.M) continue;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
+            if (gn >= a.N) continue;
+            buf_store_f4_device(acc[x][y], rp_, (uint32_t)((((size_t)split * a.M + gm_) * a.N + gn) * 4));
+        }
+    }
+    wait_vm_stores();
+    __syncthreads();
+    if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)(split_k - 1);
+    __syncthreads();
+    if (!last_flag) return;
+    splitk_finish<16>(rp_, a.out, a.M, a.N, m0, min(T3_BM, a.M - m0), n0, min(T3_BN, a.N - n0), split_k, fin);
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int64_t tile_tiles(int M, int N, int variant) {
+    if (variant == 3) return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
+    return (int64_t)((M + T2_BM - 1) / T2_BM) * ((N + T2_BN - 1) / T2_BN);
+}
+
+hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream) {
+    if (cfg.variant == 1) {
+        const int64_t m_tiles = (a.M + BM - 1) / BM;
+        const int64_t n_tiles = (a.N + BN - 1) / BN;
+        const int64_t blocks = m_tiles * n_tiles;
+        if (blocks == 0) return hipSuccess;
+        hipLaunchKernelGGL(awq_tile_kernel_v1, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
+    if (cfg.variant == 2) {
+        const int64_t blocks = tile_tiles(a.M, a.N, 2) * cfg.split_k;
+        if (blocks == 0) return hipSuccess;
+        hipLaunchKernelGGL(awq_tile_kernel_v2, dim3((unsigned)blocks), dim3(256), 0, stream, a, cfg.split_k,
+                           cfg.k_per_split, counters);
+        return hipGetLastError();
+    }
+    if (cfg.variant == 3) {
+        const int64_t blocks = tile_tiles(a.M, a.N, 3) * cfg.split_k;
+        if (blocks == 0) return hipSuccess;
+        hipLaunchKernelGGL(awq_tile_kernel_v3, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
+                           cfg.k_per_split, counters);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace awq

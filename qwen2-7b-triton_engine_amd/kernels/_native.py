@@ -67,6 +67,7 @@ SIGNATURES = {
                                              ctypes.POINTER(Plan)]),
     "awq_w4a16_counter_bytes": (ctypes.c_size_t, []),
     "awq_w4a16_plan_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_tile": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
     "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
     "awq_w4a16_validate": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
@@ -138,6 +139,12 @@ def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, group_si
     p = Plan()
     check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, rows_per_wave, k_waves, ctypes.byref(p)),
           "awq_w4a16_plan_gemv")
+    return p
+
+
+def plan_tile(M: int, N: int, K: int, variant: int = 2, split_k: int = 1, group_size: int = 128) -> Plan:
+    p = Plan()
+    check(lib().awq_w4a16_plan_tile(M, N, K, group_size, variant, split_k, ctypes.byref(p)), "awq_w4a16_plan_tile")
     return p
 
 

@@ -227,6 +227,22 @@ def test_gemv_plans_agree(gpu, m):
             _assert_close(y, y_ref, f"gemv M={m} rpw={rpw} kw={kw}")
 
 
+@pytest.mark.parametrize("m,k,n", [(65, 1024, 1032), (200, 3584, 520), (512, 2048, 264), (130, 18944, 128)])
+def test_tile_plans_agree(gpu, m, k, n):
+    """Both tile variants, and split-K counts from 1 up, give the same result."""
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=15)
+    y_ref = O.awq_gemm_oracle(x, qw, qz, s)
+    plans = [(1, 1)] + [(v, sk) for v in (2, 3) for sk in (1, 2, 3, 5, 8)]
+    for variant, sk in plans:
+        try:
+            p = _native.plan_tile(m, n, k, variant, sk)
+        except _native.AwqNativeError:
+            continue
+        print(f"tile plan M={m} K={k} N={n} variant={variant} split_k={sk}", flush=True)
+        y = _run(gpu, x, qw, qz, s, plan_obj=p)
+        _assert_close(y, y_ref, f"tile M={m} v={variant} split={sk}")
+
+
 def test_split_k_counters_left_zero(gpu):
     """The in-kernel split-K reduction resets its arrival counters, so the
     shared workspace is ready for the next call (and for graph replays)."""
