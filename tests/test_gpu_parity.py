@@ -336,3 +336,75 @@ def test_graph_capture_replay(gpu):
         torch.cuda.synchronize()
         for o, e in zip(outs, eager):
             assert torch.equal(o, e), f"replay {rep}"
+
+
+# --------------------------------------------------------------------------
+# Golden fixtures (tests/golden/make_golden.py: plain-Python values)
+# --------------------------------------------------------------------------
+
+def _golden(name):
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("name", ["awq_golden_small.npz", "awq_golden_edge.npz"])
+def test_golden_dequant_bit_exact(gpu, name):
+    print(f"golden dequant {name}", flush=True)
+    d = _golden(name)
+    qw, qz = d["qweight"], d["qzeros"]
+    s = d["scales_f16_bits"].view(np.float16)
+    k, n = qw.shape[0], s.shape[1]
+    out = torch.empty((k, n), dtype=torch.float16, device=gpu)
+    _dequant_to_fp16(_t(qw, gpu), _t(qz, gpu), _t(s, gpu), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), d["w_f16_bits"])
+
+
+def test_golden_small_gemm_every_path(gpu):
+    """The fixture's correctly rounded products, through every kernel path and
+    every row count the fixture's 5 rows allow."""
+    d = _golden("awq_golden_small.npz")
+    x = d["x_f16_bits"].view(np.float16)
+    qw, qz = d["qweight"], d["qzeros"]
+    s = d["scales_f16_bits"].view(np.float16)
+    for m in (1, 2, 5):
+        for path in _paths_for(m):
+            print(f"golden gemm M={m} path={_native.PATH_NAMES[path]}", flush=True)
+            y = _run(gpu, x[:m], qw, qz, s, path=path)
+            _assert_close(y, d["y_f64"][:m], f"golden M={m} path={path}")
+
+
+def test_golden_edge_gemm_finite_columns(gpu):
+    """Edge-case scales (subnormal, ties, negative, signed zeros) through every
+    path, element by element: |y - y_ref| <= 1.1 * 2^-10 * sum_k |x_k w_k|
+    + 2^-23, which covers the fp16 rounding of the output (2^-11 relative, and
+    the subnormal quantum 2^-24), the per-weight fp16 rounding that the GEMV
+    and factored skinny paths skip by scaling the fp32 group sum (2^-11
+    relative per term) and the fp32 accumulation (K * 2^-24 relative).
+    Outputs beyond the fp16 range must be infinities of the right sign.
+    Columns whose fp16 weights overflow to +-inf are left out: the reference's
+    output there is inf/NaN, while the paths that scale the group sum stay
+    finite."""
+    d = _golden("awq_golden_edge.npz")
+    x = d["x_f16_bits"].view(np.float16)
+    qw, qz = d["qweight"], d["qzeros"]
+    s = d["scales_f16_bits"].view(np.float16)
+    w = d["w_f16_bits"].view(np.float16).astype(np.float64)
+    keep = np.isfinite(w).all(axis=0)
+    assert 0 < keep.sum() < w.shape[1]
+    for m in (1, 2, 3):
+        y_ref = d["y_f64"][:m][:, keep]
+        mag = (np.abs(x[:m].astype(np.float64)) @ np.abs(w[:, keep]))
+        tol = 1.1 * 2.0 ** -10 * mag + 2.0 ** -23
+        big = np.abs(y_ref) > 65600.0
+        small = np.abs(y_ref) < 65400.0
+        for path in _paths_for(m):
+            print(f"golden edge gemm M={m} path={_native.PATH_NAMES[path]}", flush=True)
+            y = _run(gpu, x[:m], qw, qz, s, path=path)[:, keep].astype(np.float64)
+            assert np.all(np.isinf(y[big]) & (np.sign(y[big]) == np.sign(y_ref[big]))), f"M={m} path={path}"
+            err = np.abs(y[small] - y_ref[small])
+            assert np.all(err <= tol[small]), (
+                f"M={m} path={path}: worst excess {np.max(err - tol[small]):.3e}")

@@ -1,0 +1,268 @@
+"""Host-side tests that need no GPU: the C ABI library loads and exports what
+include/awq_w4a16.h declares, the shape dispatcher and plan validation, the
+argument checks of the C ABI and of the Python entry point (every call here
+fails validation, or has M = 0, before any device work), the roofline
+arithmetic and the bench's one-GPU contract."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from kernels import _native
+from kernels import awq_roofline as R
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "awq_w4a16.h")
+
+SHAPES = [(k, n) for _, k, n in R.QWEN2_7B_LINEARS + R.QWEN2_7B_FUSED]
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(_native.LIB_PATH):
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location(
+            "_awq_build", os.path.join(ROOT, "qwen2-7b-triton_engine_amd", "build.py"))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return _native.lib()
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(awq_w4a16_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(L):
+    declared = _declared_symbols()
+    assert len(declared) >= 10
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in include/awq_w4a16.h but not exported"
+    assert sorted(_native.SIGNATURES) == declared
+
+
+def test_abi_version_and_error_strings(L):
+    assert L.awq_w4a16_abi_version() == _native.ABI_VERSION
+    codes = [_native.AWQ_OK, _native.AWQ_ERR_NULL_POINTER, _native.AWQ_ERR_BAD_DIMS,
+             _native.AWQ_ERR_GROUP_SIZE, _native.AWQ_ERR_MISALIGNED, _native.AWQ_ERR_WORKSPACE,
+             _native.AWQ_ERR_LAUNCH, _native.AWQ_ERR_PATH, _native.AWQ_ERR_TOO_LARGE]
+    msgs = [_native.error_string(c) for c in codes]
+    assert len(set(msgs)) == len(msgs)
+    assert _native.error_string(-99) == "unknown status"
+
+
+def test_plan_struct_matches_header():
+    # 10 int32 fields, one int64, two uint64: 64 bytes, no padding.
+    assert ctypes.sizeof(_native.Plan) == 64
+    text = open(HEADER).read()
+    body = re.search(r"typedef struct awq_w4a16_plan\s*\{(.*?)\}\s*awq_w4a16_plan;", text, re.S).group(1)
+    fields = re.findall(r"\b(int32_t|int64_t|uint64_t)\s+(\w+);", body)
+    assert [f for _, f in fields] == [f for f, _ in _native.Plan._fields_]
+
+
+# ---------------------------------------------------------------------------
+# Shape dispatcher
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("k,n", SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 16, 17, 33, 64, 65, 128, 512, 2048, 2049])
+def test_auto_plan_invariants(L, m, k, n):
+    p = _native.plan_for(m, n, k)
+    if m <= 2:
+        assert p.path == _native.PATH_GEMV
+    elif m <= 64:
+        assert p.path == _native.PATH_SKINNY
+        assert p.tile_m >= m
+    else:
+        assert p.path == _native.PATH_TILE
+    assert p.grid > 0 and p.block_threads % 64 == 0 and p.block_threads <= 1024
+    if p.split_k > 1:
+        assert p.workspace_bytes == _native.counter_bytes() + p.split_k * m * n * 4
+    else:
+        assert p.workspace_bytes == 0
+    assert _native.workspace_bytes(m, n, k) == p.workspace_bytes
+
+
+@pytest.mark.parametrize("k,n", SHAPES)
+def test_tile_plans_cover_k_exactly(L, k, n):
+    """Every split-K plan gives each split a whole number of 64-row k-steps and
+    covers K exactly; the tile count fits the arrival-counter block."""
+    for variant in (2, 3):
+        for split in (1, 2, 3, 4, 5, 8):
+            try:
+                p = _native.plan_tile(512, n, k, variant, split)
+            except _native.AwqNativeError as e:
+                assert e.status == _native.AWQ_ERR_PATH
+                continue
+            per = p.rows_per_wave
+            assert per % 64 == 0
+            assert (split - 1) * per < k <= split * per
+            tm = 256 if variant == 3 else 128
+            tiles = -(-512 // tm) * -(-n // 128)
+            assert p.grid == tiles * split
+            if split > 1:
+                assert tiles * 4 <= _native.counter_bytes()
+
+
+def test_skinny_and_gemv_plan_rejections():
+    with pytest.raises(_native.AwqNativeError) as e:
+        _native.plan_gemv(3, 512, 3584, 64, 8)          # GEMV serves M <= 2
+    assert e.value.status == _native.AWQ_ERR_PATH
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_gemv(1, 512, 3584, 48, 8)          # rows per wave not an instance
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_skinny(65, 512, 3584, 256, 2)      # skinny serves M <= 64
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_skinny(8, 512, 3584, 256, 3)       # k_waves must be 1, 2 or 4
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_tile(512, 512, 3584, 1, 2)         # variant 1 has no split-K
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_tile(512, 512, 3584, 7, 1)
+
+
+def test_planned_call_rejects_altered_plan(L):
+    """gemm_planned re-derives the plan: a hand-edited field is refused before launch."""
+    m, n, k = 512, 3584, 3584
+    p = _native.plan_tile(m, n, k, 3, 1)
+    p.grid += 1
+    buf = np.zeros(1 << 12, dtype=np.uint8)
+    ptr = ctypes.c_void_p((buf.ctypes.data + 255) & ~255)
+    st = L.awq_w4a16_gemm_planned(ptr, ptr, ptr, ptr, ptr, m, n, k, 128, None, 0, ctypes.byref(p), None)
+    assert st == _native.AWQ_ERR_PATH
+
+
+# ---------------------------------------------------------------------------
+# Argument checks of the C ABI (all fail before any device work)
+# ---------------------------------------------------------------------------
+
+def _aligned_ptr(buf, align=256, offset=0):
+    return ctypes.c_void_p(((buf.ctypes.data + align - 1) & ~(align - 1)) + offset)
+
+
+def test_c_abi_argument_errors(L):
+    buf = np.zeros(1 << 16, dtype=np.uint8)
+    a = _aligned_ptr(buf)
+    mis = _aligned_ptr(buf, offset=2)
+    ws = _aligned_ptr(buf)
+
+    def gemm(x=a, qw=a, qz=a, s=a, out=a, M=4, N=512, K=3584, G=128, ws_=None, ws_bytes=0, path=0):
+        return L.awq_w4a16_gemm_ex(x, qw, qz, s, out, M, N, K, G, ws_, ws_bytes, path, None)
+
+    E = _native
+    assert gemm(qw=None) == E.AWQ_ERR_NULL_POINTER
+    assert gemm(x=None) == E.AWQ_ERR_NULL_POINTER
+    assert gemm(N=12) == E.AWQ_ERR_BAD_DIMS
+    assert gemm(K=200) == E.AWQ_ERR_BAD_DIMS
+    assert gemm(N=0) == E.AWQ_ERR_BAD_DIMS
+    assert gemm(M=-1) == E.AWQ_ERR_BAD_DIMS
+    assert gemm(G=64, K=3584) == E.AWQ_ERR_GROUP_SIZE
+    assert gemm(x=mis) == E.AWQ_ERR_MISALIGNED
+    assert gemm(s=mis) == E.AWQ_ERR_MISALIGNED
+    assert gemm(qw=ctypes.c_void_p(a.value + 2)) == E.AWQ_ERR_MISALIGNED
+    assert gemm(K=1 << 23) == E.AWQ_ERR_TOO_LARGE
+    assert gemm(M=(1 << 30) + 1) == E.AWQ_ERR_TOO_LARGE
+    assert gemm(N=1 << 21) == E.AWQ_ERR_TOO_LARGE
+    assert gemm(path=9) == E.AWQ_ERR_PATH
+    assert gemm(path=E.PATH_GEMV, M=3) == E.AWQ_ERR_PATH
+    # Split-K shapes need the workspace.
+    need = _native.workspace_bytes(1, 37888, 3584)
+    assert need > 0
+    assert gemm(M=1, N=37888, ws_=None, ws_bytes=0) == E.AWQ_ERR_WORKSPACE
+    assert gemm(M=1, N=37888, ws_=ws, ws_bytes=need - 1) == E.AWQ_ERR_WORKSPACE
+    assert gemm(M=1, N=37888, ws_=_aligned_ptr(buf, offset=4), ws_bytes=need) == E.AWQ_ERR_MISALIGNED
+    # M = 0 is a valid empty product: no launch, x and out may be NULL.
+    assert gemm(M=0, x=None, out=None) == E.AWQ_OK
+    # dequant checks
+    assert L.awq_w4a16_dequant(None, a, a, a, 512, 3584, 128, None) == E.AWQ_ERR_NULL_POINTER
+    assert L.awq_w4a16_dequant(a, a, a, mis, 512, 3584, 128, None) == E.AWQ_ERR_MISALIGNED
+    assert L.awq_w4a16_dequant(a, a, a, a, 512, 3584, 96, None) == E.AWQ_ERR_GROUP_SIZE
+
+
+# ---------------------------------------------------------------------------
+# Python entry point: argument checks (raise before touching a device)
+# ---------------------------------------------------------------------------
+
+def _cpu_operands(m=2, k=256, n=64):
+    x = torch.zeros((m, k), dtype=torch.float16)
+    qw = torch.zeros((k, n // 8), dtype=torch.int32)
+    qz = torch.zeros((k // 128, n // 8), dtype=torch.int32)
+    s = torch.zeros((k // 128, n), dtype=torch.float16)
+    return x, qw, qz, s
+
+
+def test_python_entry_rejects_bad_operands():
+    from kernels.awq_gemm import awq_gemm_forward
+
+    x, qw, qz, s = _cpu_operands()
+    with pytest.raises(ValueError, match="float16"):
+        awq_gemm_forward(x.float(), qw, qz, s)
+    with pytest.raises(ValueError, match="int32"):
+        awq_gemm_forward(x, qw.long(), qz, s)
+    with pytest.raises(ValueError, match="group_size"):
+        awq_gemm_forward(x, qw, qz, s, group_size=64)
+    with pytest.raises(ValueError, match="qweight shape"):
+        awq_gemm_forward(x, qw[:128], qz, s)
+    with pytest.raises(ValueError, match="K = "):
+        awq_gemm_forward(x[:, :200], qw, qz, s)
+    with pytest.raises(ValueError, match="scales shape"):
+        awq_gemm_forward(x, qw, qz, torch.zeros((3, 64), dtype=torch.float16))
+    # Valid operands on the CPU: refused (no CPU fallback exists).
+    with pytest.raises(ValueError, match="ROCm device"):
+        awq_gemm_forward(x, qw, qz, s)
+
+
+def test_python_plan_helper():
+    from kernels.awq_gemm import plan
+
+    d = plan(1, 37888, 3584)
+    assert d["path_name"] == "gemv"
+    assert plan(2048, 37888, 3584)["path_name"] == "tile"
+
+
+# ---------------------------------------------------------------------------
+# Roofline arithmetic against the hand-computed table of the Qwen2-7B shapes
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,k,n,expect", [
+    (1, 3584, 3584, 6_687_744),
+    (1, 3584, 512, 961_536),
+    (1, 3584, 4608, 8_596_480),
+    (1, 3584, 18944, 35_318_784),
+    (1, 3584, 37888, 70_630_400),
+    (1, 18944, 3584, 35_318_784),
+    (8, 18944, 3584, 35_634_176),
+    (64, 18944, 3584, 38_157_312),
+    (512, 18944, 3584, 58_342_400),
+    (2048, 18944, 3584, 127_548_416),
+    (2048, 3584, 37888, 240_416_768),
+])
+def test_algorithmic_bytes(m, k, n, expect):
+    assert R.algorithmic_bytes(m, n, k) == expect
+
+
+def test_bound_and_fraction():
+    assert R.bound(1, 37888, 3584) == "hbm"
+    assert R.bound(2048, 37888, 3584) == "mfma"
+    b, achieved, peak, unit, frac = R.roofline_fraction(2048, 37888, 3584, 442e-6)
+    assert (b, unit) == ("mfma", "TFLOP/s")
+    assert frac == pytest.approx(0.5, rel=1e-3)
+    b, achieved, peak, unit, frac = R.roofline_fraction(1, 37888, 3584, 70_630_400 / 4e12)
+    assert (b, unit, peak) == ("hbm", "GB/s", 8000.0)
+    assert frac == pytest.approx(0.5)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in (r.stdout + r.stderr)
