@@ -86,6 +86,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of timed CPU work")
     ap.add_argument("--no-extras", action="store_true", help="headline only (for profiling runs)")
+    ap.add_argument("--counter-pass", action="store_true",
+                    help="for rocprofv3 --pmc runs: a 64 MiB device copy (calibrates the byte counters), "
+                         "then one eager launch of every engine shape at M in {1,4,16}; no timing output")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -123,6 +126,20 @@ def main():
                 for name, k, n in ENGINE_SHAPES:
                     outs.append(awq_gemm_forward(xs[(m, k)], *layers[li][name]))
         return outs
+
+    if args.counter_pass:
+        src = torch.randint(-2**31, 2**31 - 1, (16 << 20,), device=dev, dtype=torch.int32)  # 64 MiB
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        for m in DECODE_M:
+            for name, k, n in ENGINE_SHAPES:
+                awq_gemm_forward(xs[(m, k)], *layers[0][name])
+                torch.cuda.synchronize()
+        log("counter pass done: copy 67108864 B, then " + ", ".join(
+            f"M={m} {name} {kernel_family(_native, m, n, k)}" for m in DECODE_M for name, k, n in ENGINE_SHAPES))
+        return
 
     step()  # eager: sizes the shared workspace before capture
     torch.cuda.synchronize()

@@ -65,7 +65,7 @@ typedef struct awq_w4a16_plan {
     int32_t split_k;             /* workgroups along K; > 1 uses the fp32 workspace         */
     int32_t block_threads;       /* threads per workgroup                                   */
     int32_t factored_scale;      /* skinny: 1 = scale applied per group sum, 0 = per weight */
-    int32_t reserved;            /* zero                                                    */
+    int32_t depth;               /* gemv variant 2: 128-row chunks in flight per wave; else 0 */
     int64_t grid;                /* workgroups in the one launch                            */
     uint64_t workspace_bytes;    /* split_k > 1: arrival counters + fp32 partials; else 0   */
     uint64_t lds_bytes;          /* dynamic LDS per workgroup                               */
@@ -103,10 +103,19 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
 int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 
-/* Host-only: a GEMV-path plan (M <= 2) with explicit tuning values
- * (rows_per_wave: 16, 32 or 64; k_waves: 1, 2, 4 or 8). */
-int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size,
-                        int32_t rows_per_wave, int32_t k_waves, awq_w4a16_plan* plan);
+/* Host-only: a GEMV-path plan (M <= 2) with explicit tuning values.
+ * variant 1 (all loads issued at once): tile_n 512; rows_per_wave 16, 32 or
+ * 64; k_waves 1, 2, 4 or 8; split_k and depth must be 0 (split_k is derived).
+ * variant 2 (K-streaming, one 128-row group per step): tile_n 512;
+ * rows_per_wave 16 or 32, k_waves = 128 / rows_per_wave, split_k in
+ * 1 .. K/128 with every split a whole number of groups, depth = chunks in
+ * flight per wave (2 .. 4 for 16 rows per wave, 2 .. 3 for 32).
+ * variant 3 (one workgroup per column strip over the whole K, no workspace):
+ * tile_n 32, 64, 128 or 256 output columns per workgroup; rows_per_wave 0;
+ * k_waves 16; split_k 1; depth 2 or 3 iterations in flight. */
+int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant,
+                        int32_t tile_n, int32_t rows_per_wave, int32_t k_waves, int32_t split_k,
+                        int32_t depth, awq_w4a16_plan* plan);
 
 /* Host-only: bytes of workspace awq_w4a16_gemm needs for this shape
  * (0 if none).  Replaces the module-global _dequant_buffer of

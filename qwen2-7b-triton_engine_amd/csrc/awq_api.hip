@@ -73,7 +73,7 @@ int fill_skinny(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t 
     p->split_k = (int32_t)((K + rows_per_block - 1) / rows_per_block);
     p->block_threads = (int32_t)(128 * k_waves);
     p->factored_scale = (int32_t)factored;
-    p->reserved = 0;
+    p->depth = 0;
     p->grid = skinny_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
     p->workspace_bytes =
         p->split_k > 1 ? skinny_counter_bytes() + (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
@@ -102,22 +102,58 @@ int skinny_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
 // Largest M the GEMV path serves.
 constexpr int64_t kGemvMaxM = 2;
 
-int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t k_waves, awq_w4a16_plan* p) {
+// Variants 1 and 2 use 512-column strips (tile_n = 512).  Variant 1:
+// split_k and depth are derived / unused (pass 0).  Variant 2: k_waves = 128 /
+// rows_per_wave, split_k in 1 .. K/128 with each split a whole number of
+// groups, depth 2 .. 4 chunk buffers (3 at most for 32 rows).  Variant 3:
+// tile_n 32 .. 256 columns per workgroup over the whole K, rows_per_wave 0,
+// k_waves 16, split_k 1, depth 2 or 3.
+int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, int64_t rows_per_wave,
+              int64_t k_waves, int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
     if (M > kGemvMaxM) return AWQ_ERR_PATH;
-    if (!(rows_per_wave == 16 || rows_per_wave == 32 || rows_per_wave == 64)) return AWQ_ERR_PATH;
-    if (!(k_waves == 1 || k_waves == 2 || k_waves == 4 || k_waves == 8)) return AWQ_ERR_PATH;
-    const int64_t rows_per_block = rows_per_wave * k_waves;
     p->path = AWQ_PATH_GEMV;
-    p->variant = 1;
+    p->variant = (int32_t)variant;
     p->tile_m = (int32_t)kGemvMaxM;
     p->tile_n = 512;
     p->rows_per_wave = (int32_t)rows_per_wave;
     p->k_waves = (int32_t)k_waves;
-    p->split_k = (int32_t)((K + rows_per_block - 1) / rows_per_block);
     p->block_threads = (int32_t)(64 * k_waves);
     p->factored_scale = 1;
-    p->reserved = 0;
-    p->grid = gemv_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
+    p->depth = 0;
+    if (variant == 3) {
+        // One workgroup of 16 waves per tile_n-column strip, whole K.
+        if (!(tile_n == 32 || tile_n == 64 || tile_n == 128 || tile_n == 256)) return AWQ_ERR_PATH;
+        if (rows_per_wave != 0 || k_waves != 16 || split_k != 1 || depth < 2 || depth > 3) return AWQ_ERR_PATH;
+        p->tile_n = (int32_t)tile_n;
+        p->split_k = 1;
+        p->depth = (int32_t)depth;
+        p->grid = gemv_col_blocks((int)N, (int)(tile_n / 8));
+        p->workspace_bytes = 0;
+        p->lds_bytes = 0;
+        return AWQ_OK;
+    }
+    if (tile_n != 512) return AWQ_ERR_PATH;
+    if (variant == 1) {
+        if (split_k != 0 || depth != 0) return AWQ_ERR_PATH;
+        if (!(rows_per_wave == 16 || rows_per_wave == 32 || rows_per_wave == 64)) return AWQ_ERR_PATH;
+        if (!(k_waves == 1 || k_waves == 2 || k_waves == 4 || k_waves == 8)) return AWQ_ERR_PATH;
+        const int64_t rows_per_block = rows_per_wave * k_waves;
+        p->split_k = (int32_t)((K + rows_per_block - 1) / rows_per_block);
+        p->grid = gemv_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
+    } else if (variant == 2) {
+        if (!(rows_per_wave == 16 || rows_per_wave == 32) || k_waves * rows_per_wave != kGroup) return AWQ_ERR_PATH;
+        if (depth < 2 || depth > (rows_per_wave == 16 ? 4 : 3)) return AWQ_ERR_PATH;
+        p->depth = (int32_t)depth;
+        const int64_t groups = K / kGroup;
+        if (split_k < 1 || split_k > groups) return AWQ_ERR_PATH;
+        const int64_t per = (groups + split_k - 1) / split_k;
+        if ((groups + per - 1) / per != split_k) return AWQ_ERR_PATH;
+        if (split_k > 1 && gemv_strips((int)N) * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
+        p->split_k = (int32_t)split_k;
+        p->grid = gemv_strips((int)N) * split_k;
+    } else {
+        return AWQ_ERR_PATH;
+    }
     p->workspace_bytes =
         p->split_k > 1 ? skinny_counter_bytes() + (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
     p->lds_bytes = 0;
@@ -125,10 +161,19 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t k_
     return AWQ_OK;
 }
 
-// Measured default: 64 rows per wave, 8 waves per workgroup along K (the
-// fewest split-K workgroups, whose cross-workgroup reduction is the cost).
+// Measured default (MI355X, Qwen2-7B shapes): the K-streaming variant, 16
+// rows per wave (8 waves), 3 chunks in flight, and as many K splits as keep
+// the grid within one workgroup per CU (more workgroups than CUs leaves some
+// CUs with twice the work), at least 2 chunks per split.
 int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    return fill_gemv(M, N, K, 64, 8, p);
+    const int64_t groups = K / kGroup;
+    const int64_t strips = gemv_strips((int)N);
+    int64_t split = kCUs / strips;
+    if (split > groups / 2) split = groups / 2;
+    if (split < 1) split = 1;
+    const int64_t per = (groups + split - 1) / split;
+    split = (groups + per - 1) / per;
+    return fill_gemv(M, N, K, 2, 512, 16, 8, split, 3, p);
 }
 
 int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k, awq_w4a16_plan* p) {
@@ -140,7 +185,7 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->k_waves = 1;
     p->block_threads = 256;
     p->factored_scale = 0;
-    p->reserved = 0;
+    p->depth = 0;
     p->lds_bytes = 0;
     if (variant == 3) {
         p->tile_m = 256;
@@ -199,12 +244,13 @@ int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
         const int st = fill_tile(M, N, K, p->variant, p->split_k, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_GEMV) {
-        const int st = fill_gemv(M, N, K, p->rows_per_wave, p->k_waves, &q);
+        const int st = fill_gemv(M, N, K, p->variant, p->tile_n, p->rows_per_wave, p->k_waves,
+                                 p->variant == 1 ? 0 : p->split_k, p->depth, &q);
         if (st != AWQ_OK) return st;
     } else {
         return AWQ_ERR_PATH;
     }
-    if (p->tile_m != q.tile_m || p->tile_n != q.tile_n || p->split_k != q.split_k ||
+    if (p->tile_m != q.tile_m || p->tile_n != q.tile_n || p->split_k != q.split_k || p->depth != q.depth ||
         p->block_threads != q.block_threads || p->grid != q.grid ||
         p->workspace_bytes != q.workspace_bytes || p->lds_bytes != q.lds_bytes)
         return AWQ_ERR_PATH;
@@ -251,9 +297,14 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         e = launch_skinny(a, cfg, counters, s);
     } else if (p.path == AWQ_PATH_GEMV) {
         GemvConfig cfg;
+        cfg.variant = p.variant;
         cfg.rows_per_wave = p.rows_per_wave;
         cfg.kw_count = p.k_waves;
         cfg.split_k = p.split_k;
+        const int64_t groups = K / kGroup;
+        cfg.chunks_per_split = (int)((groups + p.split_k - 1) / p.split_k);
+        cfg.depth = p.depth;
+        if (p.variant == 3) cfg.rows_per_wave = p.tile_n / 8;  // packed columns per workgroup
         a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                                               skinny_counter_bytes())
                                    : nullptr;
@@ -312,12 +363,13 @@ int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size, int
     return fill_tile(M, N, K, variant, split_k, plan);
 }
 
-int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
-                        int32_t k_waves, awq_w4a16_plan* plan) {
+int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant, int32_t tile_n,
+                        int32_t rows_per_wave, int32_t k_waves, int32_t split_k, int32_t depth,
+                        awq_w4a16_plan* plan) {
     if (!plan) return AWQ_ERR_NULL_POINTER;
     const int d = check_dims(M, N, K, group_size);
     if (d != AWQ_OK) return d;
-    return fill_gemv(M, N, K, rows_per_wave, k_waves, plan);
+    return fill_gemv(M, N, K, variant, tile_n, rows_per_wave, k_waves, split_k, depth, plan);
 }
 
 int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t path,

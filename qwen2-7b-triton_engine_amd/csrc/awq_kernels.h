@@ -29,9 +29,12 @@ struct SkinnyConfig {
 };
 
 struct GemvConfig {
-    int rows_per_wave;       // K rows per wave: 16, 32 or 64 (inside one 128-row group)
-    int kw_count;            // waves per workgroup along K: 1, 2, 4 or 8
+    int variant;             // 1: all loads at once; 2: K-streaming, one group per chunk
+    int rows_per_wave;       // K rows per wave: 16, 32 or 64 (variant 2: 16 or 32)
+    int kw_count;            // waves per workgroup along K: 1, 2, 4 or 8 (variant 2: 128 / rows_per_wave)
     int split_k;             // workgroups along K
+    int chunks_per_split;    // variant 2: 128-row groups per workgroup
+    int depth;               // variant 2: chunk buffers in flight (2, 3 or 4; 4 only for 16 rows per wave)
 };
 
 struct TileConfig {
@@ -55,6 +58,7 @@ size_t skinny_counter_bytes();
 // Same workspace contract as launch_skinny (counters, then partials).
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream);
 int64_t gemv_strips(int N);
+int64_t gemv_col_blocks(int N, int P);
 int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
 
 // Variant 2 with split_k > 1 uses the same workspace contract as launch_skinny

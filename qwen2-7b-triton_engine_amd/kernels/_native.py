@@ -43,7 +43,7 @@ class Plan(ctypes.Structure):
         ("split_k", ctypes.c_int32),
         ("block_threads", ctypes.c_int32),
         ("factored_scale", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
         ("grid", ctypes.c_int64),
         ("workspace_bytes", ctypes.c_uint64),
         ("lds_bytes", ctypes.c_uint64),
@@ -66,7 +66,8 @@ SIGNATURES = {
     "awq_w4a16_plan_skinny": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
                                              ctypes.POINTER(Plan)]),
     "awq_w4a16_counter_bytes": (ctypes.c_size_t, []),
-    "awq_w4a16_plan_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+                                           ctypes.POINTER(Plan)]),
     "awq_w4a16_plan_tile": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
     "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
@@ -135,11 +136,19 @@ def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, varian
     return p
 
 
-def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, group_size: int = 128) -> Plan:
+def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant: int = 1, split_k: int = 0,
+              depth: int | None = None, tile_n: int = 512, group_size: int = 128) -> Plan:
+    if depth is None:
+        depth = 0 if variant == 1 else 2
     p = Plan()
-    check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, rows_per_wave, k_waves, ctypes.byref(p)),
-          "awq_w4a16_plan_gemv")
+    check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, variant, tile_n, rows_per_wave, k_waves, split_k, depth,
+                                    ctypes.byref(p)), "awq_w4a16_plan_gemv")
     return p
+
+
+def plan_gemv_col(M: int, N: int, K: int, tile_n: int, depth: int = 2, group_size: int = 128) -> Plan:
+    """GEMV variant 3: one 16-wave workgroup per ``tile_n``-column strip, whole K."""
+    return plan_gemv(M, N, K, 0, 16, variant=3, split_k=1, depth=depth, tile_n=tile_n, group_size=group_size)
 
 
 def plan_tile(M: int, N: int, K: int, variant: int = 2, split_k: int = 1, group_size: int = 128) -> Plan:

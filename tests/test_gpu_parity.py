@@ -225,6 +225,21 @@ def test_gemv_plans_agree(gpu, m):
             print(f"gemv plan M={m} rows_per_wave={rpw} k_waves={kw} split={p.split_k}", flush=True)
             y = _run(gpu, x, qw, qz, s, plan_obj=p)
             _assert_close(y, y_ref, f"gemv M={m} rpw={rpw} kw={kw}")
+    # K-streaming variant: every split count that divides the 28 groups into whole chunks
+    for rpw, depths in ((16, (2, 3, 4)), (32, (2, 3))):
+        for depth in depths:
+            for split in (1, 2, 3, 4, 7, 14, 28):
+                p = _native.plan_gemv(m, n, k, rpw, 128 // rpw, variant=2, split_k=split, depth=depth)
+                print(f"gemv stream plan M={m} rows_per_wave={rpw} depth={depth} split={split}", flush=True)
+                y = _run(gpu, x, qw, qz, s, plan_obj=p)
+                _assert_close(y, y_ref, f"gemv stream M={m} rpw={rpw} depth={depth} split={split}")
+    # Whole-K column-strip variant: every strip width and depth.
+    for tile_n in (32, 64, 128, 256):
+        for depth in (2, 3):
+            p = _native.plan_gemv_col(m, n, k, tile_n, depth)
+            print(f"gemv col plan M={m} tile_n={tile_n} depth={depth} grid={p.grid}", flush=True)
+            y = _run(gpu, x, qw, qz, s, plan_obj=p)
+            _assert_close(y, y_ref, f"gemv col M={m} tile_n={tile_n} depth={depth}")
 
 
 @pytest.mark.parametrize("m,k,n", [(65, 1024, 1032), (200, 3584, 520), (512, 2048, 264), (130, 18944, 128)])

@@ -121,6 +121,19 @@ def test_skinny_and_gemv_plan_rejections():
     with pytest.raises(_native.AwqNativeError):
         _native.plan_gemv(1, 512, 3584, 48, 8)          # rows per wave not an instance
     with pytest.raises(_native.AwqNativeError):
+        _native.plan_gemv(1, 512, 3584, 64, 8, split_k=2)   # variant 1 derives split_k
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_gemv(1, 512, 3584, 16, 4, variant=2, split_k=2)   # k_waves must be 128 / rows
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_gemv(1, 512, 3584, 16, 8, variant=2, split_k=9)   # 28 groups: no split of 9 whole chunks
+    p = _native.plan_gemv(1, 512, 3584, 16, 8, variant=2, split_k=7)
+    assert (p.split_k, p.grid, p.block_threads) == (7, 7, 512)
+    with pytest.raises(_native.AwqNativeError):
+        _native.plan_gemv_col(1, 512, 3584, 48)                          # strip width not an instance
+    p = _native.plan_gemv_col(1, 3584, 3584, 128)
+    # 28 strips of 16 packed columns, grouped by 128-byte line onto 8 XCDs: 2 strips per line.
+    assert (p.grid, p.block_threads, p.workspace_bytes) == (32, 1024, 0)
+    with pytest.raises(_native.AwqNativeError):
         _native.plan_skinny(65, 512, 3584, 256, 2)      # skinny serves M <= 64
     with pytest.raises(_native.AwqNativeError):
         _native.plan_skinny(8, 512, 3584, 256, 3)       # k_waves must be 1, 2 or 4
