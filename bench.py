@@ -214,6 +214,20 @@ def main():
     avg_t = family_time[dom] / family_launches[dom]
     avg_b = family_bytes[dom] / family_launches[dom]
     achieved = avg_b / avg_t / 1e9
+    # HBM bytes per launch of the dominant kernel: rocprofv3 FETCH_SIZE + WRITE_SIZE of one launch
+    # per (M, shape), each scaled by the counter's reading for a copy of known size (the committed
+    # profile that bench.py --counter-pass feeds), averaged over the same launches as `achieved`.
+    traffic = None
+    traffic_path = os.path.join(ROOT, "profiles", "decode_sweep_pmc_traffic.json")
+    if os.path.exists(traffic_path):
+        with open(traffic_path) as f:
+            pmc = json.load(f)
+        prefix = {"gemv": "awq_gemv", "skinny": "awq_skinny", "tile": "awq_tile"}[dom]
+        keys = [(m, name) for m in DECODE_M for name, k, n in ENGINE_SHAPES if kernel_family(_native, m, n, k) == dom]
+        hits = {(e["M"], e["shape"]): e["fetch_bytes"] + e["write_bytes"] for e in pmc["launches"]
+                if e["kernel"].startswith(prefix)}
+        if keys and all(key in hits for key in keys):
+            traffic = round(sum(hits[key] for key in keys) / len(keys))
     result["roofline"] = {
         "bound": "hbm",
         "kernel": {"gemv": "awq_gemv_kernel", "skinny": "awq_skinny_kernel", "tile": "awq_tile_kernel"}[dom],
@@ -221,7 +235,8 @@ def main():
         "peak": HBM_PEAK_BPS / 1e9,
         "unit": "GB/s",
         "frac": round(achieved / (HBM_PEAK_BPS / 1e9), 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": "profiles/decode_sweep_pmc_traffic.md" if traffic is not None else None,
         "bytes_per_launch": round(avg_b),
         "avg_launch_us": round(avg_t * 1e6, 3),
         "launches_per_step": family_launches[dom],
