@@ -51,12 +51,13 @@ typedef enum awq_w4a16_path {
     AWQ_PATH_AUTO = 0,
     AWQ_PATH_SKINNY = 1,         /* decode: MFMA skinny-M streaming kernel (M <= 64)         */
     AWQ_PATH_TILE = 2,           /* prefill: LDS-tiled MFMA GEMM                            */
-    AWQ_PATH_GEMV = 3            /* decode: VALU dot2 GEMV (M <= 2)                         */
+    AWQ_PATH_GEMV = 3,           /* decode: VALU dot2 GEMV (M <= 2)                         */
+    AWQ_PATH_NARROW = 4          /* decode: K-streaming 4x4x4 MFMA kernel (M <= 16)         */
 } awq_w4a16_path;
 
 /* What the dispatcher will launch for a shape (host-side description). */
 typedef struct awq_w4a16_plan {
-    int32_t path;                /* AWQ_PATH_SKINNY or AWQ_PATH_TILE                       */
+    int32_t path;                /* AWQ_PATH_SKINNY, _TILE, _GEMV or _NARROW               */
     int32_t variant;             /* kernel variant inside the path                          */
     int32_t tile_m;              /* rows of x per work unit (skinny: 16, 32 or 64)          */
     int32_t tile_n;              /* output columns per work unit                            */
@@ -116,6 +117,16 @@ int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
 int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant,
                         int32_t tile_n, int32_t rows_per_wave, int32_t k_waves, int32_t split_k,
                         int32_t depth, awq_w4a16_plan* plan);
+
+/* Host-only: a narrow-M plan (M <= 16): the K-streaming schedule of GEMV
+ * variant 2 with v_mfma_f32_4x4x4_16b_f16 arithmetic.  rows_per_wave 16 or
+ * 32 (128 / rows_per_wave waves per workgroup); split_k in 1 .. K/128 with
+ * every split a whole number of 128-row groups; depth = groups in flight
+ * per wave (2 or 3; 2 for 32 rows per wave); factored_scale 1 = zero and
+ * scale applied to group sums (M <= 8), 0 = fp16 weight (q - z) * s formed
+ * per weight as the reference does. */
+int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
+                          int32_t split_k, int32_t depth, int32_t factored_scale, awq_w4a16_plan* plan);
 
 /* Host-only: bytes of workspace awq_w4a16_gemm needs for this shape
  * (0 if none).  Replaces the module-global _dequant_buffer of

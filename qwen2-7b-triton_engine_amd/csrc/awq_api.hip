@@ -10,11 +10,9 @@ using namespace awq;
 
 namespace {
 
-// Active waves the decode dispatcher aims for: 256 CUs x 4 SIMDs x 2.
-constexpr int64_t kSkinnyTargetWaves = 2048;
 // Largest M the skinny path serves (4 MFMA blocks of 16 rows).
 constexpr int64_t kSkinnyMaxM = 64;
-// M above which AUTO picks the tile kernel.
+// M above which AUTO never picks the skinny kernel.
 constexpr int64_t kAutoSkinnyMaxM = 64;
 // LDS the skinny dispatcher allows one workgroup for its K reduction.
 constexpr uint64_t kSkinnyLdsBudget = 64 * 1024;
@@ -83,20 +81,38 @@ int fill_skinny(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t 
     return AWQ_OK;
 }
 
-// Defaults measured on MI355X (K range per wave x waves per workgroup swept
-// per shape): two waves along K per workgroup; 512 rows per wave for the long
-// K of down_proj, 256 otherwise; the chunk-pipelined main loop for one row
-// block, the plain loop (smaller register file, more waves) for more.
+// Defaults measured on MI355X (K range per wave x waves per workgroup x main
+// loop swept over the Qwen2-7B shapes at M = 4 and 16).  K rows per split
+// (rows_per_wave x waves): wide N (>= 64 column-tile pairs) -- 1024 rows for
+// M <= 4, all of K above (the split-K partials grow with M); narrow N --
+// 512 rows for K <= 8192, else 1024 (M <= 4) or 2048.  Four waves along K
+// for narrow N, two for wide N (fewer waves, more workgroups), fewer when
+// the LDS reduction would not fit; the chunk-pipelined main loop for K
+// ranges of 512 rows per wave and more, the plain loop otherwise.
 int skinny_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (M > kSkinnyMaxM) return AWQ_ERR_PATH;
     const int mb = m_blocks_for(M);
-    int64_t kw = 2;
+    const bool wide = skinny_pairs((int)N) >= 64;
+    int64_t kw = wide ? 2 : 4;
     while (kw > 1 && skinny_lds_bytes((int)M, mb, (int)kw) > kSkinnyLdsBudget) kw /= 2;
-    int64_t r = K >= 8192 ? 512 : 256;
-    while (r > K) r /= 2;
-    if (r < kGroup) r = r >= 64 ? 64 : 32;
-    const int64_t variant = mb == 1 ? 1 : 2;
+    int64_t rows_per_split;
+    if (wide) rows_per_split = M <= 4 ? 1024 : K;
+    else if (K > 8192) rows_per_split = M <= 4 ? 1024 : 2048;
+    else rows_per_split = 512;
+    const int64_t want = (rows_per_split + kw - 1) / kw;
+    int64_t r = want <= 32 ? 32 : (want <= 64 ? 64 : (want + kGroup - 1) / kGroup * kGroup);
+    if (r > K) r = K;
+    const int64_t variant = (mb == 1 && r >= 512) ? 1 : 2;
     return fill_skinny(M, N, K, r, kw, variant, mb == 4 ? 0 : 1, p);
+}
+
+// AUTO between skinny and tile for 16 < M <= 64: the tile kernel's 256-row
+// tiles waste MFMA work at such M but read the weights with far fewer,
+// larger workgroups; it wins for narrow N, the skinny kernel for wide N
+// (measured at M = 32 .. 64 on the Qwen2-7B shapes).
+bool auto_skinny(int64_t M, int64_t N) {
+    if (M <= 16) return true;
+    return M <= kAutoSkinnyMaxM && skinny_pairs((int)N) >= 64;
 }
 
 // Largest M the GEMV path serves.
@@ -165,15 +181,59 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
 // rows per wave (8 waves), 3 chunks in flight, and as many K splits as keep
 // the grid within one workgroup per CU (more workgroups than CUs leaves some
 // CUs with twice the work), at least 2 chunks per split.
+int64_t stream_split(int64_t N, int64_t K);
+
 int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    return fill_gemv(M, N, K, 2, 512, 16, 8, stream_split(N, K), 3, p);
+}
+
+constexpr int64_t kNarrowMaxM = 16;
+
+int fill_narrow(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t split_k, int64_t depth,
+                int64_t factored, awq_w4a16_plan* p) {
+    if (M > kNarrowMaxM) return AWQ_ERR_PATH;
+    if (!(rows_per_wave == 16 || rows_per_wave == 32)) return AWQ_ERR_PATH;
+    if (depth < 2 || depth > (rows_per_wave == 16 ? 3 : 2)) return AWQ_ERR_PATH;
+    if (factored != 0 && factored != 1) return AWQ_ERR_PATH;
+    const int mb = narrow_blocks_for((int)M);
+    if (factored && mb > 2) return AWQ_ERR_PATH;
+    const int64_t groups = K / kGroup;
+    if (split_k < 1 || split_k > groups) return AWQ_ERR_PATH;
+    const int64_t per = (groups + split_k - 1) / split_k;
+    if ((groups + per - 1) / per != split_k) return AWQ_ERR_PATH;
+    if (split_k > 1 && gemv_strips((int)N) * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
+    p->path = AWQ_PATH_NARROW;
+    p->variant = 1;
+    p->tile_m = 4 * mb;
+    p->tile_n = 512;
+    p->rows_per_wave = (int32_t)rows_per_wave;
+    p->k_waves = (int32_t)(kGroup / rows_per_wave);
+    p->split_k = (int32_t)split_k;
+    p->block_threads = 64 * p->k_waves;
+    p->factored_scale = (int32_t)factored;
+    p->depth = (int32_t)depth;
+    p->grid = gemv_strips((int)N) * split_k;
+    p->workspace_bytes =
+        split_k > 1 ? skinny_counter_bytes() + (uint64_t)split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    p->lds_bytes = 0;
+    if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
+    return AWQ_OK;
+}
+
+// Split count of the K-streaming kernels: as many K splits as keep the grid
+// within one workgroup per CU, at least 2 groups per split.
+int64_t stream_split(int64_t N, int64_t K) {
     const int64_t groups = K / kGroup;
     const int64_t strips = gemv_strips((int)N);
     int64_t split = kCUs / strips;
     if (split > groups / 2) split = groups / 2;
     if (split < 1) split = 1;
     const int64_t per = (groups + split - 1) / split;
-    split = (groups + per - 1) / per;
-    return fill_gemv(M, N, K, 2, 512, 16, 8, split, 3, p);
+    return (groups + per - 1) / per;
+}
+
+int narrow_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    return fill_narrow(M, N, K, 16, stream_split(N, K), 2, narrow_blocks_for((int)M) <= 2 ? 1 : 0, p);
 }
 
 int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k, awq_w4a16_plan* p) {
@@ -243,6 +303,9 @@ int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
     } else if (p->path == AWQ_PATH_TILE) {
         const int st = fill_tile(M, N, K, p->variant, p->split_k, &q);
         if (st != AWQ_OK) return st;
+    } else if (p->path == AWQ_PATH_NARROW) {
+        const int st = fill_narrow(M, N, K, p->rows_per_wave, p->split_k, p->depth, p->factored_scale, &q);
+        if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_GEMV) {
         const int st = fill_gemv(M, N, K, p->variant, p->tile_n, p->rows_per_wave, p->k_waves,
                                  p->variant == 1 ? 0 : p->split_k, p->depth, &q);
@@ -295,6 +358,18 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
                                                               skinny_counter_bytes())
                                    : nullptr;
         e = launch_skinny(a, cfg, counters, s);
+    } else if (p.path == AWQ_PATH_NARROW) {
+        NarrowConfig cfg;
+        cfg.rows_per_wave = p.rows_per_wave;
+        cfg.split_k = p.split_k;
+        const int64_t groups = K / kGroup;
+        cfg.chunks_per_split = (int)((groups + p.split_k - 1) / p.split_k);
+        cfg.depth = p.depth;
+        cfg.factored = p.factored_scale != 0;
+        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                              skinny_counter_bytes())
+                                   : nullptr;
+        e = launch_narrow(a, cfg, static_cast<uint32_t*>(workspace), s);
     } else if (p.path == AWQ_PATH_GEMV) {
         GemvConfig cfg;
         cfg.variant = p.variant;
@@ -372,6 +447,14 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
     return fill_gemv(M, N, K, variant, tile_n, rows_per_wave, k_waves, split_k, depth, plan);
 }
 
+int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
+                          int32_t split_k, int32_t depth, int32_t factored_scale, awq_w4a16_plan* plan) {
+    if (!plan) return AWQ_ERR_NULL_POINTER;
+    const int d = check_dims(M, N, K, group_size);
+    if (d != AWQ_OK) return d;
+    return fill_narrow(M, N, K, rows_per_wave, split_k, depth, factored_scale, plan);
+}
+
 int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t path,
                        awq_w4a16_plan* plan) {
     if (!plan) return AWQ_ERR_NULL_POINTER;
@@ -380,9 +463,10 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
     switch (path) {
         case AWQ_PATH_AUTO:
             if (M <= kGemvMaxM) return gemv_plan(M, N, K, plan);
-            return M <= kAutoSkinnyMaxM ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);
+            return auto_skinny(M, N) ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);
         case AWQ_PATH_SKINNY: return skinny_plan(M, N, K, plan);
         case AWQ_PATH_GEMV: return gemv_plan(M, N, K, plan);
+        case AWQ_PATH_NARROW: return narrow_plan(M, N, K, plan);
         case AWQ_PATH_TILE: return tile_plan(M, N, K, plan);
         default: return AWQ_ERR_PATH;
     }

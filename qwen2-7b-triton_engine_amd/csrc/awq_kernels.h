@@ -37,6 +37,14 @@ struct GemvConfig {
     int depth;               // variant 2: chunk buffers in flight (2, 3 or 4; 4 only for 16 rows per wave)
 };
 
+struct NarrowConfig {
+    int rows_per_wave;       // 16 or 32 (128 / rows_per_wave waves per workgroup)
+    int split_k;             // workgroups along K
+    int chunks_per_split;    // 128-row groups per workgroup
+    int depth;               // chunks in flight: 2 or 3 (3 only for 16 rows per wave)
+    bool factored;           // zero and scale per group sum (M <= 8) or per weight
+};
+
 struct TileConfig {
     int variant;             // 1: 128x128x32; 2: 128x128x64, prefetch, XCD order, split-K; 3: 256x128x64, x ring in LDS
     int tile_m, tile_n;
@@ -60,6 +68,10 @@ hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* count
 int64_t gemv_strips(int N);
 int64_t gemv_col_blocks(int N, int P);
 int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
+
+// Same workspace contract as launch_skinny; one arrival counter per 512-column strip.
+hipError_t launch_narrow(const GemmArgs& a, const NarrowConfig& cfg, uint32_t* counters, hipStream_t stream);
+int narrow_blocks_for(int M);
 
 // Variant 2 with split_k > 1 uses the same workspace contract as launch_skinny
 // (counters: one per tile).

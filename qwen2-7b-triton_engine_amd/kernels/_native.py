@@ -27,7 +27,8 @@ PATH_AUTO = 0
 PATH_SKINNY = 1
 PATH_TILE = 2
 PATH_GEMV = 3
-PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile", PATH_GEMV: "gemv"}
+PATH_NARROW = 4
+PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile", PATH_GEMV: "gemv", PATH_NARROW: "narrow"}
 
 
 class Plan(ctypes.Structure):
@@ -69,6 +70,8 @@ SIGNATURES = {
     "awq_w4a16_plan_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                            ctypes.POINTER(Plan)]),
     "awq_w4a16_plan_tile": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_narrow": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
+                                             ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
     "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
     "awq_w4a16_validate": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
@@ -143,6 +146,17 @@ def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant:
     p = Plan()
     check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, variant, tile_n, rows_per_wave, k_waves, split_k, depth,
                                     ctypes.byref(p)), "awq_w4a16_plan_gemv")
+    return p
+
+
+def plan_narrow(M: int, N: int, K: int, rows_per_wave: int, split_k: int, depth: int = 2,
+                factored_scale: int | None = None, group_size: int = 128) -> Plan:
+    """Narrow-M path (M <= 16): GEMV schedule, 4x4x4 MFMA arithmetic."""
+    if factored_scale is None:
+        factored_scale = 1 if M <= 8 else 0
+    p = Plan()
+    check(lib().awq_w4a16_plan_narrow(M, N, K, group_size, rows_per_wave, split_k, depth, factored_scale,
+                                      ctypes.byref(p)), "awq_w4a16_plan_narrow")
     return p
 
 

@@ -423,3 +423,38 @@ def test_golden_edge_gemm_finite_columns(gpu):
             err = np.abs(y[small] - y_ref[small])
             assert np.all(err <= tol[small]), (
                 f"M={m} path={path}: worst excess {np.max(err - tol[small]):.3e}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16])
+def test_narrow_plans_agree(gpu, m):
+    """Narrow-M kernel (4x4x4 MFMA on the K-streaming schedule): every instance
+    for this M, split counts from 1 up, both zero/scale modes."""
+    k, n = 3584, 1032
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=16)
+    y_ref = O.awq_gemm_oracle(x, qw, qz, s)
+    mb = 1 if m <= 4 else (2 if m <= 8 else 4)
+    for rpw, depths in ((16, (2, 3)), (32, (2,))):
+        for depth in depths:
+            for factored in (0,):
+                for split in (1, 3, 7, 28):
+                    if mb == 4 and (rpw, depth) != (16, 2):
+                        continue
+                    p = _native.plan_narrow(m, n, k, rpw, split, depth, factored)
+                    print(f"narrow plan M={m} rpw={rpw} depth={depth} factored={factored} split={split}", flush=True)
+                    y = _run(gpu, x, qw, qz, s, plan_obj=p)
+                    _assert_close(y, y_ref, f"narrow M={m} rpw={rpw} d={depth} f={factored} split={split}")
+
+
+def test_narrow_one_hot_bit_exact(gpu):
+    """Per-weight mode forms the reference's fp16 weight exactly: one-hot rows
+    of x reproduce dequantised rows bit for bit."""
+    k, n = 384, 520
+    _, qw, qz, s = O.make_inputs(1, k, n, seed=17)
+    w = O.dequant_awq(qw, qz, s)
+    rows = [0, 1, 130, 255, 383]
+    x = np.zeros((len(rows), k), dtype=np.float16)
+    for i, r in enumerate(rows):
+        x[i, r] = 1.0
+    p = _native.plan_narrow(len(rows), n, k, 16, 1, 2, 0)
+    y = _run(gpu, x, qw, qz, s, plan_obj=p)
+    assert np.array_equal(y.view(np.uint16), w[rows].view(np.uint16))

@@ -78,9 +78,10 @@ def test_plan_struct_matches_header():
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 16, 17, 33, 64, 65, 128, 512, 2048, 2049])
 def test_auto_plan_invariants(L, m, k, n):
     p = _native.plan_for(m, n, k)
+    wide = -(-(-(-n // 128)) // 2) >= 64   # 128-column tile pairs
     if m <= 2:
         assert p.path == _native.PATH_GEMV
-    elif m <= 64:
+    elif m <= 16 or (m <= 64 and wide):
         assert p.path == _native.PATH_SKINNY
         assert p.tile_m >= m
     else:
