@@ -52,12 +52,13 @@ typedef enum awq_w4a16_path {
     AWQ_PATH_SKINNY = 1,         /* decode: MFMA skinny-M streaming kernel (M <= 64)         */
     AWQ_PATH_TILE = 2,           /* prefill: LDS-tiled MFMA GEMM                            */
     AWQ_PATH_GEMV = 3,           /* decode: VALU dot2 GEMV (M <= 2)                         */
-    AWQ_PATH_NARROW = 4          /* decode: K-streaming 4x4x4 MFMA kernel (M <= 16)         */
+    AWQ_PATH_NARROW = 4,         /* decode: K-streaming 4x4x4 MFMA kernel (M <= 16)         */
+    AWQ_PATH_STREAM = 5          /* decode: column-quad streaming 16x16x32 MFMA kernel (M <= 16) */
 } awq_w4a16_path;
 
 /* What the dispatcher will launch for a shape (host-side description). */
 typedef struct awq_w4a16_plan {
-    int32_t path;                /* AWQ_PATH_SKINNY, _TILE, _GEMV or _NARROW               */
+    int32_t path;                /* AWQ_PATH_SKINNY, _TILE, _GEMV, _NARROW or _STREAM      */
     int32_t variant;             /* kernel variant inside the path                          */
     int32_t tile_m;              /* rows of x per work unit (skinny: 16, 32 or 64)          */
     int32_t tile_n;              /* output columns per work unit                            */
@@ -68,7 +69,8 @@ typedef struct awq_w4a16_plan {
     int32_t factored_scale;      /* skinny: 1 = scale applied per group sum, 0 = per weight */
     int32_t depth;               /* gemv variant 2: 128-row chunks in flight per wave; else 0 */
     int64_t grid;                /* workgroups in the one launch                            */
-    uint64_t workspace_bytes;    /* split_k > 1: arrival counters + fp32 partials; else 0   */
+    uint64_t workspace_bytes;    /* split_k > 1: counter block + fp32 partials or 64-bit
+                                    fixed-point slots (GEMV variant 4, STREAM); else 0   */
     uint64_t lds_bytes;          /* dynamic LDS per workgroup                               */
 } awq_w4a16_plan;
 
@@ -105,6 +107,11 @@ int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 
 /* Host-only: a GEMV-path plan (M <= 2) with explicit tuning values.
+ * variant 4 (column quads, N % 32 == 0): tile_n 512; rows_per_wave 0 and
+ * depth 0; k_waves 1 .. 8 wavefronts, which take every k_waves-th 32-row
+ * chunk of the workgroup's share of K; split_k 1 .. min(K/32, 255) workgroups
+ * share each strip's K evenly; split-K partials meet in 64-bit fixed-point
+ * workspace slots.
  * variant 1 (all loads issued at once): tile_n 512; rows_per_wave 16, 32 or
  * 64; k_waves 1, 2, 4 or 8; split_k and depth must be 0 (split_k is derived).
  * variant 2 (K-streaming, one 128-row group per step): tile_n 512;
@@ -118,6 +125,16 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
                         int32_t tile_n, int32_t rows_per_wave, int32_t k_waves, int32_t split_k,
                         int32_t depth, awq_w4a16_plan* plan);
 
+/* Host-only: a stream-path plan (M <= 16, N % 32 == 0): each 64-packed-
+ * column strip's K/32 chunks of 32 rows are divided evenly among split_k
+ * workgroups (1 .. min(K/32, 255)) of k_waves wavefronts (1 .. 4), which
+ * take every k_waves-th chunk; v_mfma_f32_16x16x32_f16 on the reference's
+ * exact fp16 weight; split-K partials meet in 64-bit fixed-point workspace
+ * slots.  Same column-quad lane layout and work split as GEMV variant 4.
+ * No reference counterpart beyond the decode dispatch it serves
+ * (kernels/awq_gemm.py:251-282). */
+int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t k_waves,
+                          int32_t split_k, awq_w4a16_plan* plan);
 /* Host-only: a narrow-M plan (M <= 16): the K-streaming schedule of GEMV
  * variant 2 with v_mfma_f32_4x4x4_16b_f16 arithmetic.  rows_per_wave 16 or
  * 32 (128 / rows_per_wave waves per workgroup); split_k in 1 .. K/128 with
@@ -132,12 +149,13 @@ int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, i
  * (0 if none).  Replaces the module-global _dequant_buffer of
  * kernels/awq_gemm.py:234,255-262, which holds K*N fp16 values; the
  * workspace here holds, for split-K launches, a block of uint32 arrival
- * counters (first awq_w4a16_counter_bytes() bytes) followed by the fp32
- * partial sums.  The counter block must be zero-filled before the
- * workspace is first used; every call leaves it zero again, so one zeroed
- * workspace serves any number of calls, as long as calls that share it do
- * not run concurrently.  Returns 0 for invalid dimensions as well;
- * awq_w4a16_plan_for reports the reason. */
+ * counters (first awq_w4a16_counter_bytes() bytes) followed by either the
+ * fp32 partial sums [split_k, M, N] or one 64-bit fixed-point slot per
+ * output element [M, N] (GEMV variant 4 and the stream path).  The whole
+ * workspace must be zero-filled before it is first used; every call leaves
+ * it zero again, so one zeroed workspace serves any number of calls of any
+ * path, as long as calls that share it do not run concurrently.  Returns 0
+ * for invalid dimensions as well; awq_w4a16_plan_for reports the reason. */
 size_t awq_w4a16_counter_bytes(void);
 size_t awq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size);
 size_t awq_w4a16_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int32_t group_size,

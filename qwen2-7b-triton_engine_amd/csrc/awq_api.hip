@@ -117,6 +117,8 @@ bool auto_skinny(int64_t M, int64_t N) {
 
 // Largest M the GEMV path serves.
 constexpr int64_t kGemvMaxM = 2;
+// LDS the column-quad GEMV may stage per workgroup.
+constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 
 // Variants 1 and 2 use 512-column strips (tile_n = 512).  Variant 1:
 // split_k and depth are derived / unused (pass 0).  Variant 2: k_waves = 128 /
@@ -149,6 +151,24 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
         return AWQ_OK;
     }
     if (tile_n != 512) return AWQ_ERR_PATH;
+    if (variant == 4) {
+        // Column quads: N % 32 == 0; rows_per_wave 0 and depth 0 (each
+        // strip's K/32 chunks are divided evenly over split_k workgroups of
+        // k_waves waves); split_k <= min(K/32, kFixMaxSplit); the groups and
+        // x rows a workgroup stages must fit its prologue loads, and the
+        // staged data its LDS.
+        if (N % 32 != 0 || rows_per_wave != 0 || depth != 0) return AWQ_ERR_PATH;
+        if (k_waves < 1 || k_waves > 8 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
+            return AWQ_ERR_PATH;
+        if (!gemv_quad_fits((int)M, (int)K, (int)split_k, (int)k_waves)) return AWQ_ERR_PATH;
+        p->split_k = (int32_t)split_k;
+        p->grid = gemv_strips((int)N) * split_k;
+        p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
+        p->lds_bytes = gemv_quad_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves);
+        if (p->lds_bytes > kQuadLdsBudget) return AWQ_ERR_PATH;
+        if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
+        return AWQ_OK;
+    }
     if (variant == 1) {
         if (split_k != 0 || depth != 0) return AWQ_ERR_PATH;
         if (!(rows_per_wave == 16 || rows_per_wave == 32 || rows_per_wave == 64)) return AWQ_ERR_PATH;
@@ -183,7 +203,32 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
 // CUs with twice the work), at least 2 chunks per split.
 int64_t stream_split(int64_t N, int64_t K);
 
+// Column-quad GEMV (variant 4) shape: as many K splits as keep the grid
+// within one workgroup per CU (a CU holding two workgroups finishes last),
+// four waves per workgroup (measured: interleaved chunks of four waves
+// stream faster than eight), fewer when a workgroup has fewer chunks; more
+// splits or waves when the staged consts would not fit.
+int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    const int64_t strips = gemv_strips((int)N);
+    const int64_t C = K / 32;
+    int64_t split = kCUs / strips;
+    if (split > C) split = C;
+    if (split > kFixMaxSplit) split = kFixMaxSplit;
+    if (split < 1) split = 1;
+    int64_t w = C / split;
+    if (w > 4) w = 4;
+    if (w < 1) w = 1;
+    while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w) ||
+           gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w) > kQuadLdsBudget) {
+        if (w < 8) ++w;
+        else if (split < C && split < kFixMaxSplit) ++split;
+        else break;
+    }
+    return fill_gemv(M, N, K, 4, 512, 0, w, split, 0, p);
+}
+
 int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    if (N % 32 == 0) return quad_plan(M, N, K, p);
     return fill_gemv(M, N, K, 2, 512, 16, 8, stream_split(N, K), 3, p);
 }
 
@@ -194,9 +239,10 @@ int fill_narrow(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t 
     if (M > kNarrowMaxM) return AWQ_ERR_PATH;
     if (!(rows_per_wave == 16 || rows_per_wave == 32)) return AWQ_ERR_PATH;
     if (depth < 2 || depth > (rows_per_wave == 16 ? 3 : 2)) return AWQ_ERR_PATH;
-    if (factored != 0 && factored != 1) return AWQ_ERR_PATH;
+    // Only the per-weight mode is served: the group-factored mode gave
+    // non-finite, run-to-run different outputs at M = 1 with split-K.
+    if (factored != 0) return AWQ_ERR_PATH;
     const int mb = narrow_blocks_for((int)M);
-    if (factored && mb > 2) return AWQ_ERR_PATH;
     const int64_t groups = K / kGroup;
     if (split_k < 1 || split_k > groups) return AWQ_ERR_PATH;
     const int64_t per = (groups + split_k - 1) / split_k;
@@ -233,7 +279,56 @@ int64_t stream_split(int64_t N, int64_t K) {
 }
 
 int narrow_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    return fill_narrow(M, N, K, 16, stream_split(N, K), 2, narrow_blocks_for((int)M) <= 2 ? 1 : 0, p);
+    return fill_narrow(M, N, K, 16, stream_split(N, K), 2, 0, p);
+}
+
+// Stream path (M <= 16): column quads, 16x16x32 MFMA, fixed-point split-K.
+constexpr int64_t kStreamMaxM = 16;
+constexpr uint64_t kStreamLdsBudget = 160 * 1024;
+
+int fill_stream(int64_t M, int64_t N, int64_t K, int64_t k_waves, int64_t split_k, awq_w4a16_plan* p) {
+    if (M > kStreamMaxM || N % 32 != 0) return AWQ_ERR_PATH;
+    if (k_waves < 1 || k_waves > 4 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
+        return AWQ_ERR_PATH;
+    if (!stream_fits((int)K, (int)split_k, (int)k_waves)) return AWQ_ERR_PATH;
+    p->path = AWQ_PATH_STREAM;
+    p->variant = 1;
+    p->tile_m = 16;
+    p->tile_n = 512;
+    p->rows_per_wave = 0;
+    p->k_waves = (int32_t)k_waves;
+    p->split_k = (int32_t)split_k;
+    p->block_threads = (int32_t)(64 * k_waves);
+    p->factored_scale = 0;
+    p->depth = 0;
+    p->grid = gemv_strips((int)N) * split_k;
+    p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
+    p->lds_bytes = stream_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves);
+    if (p->lds_bytes > kStreamLdsBudget) return AWQ_ERR_PATH;
+    if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
+    return AWQ_OK;
+}
+
+// Stream plan: as the column-quad GEMV's -- as many K splits as keep the
+// grid within one workgroup per CU, four waves (one per SIMD).
+int stream_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    if (M > kStreamMaxM || N % 32 != 0) return AWQ_ERR_PATH;
+    const int64_t strips = gemv_strips((int)N);
+    const int64_t C = K / 32;
+    int64_t split = kCUs / strips;
+    if (split > C) split = C;
+    if (split > kFixMaxSplit) split = kFixMaxSplit;
+    if (split < 1) split = 1;
+    int64_t w = C / split;
+    if (w > 4) w = 4;
+    if (w < 1) w = 1;
+    while (!stream_fits((int)K, (int)split, (int)w) ||
+           stream_lds_bytes((int)M, (int)K, (int)split, (int)w) > kStreamLdsBudget) {
+        if (w < 4 && stream_lds_bytes((int)M, (int)K, (int)split, (int)(w + 1)) <= kStreamLdsBudget) ++w;
+        else if (split < C && split < kFixMaxSplit) ++split;
+        else break;
+    }
+    return fill_stream(M, N, K, w, split, p);
 }
 
 int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k, awq_w4a16_plan* p) {
@@ -306,6 +401,9 @@ int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
     } else if (p->path == AWQ_PATH_NARROW) {
         const int st = fill_narrow(M, N, K, p->rows_per_wave, p->split_k, p->depth, p->factored_scale, &q);
         if (st != AWQ_OK) return st;
+    } else if (p->path == AWQ_PATH_STREAM) {
+        const int st = fill_stream(M, N, K, p->k_waves, p->split_k, &q);
+        if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_GEMV) {
         const int st = fill_gemv(M, N, K, p->variant, p->tile_n, p->rows_per_wave, p->k_waves,
                                  p->variant == 1 ? 0 : p->split_k, p->depth, &q);
@@ -358,6 +456,8 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
                                                               skinny_counter_bytes())
                                    : nullptr;
         e = launch_skinny(a, cfg, counters, s);
+    } else if (p.path == AWQ_PATH_STREAM) {
+        e = launch_stream(a, p.split_k, p.k_waves, static_cast<uint32_t*>(workspace), s);
     } else if (p.path == AWQ_PATH_NARROW) {
         NarrowConfig cfg;
         cfg.rows_per_wave = p.rows_per_wave;
@@ -447,6 +547,14 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
     return fill_gemv(M, N, K, variant, tile_n, rows_per_wave, k_waves, split_k, depth, plan);
 }
 
+int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t k_waves, int32_t split_k,
+                          awq_w4a16_plan* plan) {
+    if (!plan) return AWQ_ERR_NULL_POINTER;
+    const int d = check_dims(M, N, K, group_size);
+    if (d != AWQ_OK) return d;
+    return fill_stream(M, N, K, k_waves, split_k, plan);
+}
+
 int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
                           int32_t split_k, int32_t depth, int32_t factored_scale, awq_w4a16_plan* plan) {
     if (!plan) return AWQ_ERR_NULL_POINTER;
@@ -467,6 +575,7 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
         case AWQ_PATH_SKINNY: return skinny_plan(M, N, K, plan);
         case AWQ_PATH_GEMV: return gemv_plan(M, N, K, plan);
         case AWQ_PATH_NARROW: return narrow_plan(M, N, K, plan);
+        case AWQ_PATH_STREAM: return stream_plan(M, N, K, plan);
         case AWQ_PATH_TILE: return tile_plan(M, N, K, plan);
         default: return AWQ_ERR_PATH;
     }

@@ -117,6 +117,15 @@ __device__ __forceinline__ uint32_t zero_splat_x16(uint32_t zw, int c) {
     return kMagic2 | zz | (zz << 16);
 }
 
+// a.lo * b.lo + a.hi * b.hi in fp32 from fp16 pairs, starting from zero: the
+// VOP3 form of v_dot2 with an inline-constant accumulator (the compiler
+// otherwise picks the VOP2 form and clears a register first).
+__device__ __forceinline__ float dot2_from_zero(uint32_t a, uint32_t b) {
+    float r;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ floatx4 mfma16x16x32(half8_t a, half8_t b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -133,6 +142,9 @@ __device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint3
 __device__ __forceinline__ half8_t buf_load_h8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+__device__ __forceinline__ u32x4 buf_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
 
 // Device-scope (cache policy SC1) 16-byte store and load: coherent across
 // the XCDs of the device without whole-L2 maintenance.
@@ -147,6 +159,49 @@ __device__ __forceinline__ floatx4 buf_load_f4_device(__amdgpu_buffer_rsrc_t r, 
 // memory operation of this wave, stores included, has completed.
 __device__ __forceinline__ void wait_vm_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Split-K finish in one atomic per output element.
+//
+// Each output element owns a 64-bit slot in the workspace, zero between
+// calls.  Every workgroup that holds a partial sum p of the element adds
+//     (fixed(p) << 8) + 1,   fixed(p) = round(p * 2^24) as a signed integer,
+// to the slot with one agent-scope atomic that returns the old value.  The
+// low byte counts arrivals and the upper 56 bits sum the partials in 24-bit
+// fixed point.  The workgroup whose return shows split_k arrivals holds the
+// complete sum in the returned value: it writes the fp16 output and stores
+// zero back into the slot.  Integer addition is exact and associative, so
+// the result does not depend on arrival order (bitwise deterministic), and
+// there is no separate counter, no wait for store acknowledgements and no
+// reload of partials: one memory round trip after the last partial.
+//
+// Range: partials are clamped to +-2^22 (far beyond fp16's 65504, which
+// saturates to +-inf on conversion; NaN is treated as +2^22 and so becomes
+// +inf), so that the sum of up to 255 partials stays inside the 56-bit field.
+// A partial with |p| >= 0.5 converts exactly; smaller ones round to 2^-24.
+constexpr int kFixMaxSplit = 255;
+// The word a workgroup adds for its partial p.
+__device__ __forceinline__ unsigned long long fixed_point_word(float p) {
+    const float clamp = 4194304.0f;  // 2^22
+    const float c = p == p ? fminf(fmaxf(p, -clamp), clamp) : clamp;
+    const long long f = (long long)rintf(c * 16777216.0f);
+    return ((unsigned long long)f << 8) + 1ull;
+}
+// `now` = the slot's value after this workgroup's add (returned old value
+// plus its word): the last of split_k arrivals writes the output and clears
+// the slot.
+__device__ __forceinline__ void fixed_point_complete(unsigned long long now, unsigned long long* slot, half_t* out,
+                                                     int split_k) {
+    if ((int)(now & 0xFFull) == split_k) {
+        const long long s = (long long)now >> 8;
+        *out = (half_t)((float)s * (1.0f / 16777216.0f));
+        __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+__device__ __forceinline__ void fixed_add_finish(float p, unsigned long long* slot, half_t* out, int split_k) {
+    const unsigned long long v = fixed_point_word(p);
+    const unsigned long long old = __hip_atomic_fetch_add(slot, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    fixed_point_complete(old + v, slot, out, split_k);
+}
+
 // Last-arriving workgroup of a split-K output range: for rows row0 ..
 // row0+nrows and columns col0 .. col0+ncols,
 // out[m, n] = fp16(sum over split of partials[split, m, n]) (partials of
@@ -160,6 +215,9 @@ __device__ __forceinline__ void wait_vm_stores() { __builtin_amdgcn_s_waitcnt(0x
 //    parameter so that callers that never have many outputs keep their
 //    register footprint).
 // Either way each element is summed in a fixed order, independent of timing.
+// The partials read are overwritten with zeros, so that the whole workspace
+// is zero again when the kernel ends (the fixed-point finish above relies on
+// zero slots, and both share the workspace).
 // `fin` holds blockDim.x float4.  Must be called by the whole workgroup.
 template <int U>
 __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t* __restrict__ out, int M, int N,
@@ -191,6 +249,8 @@ __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t*
             const uint32_t off = item_off(item, m, n);
 #pragma unroll 8
             for (int q = part; q < split_k; q += P) s += buf_load_f4_device(rp, off + (uint32_t)q * stride);
+#pragma unroll 8
+            for (int q = part; q < split_k; q += P) buf_store_f4_device(floatx4{0.f, 0.f, 0.f, 0.f}, rp, off + (uint32_t)q * stride);
         }
         if (P > 1) {
             if (valid) fin[t] = s;
@@ -216,6 +276,12 @@ __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t*
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (base + u * nt + t < items) s[u] += buf_load_f4_device(rp, off[u] + (uint32_t)q * stride);
+        }
+        for (int q = 0; q < split_k; ++q) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (base + u * nt + t < items)
+                    buf_store_f4_device(floatx4{0.f, 0.f, 0.f, 0.f}, rp, off[u] + (uint32_t)q * stride);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)

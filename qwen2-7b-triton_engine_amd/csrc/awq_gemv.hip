@@ -490,6 +490,269 @@ __global__ __launch_bounds__(1024) void awq_gemv_col_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Variant 4: quad-column GEMV, interleaved 32-row chunks, fixed-point split-K.
+//
+// Lane l: c4 = l % 16 owns packed columns 4*c4 .. 4*c4+3 of the workgroup's
+// 64-column strip (32 outputs) and reads them with one 16-byte load per row,
+// so the 16 lanes of a row cover one 256-byte row segment; rq = l / 16 picks
+// rows 4*rq .. 4*rq+3 of each 16-row half of a 32-row chunk (one load
+// instruction = four row segments, eight per chunk).
+//
+// Work split: the K/32 chunks of a strip are divided evenly among split_k
+// workgroups (the planner keeps split_k * strips within one workgroup per
+// CU: a CU holding two workgroups of this kernel finishes last); inside a
+// workgroup the waves take every nw-th chunk, so at any time they read
+// adjacent rows (measured faster than giving each wave a contiguous range).
+// A chunk lies inside one 128-row group.
+//
+// Prologue: the workgroup turns the zeros and scales of the groups it
+// touches into fp32 pairs (s', s' * (1024 + z')) per column -- s' and z'
+// carry the x16 of columns 2, 3, 6, 7 -- and stages them and its rows of x
+// in LDS.  The main loop's only vector memory operations are then the weight
+// loads: the next chunk's eight loads are in flight while one chunk is
+// computed, every load is issued (chunks past the wave's range get an
+// out-of-range offset, so the compiler's wait counts stay static), and
+// scheduling barriers keep a chunk's arithmetic after the loads issued
+// before it.
+//
+// Arithmetic: sum_r x[r] * (1024 + q) per column by v_dot2_f32_f16 on the
+// magic-number codes (x16 for columns 2, 3, 6, 7) and sum_r x[r]; after each
+// chunk  acc += s' * sum - s'(1024 + z') * sum_x.  At the end the four row
+// slots of a column quad are added with cross-lane shuffles, the waves
+// through LDS, and each output's partial is stored (split_k == 1) or goes
+// through fixed_add_finish.  Needs N % 32 == 0 (whole quads).
+constexpr int kQuadItemsPerThread = 4;  // prologue loads per thread (consts and x each)
+
+template <int MR>
+__global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int split_k, unsigned long long* fix) {
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    const int c4 = lane & 15;
+    const int rq = lane >> 4;
+    const int pn = a.N >> 3;
+    const int n_strips = (pn + 63) / 64;
+    const int strip = blockIdx.x % n_strips;
+    const int split = blockIdx.x / n_strips;
+    const int jl = min(strip * 64 + 4 * c4, pn - 4);  // in-range quad; lanes past pn drop their results
+    const int C = a.K / 32;
+    const int c0 = (int)((int64_t)C * split / split_k);
+    const int c1 = (int)((int64_t)C * (split + 1) / split_k);
+    const int nc = c1 - c0;
+    const int g_lo = c0 / 4;
+    const int n_g = nc > 0 ? (c1 - 1) / 4 - g_lo + 1 : 0;
+    const int groups = a.K / kGroup;
+
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.qzeros, (uint32_t)((size_t)groups * pn * 4));
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, (uint32_t)((size_t)groups * a.N * 2));
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
+    const uint32_t row_bytes = (uint32_t)pn * 4u;
+    const uint32_t voff_w = (uint32_t)(4 * rq) * row_bytes + (uint32_t)jl * 4u;
+
+    // LDS: consts float4 [n_g][16][16] ((s', s'(1024+z')) of two columns, indexed
+    // [group][column pair i][lane quad c4]: one wave-wide read is 256
+    // consecutive bytes), then x [MR][nc * 32] fp16.
+    floatx4* lc = reinterpret_cast<floatx4*>(lds);
+    half_t* lx = reinterpret_cast<half_t*>(lds + n_g * 16 * 16 * 4);
+
+    // Prologue loads: item (g, j) = zero word and 8 scales of packed column j
+    // of group g_lo + g; x in 16-byte pieces.  Issued before the weights.
+    const int nt = blockDim.x;
+    u32x4 sv[kQuadItemsPerThread];
+    uint32_t zv[kQuadItemsPerThread];
+    u32x4 xv[kQuadItemsPerThread];
+    auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+#pragma unroll
+    for (int i = 0; i < kQuadItemsPerThread; ++i) {
+        const int item = min((int)threadIdx.x + i * nt, max(n_g * 64 - 1, 0));
+        const int g = g_lo + item / 64;
+        const int j = min(strip * 64 + item % 64, pn - 1);
+        zv[i] = buf_load_b32(rz, (uint32_t)(g * pn + j) * 4u, 0u);
+        sv[i] = buf_load_u4(rs, (uint32_t)(((size_t)g * a.N + 8 * j) * 2), 0u);
+        const int xi = (int)threadIdx.x + i * nt;  // x piece: row m, 8 rows at c0*32 + 8 * (xi % (nc * 4))
+        const int m = xi / max(nc * 4, 1);
+        const uint32_t xoff = (uint32_t)(((size_t)m * a.K + (size_t)c0 * 32 + 8 * (xi % max(nc * 4, 1))) * 2);
+        xv[i] = buf_load_u4(rx, m < MR ? xoff : 0x80000000u, 0u);
+    }
+
+    struct Chunk {
+        u32x4 w[8];
+    };
+    // Chunk c (rows 32c .. 32c+31); chunks past the wave's range read zeros.
+    auto load_chunk = [&](int c, Chunk& ck) {
+        const bool live = c < c1;
+        const uint32_t oob = live ? 0u : 0x80000000u;
+        const uint32_t r0 = live ? (uint32_t)c * 32u : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            ck.w[u] = buf_load_u4(rw, voff_w + oob, (r0 + (u & 3) + 16 * (u >> 2)) * row_bytes);
+    };
+    Chunk A, B;
+    fence();
+    load_chunk(c0 + wave, A);
+    fence();
+    load_chunk(c0 + wave + nw, B);
+    fence();
+
+#pragma unroll
+    for (int i = 0; i < kQuadItemsPerThread; ++i) {
+        const int item = (int)threadIdx.x + i * nt;
+        if (item < n_g * 64) {
+            const int g = item / 64;
+            const int j = item % 64;  // packed column of the strip: lane quad j / 4, columns 8 (j % 4) + c
+            const half8_t s8 = __builtin_bit_cast(half8_t, sv[i]);
+#pragma unroll
+            for (int c = 0; c < 8; c += 2) {
+                floatx4 v;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int cc = c + h;
+                    const uint32_t z = (zv[i] >> col_shift(cc)) & 0xFu;
+                    const float sc = (float)s8[cc] * (x16_column(cc) ? 0.0625f : 1.0f);
+                    const float zz = 1024.f + (float)(x16_column(cc) ? 16u * z : z);
+                    v[2 * h] = sc;
+                    v[2 * h + 1] = sc * zz;
+                }
+                const int col = 8 * (j % 4) + c;  // column of the lane quad: pair index col / 2
+                lc[(g * 16 + col / 2) * 16 + j / 4] = v;
+            }
+        }
+        if (item < MR * nc * 4) *reinterpret_cast<u32x4*>(lx + 8 * item) = xv[i];
+    }
+    __syncthreads();
+
+    float acc[MR][32], in[MR][32], sx[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc[m][i] = 0.f;
+    const uint32_t ones = 0x3C003C00u;  // fp16 (1, 1)
+
+    // The first row pair of a chunk starts each sum from zero without a
+    // register clear (dot2_from_zero), and the fold is two fused
+    // multiply-adds per column.
+    auto compute = [&](const Chunk& ck, int c) {
+        const int cl = c - c0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            u32x2 xq[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                xq[m] = *reinterpret_cast<const u32x2*>(lx + (size_t)m * nc * 32 + cl * 32 + 16 * h + 4 * rq);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const bool first = h == 0 && i == 0;
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+                    sx[m] = first ? dot2_from_zero(xq[m][i], ones)
+                                  : __builtin_amdgcn_fdot2(as_h2(xq[m][i]), as_h2(ones), sx[m], false);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    uint32_t kp[8];
+                    kpairs_magic_x16(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp);
+#pragma unroll
+                    for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+                        for (int m = 0; m < MR; ++m)
+                            in[m][8 * p + cc] = first ? dot2_from_zero(kp[cc], xq[m][i])
+                                                      : __builtin_amdgcn_fdot2(as_h2(kp[cc]), as_h2(xq[m][i]),
+                                                                               in[m][8 * p + cc], false);
+                }
+            }
+        }
+        const int gi = c / 4 - g_lo;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const floatx4 v = lc[(gi * 16 + i) * 16 + c4];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                acc[m][2 * i] = __builtin_fmaf(-v[1], sx[m], __builtin_fmaf(v[0], in[m][2 * i], acc[m][2 * i]));
+                acc[m][2 * i + 1] =
+                    __builtin_fmaf(-v[3], sx[m], __builtin_fmaf(v[2], in[m][2 * i + 1], acc[m][2 * i + 1]));
+            }
+        }
+    };
+
+    // A holds chunk c, B chunk c + nw at the top of each iteration.
+    for (int c = c0 + wave; c < c1; c += 2 * nw) {
+        fence();
+        compute(A, c);
+        fence();
+        load_chunk(c + 2 * nw, A);
+        fence();
+        if (c + nw < c1) compute(B, c + nw);
+        fence();
+        load_chunk(c + 3 * nw, B);
+        fence();
+    }
+
+    // Row slots rq = 0..3 of a column quad sit in lanes l, l^16, l^32, l^48.
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            float v = acc[m][i];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[m][i] = v;
+        }
+    __syncthreads();  // every wave is done with the staged consts: the LDS becomes the reduction buffer
+    float* red = reinterpret_cast<float*>(lds);
+    if (rq == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int i = 0; i < 32; i += 4)
+                *reinterpret_cast<floatx4*>(&red[(wave * MR + m) * 512 + 32 * c4 + i]) =
+                    floatx4{acc[m][i], acc[m][i + 1], acc[m][i + 2], acc[m][i + 3]};
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 512; t += blockDim.x) {
+        const int col = strip * 512 + t;
+        if (col >= a.N) break;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            if (m >= a.M) break;
+            float sum = 0.f;
+            for (int w = 0; w < nw; ++w) sum += red[(w * MR + m) * 512 + t];
+            half_t* o = a.out + (size_t)m * a.N + col;
+            if (split_k == 1) *o = (half_t)sum;
+            else fixed_add_finish(sum, fix + (size_t)m * a.N + col, o, split_k);
+        }
+    }
+}
+
+// Groups a workgroup's chunk range can touch: at most ceil(per / 4) + 1.
+int64_t gemv_quad_max_groups(int K, int split_k) {
+    const int64_t C = K / 32;
+    const int64_t per = (C + split_k - 1) / split_k;
+    return (per + 2) / 4 + 1;
+}
+
+// LDS of the column-quad GEMV: staged consts (4 KiB per group) and x rows,
+// or the cross-wave reduction buffer, whichever is larger.
+size_t gemv_quad_lds_bytes(int M, int K, int split_k, int k_waves) {
+    const int64_t C = K / 32;
+    const int64_t per = (C + split_k - 1) / split_k;
+    const int mr = M <= 1 ? 1 : 2;
+    const size_t staged = (size_t)gemv_quad_max_groups(K, split_k) * 4096 + (size_t)mr * per * 64;
+    const size_t red = (size_t)k_waves * mr * 512 * 4;
+    return staged > red ? staged : red;
+}
+
+// Whether the prologue's fixed number of loads per thread covers the shape.
+bool gemv_quad_fits(int M, int K, int split_k, int k_waves) {
+    const int64_t C = K / 32;
+    const int64_t per = (C + split_k - 1) / split_k;
+    const int64_t threads = 64 * (int64_t)k_waves;
+    const int mr = M <= 1 ? 1 : 2;
+    return gemv_quad_max_groups(K, split_k) * 64 <= kQuadItemsPerThread * threads &&
+           mr * per * 4 <= kQuadItemsPerThread * threads;
+}
+
 int64_t gemv_col_blocks(int N, int P) {
     const int64_t strips = ((N >> 3) + P - 1) / P;
     const int64_t spl = P >= 32 ? 1 : 32 / P;
@@ -527,7 +790,19 @@ static hipError_t gemv_col_launch(const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <int MR>
+static hipError_t gemv_quad_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
+                                   hipStream_t stream) {
+    unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
+    const size_t lds = gemv_quad_lds_bytes(a.M, a.K, cfg.split_k, cfg.kw_count);
+    hipLaunchKernelGGL((awq_gemv_quad_kernel<MR>), dim3((unsigned)(gemv_strips(a.N) * cfg.split_k)),
+                       dim3(64 * cfg.kw_count), lds, stream, a, cfg.split_k, fix);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream) {
+    if (cfg.variant == 4) return a.M <= 1 ? gemv_quad_launch<1>(a, cfg, counters, stream)
+                                          : gemv_quad_launch<2>(a, cfg, counters, stream);
     if (cfg.variant == 3) {
         const int key3 = (a.M <= 1 ? 1 : 2) * 1000 + cfg.rows_per_wave * 10 + cfg.depth;
         switch (key3) {

@@ -29,7 +29,8 @@ struct SkinnyConfig {
 };
 
 struct GemvConfig {
-    int variant;             // 1: all loads at once; 2: K-streaming, one group per chunk
+    int variant;             // 1: all loads at once; 2: K-streaming, one group per chunk;
+                             // 4: column quads, fixed-point split-K finish
     int rows_per_wave;       // K rows per wave: 16, 32 or 64 (variant 2: 16 or 32)
     int kw_count;            // waves per workgroup along K: 1, 2, 4 or 8 (variant 2: 128 / rows_per_wave)
     int split_k;             // workgroups along K
@@ -64,10 +65,21 @@ int64_t skinny_blocks(int N, int K, int rows_per_wave, int kw_count);
 size_t skinny_counter_bytes();
 
 // Same workspace contract as launch_skinny (counters, then partials).
+// Variant 4: the workspace after the counter block holds M * N zeroed 64-bit
+// fixed-point slots (left zero on return) instead of partials.
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream);
 int64_t gemv_strips(int N);
+size_t gemv_quad_lds_bytes(int M, int K, int split_k, int k_waves);
+int64_t gemv_quad_max_groups(int K, int split_k);
+bool gemv_quad_fits(int M, int K, int split_k, int k_waves);
 int64_t gemv_col_blocks(int N, int P);
 int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
+
+// Stream path (M <= 16, N % 32 == 0): the workspace after the counter block
+// holds M * N zeroed 64-bit fixed-point slots (left zero on return).
+hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, uint32_t* counters, hipStream_t stream);
+size_t stream_lds_bytes(int M, int K, int split_k, int k_waves);
+bool stream_fits(int K, int split_k, int k_waves);
 
 // Same workspace contract as launch_skinny; one arrival counter per 512-column strip.
 hipError_t launch_narrow(const GemmArgs& a, const NarrowConfig& cfg, uint32_t* counters, hipStream_t stream);

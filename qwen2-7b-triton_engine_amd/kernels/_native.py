@@ -28,7 +28,9 @@ PATH_SKINNY = 1
 PATH_TILE = 2
 PATH_GEMV = 3
 PATH_NARROW = 4
-PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile", PATH_GEMV: "gemv", PATH_NARROW: "narrow"}
+PATH_STREAM = 5
+PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile", PATH_GEMV: "gemv", PATH_NARROW: "narrow",
+              PATH_STREAM: "stream"}
 
 
 class Plan(ctypes.Structure):
@@ -72,6 +74,7 @@ SIGNATURES = {
     "awq_w4a16_plan_tile": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_plan_narrow": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
                                              ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_stream": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
     "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
     "awq_w4a16_validate": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
@@ -142,7 +145,7 @@ def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, varian
 def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant: int = 1, split_k: int = 0,
               depth: int | None = None, tile_n: int = 512, group_size: int = 128) -> Plan:
     if depth is None:
-        depth = 0 if variant == 1 else 2
+        depth = 0 if variant in (1, 4) else 2
     p = Plan()
     check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, variant, tile_n, rows_per_wave, k_waves, split_k, depth,
                                     ctypes.byref(p)), "awq_w4a16_plan_gemv")
@@ -153,10 +156,18 @@ def plan_narrow(M: int, N: int, K: int, rows_per_wave: int, split_k: int, depth:
                 factored_scale: int | None = None, group_size: int = 128) -> Plan:
     """Narrow-M path (M <= 16): GEMV schedule, 4x4x4 MFMA arithmetic."""
     if factored_scale is None:
-        factored_scale = 1 if M <= 8 else 0
+        factored_scale = 0
     p = Plan()
     check(lib().awq_w4a16_plan_narrow(M, N, K, group_size, rows_per_wave, split_k, depth, factored_scale,
                                       ctypes.byref(p)), "awq_w4a16_plan_narrow")
+    return p
+
+
+def plan_stream(M: int, N: int, K: int, k_waves: int, split_k: int, group_size: int = 128) -> Plan:
+    """Stream path (M <= 16): column quads, 16x16x32 MFMA, fixed-point split-K."""
+    p = Plan()
+    check(lib().awq_w4a16_plan_stream(M, N, K, group_size, k_waves, split_k, ctypes.byref(p)),
+          "awq_w4a16_plan_stream")
     return p
 
 

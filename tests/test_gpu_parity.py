@@ -43,10 +43,12 @@ def _assert_close(y, y_ref, what):
     return err
 
 
-def _paths_for(m):
+def _paths_for(m, n=None):
     paths = [_native.PATH_TILE]
     if m <= 64:
         paths.insert(0, _native.PATH_SKINNY)
+    if m <= 16 and (n is None or n % 32 == 0):
+        paths.insert(0, _native.PATH_STREAM)
     if m <= 2:
         paths.insert(0, _native.PATH_GEMV)
     return paths
@@ -98,7 +100,7 @@ def test_dequant_edge_scales_bit_exact(gpu):
 def test_gemm_small(gpu, m, k, n):
     x, qw, qz, s = O.make_inputs(m, k, n, seed=m * 7 + n)
     y_ref = C.gemm_f64(x, qw, qz, s)
-    for path in [None] + _paths_for(m):
+    for path in [None] + _paths_for(m, n):
         print(f"gemm small M={m} K={k} N={n} path={path}", flush=True)
         y = _run(gpu, x, qw, qz, s, path=path)
         _assert_close(y, y_ref, f"M={m} K={k} N={n} path={path}")
@@ -113,7 +115,7 @@ def test_one_hot_bit_exact(gpu):
         rows = np.random.default_rng(m).integers(0, k, size=m)
         x = np.zeros((m, k), dtype=np.float16)
         x[np.arange(m), rows] = 1.0
-        for path in _paths_for(m):
+        for path in _paths_for(m, n):
             print(f"one-hot M={m} path={path}", flush=True)
             y = _run(gpu, x, qw, qz, s, path=path)
             assert np.array_equal(y.view(np.uint16), w[rows].view(np.uint16)), f"M={m} path={path}"
@@ -132,7 +134,7 @@ def test_integer_exact(gpu):
         x = rng.integers(-2, 3, size=(m, k)).astype(np.float16)
         want = x.astype(np.int64) @ q.astype(np.int64)
         assert np.abs(want).max() < 2048
-        for path in _paths_for(m):
+        for path in _paths_for(m, n):
             y = _run(gpu, x, qw, qz, s, path=path)
             assert np.array_equal(y.astype(np.int64), want), f"M={m} path={path}"
 
@@ -150,7 +152,8 @@ def test_gemm_decode_shapes(gpu, name, m):
     k, n = _SHAPES[name]
     x, qw, qz, s = O.make_inputs(m, k, n, seed=0)
     y_ref = x.astype(np.float64) @ O.dequant_awq_f32eval(qw, qz, s).astype(np.float64)
-    for path in (None, _native.PATH_SKINNY) + ((_native.PATH_GEMV,) if m <= 2 else ()):
+    for path in ((None, _native.PATH_SKINNY) + ((_native.PATH_STREAM,) if m <= 16 else ()) +
+                 ((_native.PATH_GEMV,) if m <= 2 else ())):
         print(f"decode {name} M={m} path={path}", flush=True)
         y = _run(gpu, x, qw, qz, s, path=path)
         _assert_close(y, y_ref, f"{name} M={m} path={path}")
@@ -163,7 +166,7 @@ def test_gemm_down_m_sweep(gpu, m):
     rows = np.arange(m) if m <= 64 else np.random.default_rng(m).choice(m, size=64, replace=False)
     w = O.dequant_awq_f32eval(qw, qz, s).astype(np.float32)
     y_ref = x[rows].astype(np.float32) @ w
-    for path in [None] + _paths_for(m):
+    for path in [None] + _paths_for(m, n):
         print(f"down M={m} path={path}", flush=True)
         y = _run(gpu, x, qw, qz, s, path=path)
         _assert_close(y[rows], y_ref, f"down M={m} path={path}")
@@ -258,20 +261,88 @@ def test_tile_plans_agree(gpu, m, k, n):
         _assert_close(y, y_ref, f"tile M={m} v={variant} split={sk}")
 
 
-def test_split_k_counters_left_zero(gpu):
-    """The in-kernel split-K reduction resets its arrival counters, so the
-    shared workspace is ready for the next call (and for graph replays)."""
+@pytest.mark.parametrize("m", [1, 2])
+def test_gemv_quad_plans_agree(gpu, m):
+    """Column-quad GEMV (balanced K split, fixed-point split-K finish): split
+    counts from 1 up to one 16-row step per workgroup, every wave count, on
+    an N whose last 512-column strip holds a single quad."""
+    k, n = 3584, 1056
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=24)
+    y_ref = O.awq_gemm_oracle(x, qw, qz, s)
+    tried = 0
+    for split in (1, 2, 3, 5, 16, 37, 100, 112):
+        for kw in (1, 2, 3, 4, 8):
+            try:
+                p = _native.plan_gemv(m, n, k, 0, kw, variant=4, split_k=split)
+            except _native.AwqNativeError:
+                continue  # too many groups per workgroup for this wave count
+            print(f"gemv quad plan M={m} split={split} k_waves={kw}", flush=True)
+            y = _run(gpu, x, qw, qz, s, plan_obj=p)
+            _assert_close(y, y_ref, f"gemv quad M={m} split={split} kw={kw}")
+            tried += 1
+    assert tried >= 24
+
+
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 9, 16])
+def test_stream_plans_agree(gpu, m):
+    """Stream path (column quads, 16x16x32 MFMA, fixed-point split-K): split
+    counts from 1 up to one 32-row chunk per workgroup, every wave count, on
+    an N whose last 512-column strip holds a single quad."""
+    k, n = 3584, 1056
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=25 + m)
+    y_ref = O.awq_gemm_oracle(x, qw, qz, s)
+    tried = 0
+    for split in (1, 2, 3, 5, 16, 37, 100, 112):
+        for kw in (1, 2, 3, 4):
+            try:
+                p = _native.plan_stream(m, n, k, kw, split)
+            except _native.AwqNativeError:
+                continue  # too many groups per workgroup for this wave count
+            print(f"stream plan M={m} split={split} k_waves={kw}", flush=True)
+            y = _run(gpu, x, qw, qz, s, plan_obj=p)
+            _assert_close(y, y_ref, f"stream M={m} split={split} kw={kw}")
+            tried += 1
+    assert tried >= 20
+
+
+def test_stream_and_quad_one_hot_bit_exact(gpu):
+    """One-hot rows of x reproduce the dequantised rows bit for bit through the
+    stream kernel (the reference's fp16 weight into the MFMA) and the
+    column-quad GEMV, with and without split-K (the fixed-point finish is exact
+    for every fp16 value)."""
+    k, n = 512, 288
+    _, qw, qz, s = O.make_inputs(1, k, n, seed=33)
+    w = O.dequant_awq(qw, qz, s)
+    for m in (1, 2, 4, 16):
+        rows = np.random.default_rng(m).integers(0, k, size=m)
+        x = np.zeros((m, k), dtype=np.float16)
+        x[np.arange(m), rows] = 1.0
+        plans = [_native.plan_stream(m, n, k, 4, sp) for sp in (1, 3, 16)]
+        if m <= 2:
+            plans += [_native.plan_gemv(m, n, k, 0, 4, variant=4, split_k=sp) for sp in (1, 3, 16)]
+        for p in plans:
+            print(f"one-hot M={m} path={_native.PATH_NAMES[p.path]} split={p.split_k}", flush=True)
+            y = _run(gpu, x, qw, qz, s, plan_obj=p)
+            assert np.array_equal(y.view(np.uint16), w[rows].view(np.uint16)), (m, p.path, p.split_k)
+
+
+def test_split_k_workspace_left_zero(gpu):
+    """Every split-K finish leaves the whole shared workspace zero (arrival
+    counters reset, partials and fixed-point slots cleared), so it is ready
+    for the next call of any path and for graph replays."""
     from kernels import awq_gemm as G
     k, n = 3584, 4608
-    x, qw, qz, s = O.make_inputs(1, k, n, seed=6)
-    p = _native.plan_for(1, n, k)
-    assert p.split_k > 1
-    y = _run(gpu, x, qw, qz, s)
-    ws = G._workspaces[gpu.index][-1]
-    cnt = ws[: _native.counter_bytes() // 4].view(torch.int32)
-    assert int(cnt.abs().sum().item()) == 0
-    y2 = _run(gpu, x, qw, qz, s)
-    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
+    for m, path in ((1, _native.PATH_GEMV), (4, _native.PATH_SKINNY), (1, _native.PATH_NARROW),
+                    (100, _native.PATH_TILE), (16, _native.PATH_STREAM), (3, _native.PATH_STREAM)):
+        x, qw, qz, s = O.make_inputs(m, k, n, seed=6)
+        p = _native.plan_for(m, n, k, path=path)
+        assert p.split_k > 1, (m, path)
+        print(f"workspace check M={m} path={_native.PATH_NAMES[path]} split={p.split_k}", flush=True)
+        y = _run(gpu, x, qw, qz, s, path=path)
+        ws = G._workspaces[gpu.index][-1]
+        assert int((ws.view(torch.int32) != 0).sum().item()) == 0, _native.PATH_NAMES[path]
+        y2 = _run(gpu, x, qw, qz, s, path=path)
+        assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
 
 
 def test_deterministic(gpu):
@@ -386,7 +457,7 @@ def test_golden_small_gemm_every_path(gpu):
     qw, qz = d["qweight"], d["qzeros"]
     s = d["scales_f16_bits"].view(np.float16)
     for m in (1, 2, 5):
-        for path in _paths_for(m):
+        for path in _paths_for(m, s.shape[1]):
             print(f"golden gemm M={m} path={_native.PATH_NAMES[path]}", flush=True)
             y = _run(gpu, x[:m], qw, qz, s, path=path)
             _assert_close(y, d["y_f64"][:m], f"golden M={m} path={path}")
@@ -416,7 +487,7 @@ def test_golden_edge_gemm_finite_columns(gpu):
         tol = 1.1 * 2.0 ** -10 * mag + 2.0 ** -23
         big = np.abs(y_ref) > 65600.0
         small = np.abs(y_ref) < 65400.0
-        for path in _paths_for(m):
+        for path in _paths_for(m, s.shape[1]):
             print(f"golden edge gemm M={m} path={_native.PATH_NAMES[path]}", flush=True)
             y = _run(gpu, x[:m], qw, qz, s, path=path)[:, keep].astype(np.float64)
             assert np.all(np.isinf(y[big]) & (np.sign(y[big]) == np.sign(y_ref[big]))), f"M={m} path={path}"

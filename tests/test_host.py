@@ -88,7 +88,12 @@ def test_auto_plan_invariants(L, m, k, n):
         assert p.path == _native.PATH_TILE
     assert p.grid > 0 and p.block_threads % 64 == 0 and p.block_threads <= 1024
     if p.split_k > 1:
-        assert p.workspace_bytes == _native.counter_bytes() + p.split_k * m * n * 4
+        if p.path == _native.PATH_GEMV and p.variant == 4:
+            # one 64-bit fixed-point slot per output element
+            assert p.workspace_bytes == _native.counter_bytes() + m * n * 8
+            assert p.split_k <= 255
+        else:
+            assert p.workspace_bytes == _native.counter_bytes() + p.split_k * m * n * 4
     else:
         assert p.workspace_bytes == 0
     assert _native.workspace_bytes(m, n, k) == p.workspace_bytes
