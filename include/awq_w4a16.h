@@ -107,8 +107,10 @@ int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 
 /* Host-only: a GEMV-path plan (M <= 2) with explicit tuning values.
- * variant 4 (column quads, N % 32 == 0): tile_n 512; rows_per_wave 0 and
- * depth 0; k_waves 1 .. 8 wavefronts, which take every k_waves-th 32-row
+ * variant 4 (column quads, N % 32 == 0; variant 5: the same with the column
+ * sums on v_mfma_f32_16x16x32_f16): tile_n 512; rows_per_wave 0; depth 2
+ * .. 4 chunk buffers per wavefront (depth - 1 chunks of loads in flight
+ * while one is computed); k_waves 1 .. 8 wavefronts, which take every k_waves-th 32-row
  * chunk of the workgroup's share of K; split_k 1 .. min(K/32, 255) workgroups
  * share each strip's K evenly; split-K partials meet in 64-bit fixed-point
  * workspace slots.
@@ -129,12 +131,13 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
  * column strip's K/32 chunks of 32 rows are divided evenly among split_k
  * workgroups (1 .. min(K/32, 255)) of k_waves wavefronts (1 .. 4), which
  * take every k_waves-th chunk; v_mfma_f32_16x16x32_f16 on the reference's
- * exact fp16 weight; split-K partials meet in 64-bit fixed-point workspace
- * slots.  Same column-quad lane layout and work split as GEMV variant 4.
- * No reference counterpart beyond the decode dispatch it serves
- * (kernels/awq_gemm.py:251-282). */
-int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t k_waves,
-                          int32_t split_k, awq_w4a16_plan* plan);
+ * exact fp16 weight.  Split-K finish: variant 1, 64-bit fixed-point
+ * workspace slots (one atomic per output element per workgroup); variant 2,
+ * fp32 partials and the last-arriving workgroup adds them.  Same
+ * column-quad lane layout and work split as GEMV variant 4.  No reference
+ * counterpart beyond the decode dispatch it serves (kernels/awq_gemm.py:251-282). */
+int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant,
+                          int32_t k_waves, int32_t split_k, awq_w4a16_plan* plan);
 /* Host-only: a narrow-M plan (M <= 16): the K-streaming schedule of GEMV
  * variant 2 with v_mfma_f32_4x4x4_16b_f16 arithmetic.  rows_per_wave 16 or
  * 32 (128 / rows_per_wave waves per workgroup); split_k in 1 .. K/128 with

@@ -151,17 +151,20 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
         return AWQ_OK;
     }
     if (tile_n != 512) return AWQ_ERR_PATH;
-    if (variant == 4) {
-        // Column quads: N % 32 == 0; rows_per_wave 0 and depth 0 (each
+    if (variant == 4 || variant == 5) {
+        // Column quads (5: MFMA column sums): N % 32 == 0; rows_per_wave 0;
+        // depth 2 .. 4 chunk buffers per wave (each
         // strip's K/32 chunks are divided evenly over split_k workgroups of
         // k_waves waves); split_k <= min(K/32, kFixMaxSplit); the groups and
         // x rows a workgroup stages must fit its prologue loads, and the
         // staged data its LDS.
-        if (N % 32 != 0 || rows_per_wave != 0 || depth != 0) return AWQ_ERR_PATH;
+        if (N % 32 != 0 || rows_per_wave != 0 || depth < 2 || depth > 4) return AWQ_ERR_PATH;
+        if (variant == 4 && M > 1 && depth > 3) return AWQ_ERR_PATH;  // that instance would spill registers
         if (k_waves < 1 || k_waves > 8 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
             return AWQ_ERR_PATH;
         if (!gemv_quad_fits((int)M, (int)K, (int)split_k, (int)k_waves)) return AWQ_ERR_PATH;
         p->split_k = (int32_t)split_k;
+        p->depth = (int32_t)depth;
         p->grid = gemv_strips((int)N) * split_k;
         p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
         p->lds_bytes = gemv_quad_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves);
@@ -224,7 +227,7 @@ int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
         else if (split < C && split < kFixMaxSplit) ++split;
         else break;
     }
-    return fill_gemv(M, N, K, 4, 512, 0, w, split, 0, p);
+    return fill_gemv(M, N, K, 5, 512, 0, w, split, 2, p);
 }
 
 int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
@@ -286,13 +289,16 @@ int narrow_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
 constexpr int64_t kStreamMaxM = 16;
 constexpr uint64_t kStreamLdsBudget = 160 * 1024;
 
-int fill_stream(int64_t M, int64_t N, int64_t K, int64_t k_waves, int64_t split_k, awq_w4a16_plan* p) {
-    if (M > kStreamMaxM || N % 32 != 0) return AWQ_ERR_PATH;
+// variant 1: fixed-point split-K finish; 2: fp32 partials and a last-arriving workgroup.
+int fill_stream(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t k_waves, int64_t split_k,
+                awq_w4a16_plan* p) {
+    if (M > kStreamMaxM || N % 32 != 0 || (variant != 1 && variant != 2)) return AWQ_ERR_PATH;
+    if (variant == 2 && split_k > 1 && gemv_strips((int)N) * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
     if (k_waves < 1 || k_waves > 4 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
         return AWQ_ERR_PATH;
     if (!stream_fits((int)K, (int)split_k, (int)k_waves)) return AWQ_ERR_PATH;
     p->path = AWQ_PATH_STREAM;
-    p->variant = 1;
+    p->variant = (int32_t)variant;
     p->tile_m = 16;
     p->tile_n = 512;
     p->rows_per_wave = 0;
@@ -302,7 +308,8 @@ int fill_stream(int64_t M, int64_t N, int64_t K, int64_t k_waves, int64_t split_
     p->factored_scale = 0;
     p->depth = 0;
     p->grid = gemv_strips((int)N) * split_k;
-    p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
+    p->workspace_bytes = split_k <= 1 ? 0u
+                         : kCounterBytes + (uint64_t)M * (uint64_t)N * (variant == 1 ? 8u : 4u * (uint64_t)split_k);
     p->lds_bytes = stream_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves);
     if (p->lds_bytes > kStreamLdsBudget) return AWQ_ERR_PATH;
     if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
@@ -328,7 +335,7 @@ int stream_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
         else if (split < C && split < kFixMaxSplit) ++split;
         else break;
     }
-    return fill_stream(M, N, K, w, split, p);
+    return fill_stream(M, N, K, M <= 2 ? 1 : 2, w, split, p);
 }
 
 int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k, awq_w4a16_plan* p) {
@@ -402,7 +409,7 @@ int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
         const int st = fill_narrow(M, N, K, p->rows_per_wave, p->split_k, p->depth, p->factored_scale, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_STREAM) {
-        const int st = fill_stream(M, N, K, p->k_waves, p->split_k, &q);
+        const int st = fill_stream(M, N, K, p->variant, p->k_waves, p->split_k, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_GEMV) {
         const int st = fill_gemv(M, N, K, p->variant, p->tile_n, p->rows_per_wave, p->k_waves,
@@ -457,7 +464,10 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
                                    : nullptr;
         e = launch_skinny(a, cfg, counters, s);
     } else if (p.path == AWQ_PATH_STREAM) {
-        e = launch_stream(a, p.split_k, p.k_waves, static_cast<uint32_t*>(workspace), s);
+        a.partials = p.variant == 2 && p.split_k > 1
+                         ? reinterpret_cast<float*>(static_cast<char*>(workspace) + skinny_counter_bytes())
+                         : nullptr;
+        e = launch_stream(a, p.split_k, p.k_waves, p.variant == 2, static_cast<uint32_t*>(workspace), s);
     } else if (p.path == AWQ_PATH_NARROW) {
         NarrowConfig cfg;
         cfg.rows_per_wave = p.rows_per_wave;
@@ -547,12 +557,12 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
     return fill_gemv(M, N, K, variant, tile_n, rows_per_wave, k_waves, split_k, depth, plan);
 }
 
-int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t k_waves, int32_t split_k,
-                          awq_w4a16_plan* plan) {
+int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant, int32_t k_waves,
+                          int32_t split_k, awq_w4a16_plan* plan) {
     if (!plan) return AWQ_ERR_NULL_POINTER;
     const int d = check_dims(M, N, K, group_size);
     if (d != AWQ_OK) return d;
-    return fill_stream(M, N, K, k_waves, split_k, plan);
+    return fill_stream(M, N, K, variant, k_waves, split_k, plan);
 }
 
 int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,

@@ -510,8 +510,8 @@ __global__ __launch_bounds__(1024) void awq_gemv_col_kernel(GemmArgs a) {
 // touches into fp32 pairs (s', s' * (1024 + z')) per column -- s' and z'
 // carry the x16 of columns 2, 3, 6, 7 -- and stages them and its rows of x
 // in LDS.  The main loop's only vector memory operations are then the weight
-// loads: the next chunk's eight loads are in flight while one chunk is
-// computed, every load is issued (chunks past the wave's range get an
+// loads: a ring of D chunk buffers keeps D - 1 chunks' loads in flight while
+// one chunk is computed, every load is issued (chunks past the wave's range get an
 // out-of-range offset, so the compiler's wait counts stay static), and
 // scheduling barriers keep a chunk's arithmetic after the loads issued
 // before it.
@@ -524,7 +524,15 @@ __global__ __launch_bounds__(1024) void awq_gemv_col_kernel(GemmArgs a) {
 // through fixed_add_finish.  Needs N % 32 == 0 (whole quads).
 constexpr int kQuadItemsPerThread = 4;  // prologue loads per thread (consts and x each)
 
-template <int MR>
+// MM (variant 5): the column sums of a chunk come from v_mfma_f32_16x16x32_f16
+// instead of v_dot2: the magic-number k-pairs of a lane's 8 rows of one column
+// are its B fragment as they are (lane n = c4, k-block = rq: the MFMA
+// operand layout), x rows m = c4 < M supply A in the same k order, and an
+// MFMA against ones gives sum_r x[r]; the MFMA sums the 32 rows inside the
+// chunk, so lane (c4, rq = 0) holds row m of its 32 columns in register m
+// and no cross-lane reduction is needed.  The fold per chunk touches the M
+// live rows only.
+template <int MR, bool MM, int D>
 __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int split_k, unsigned long long* fix) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int lane = threadIdx.x & 63;
@@ -590,11 +598,15 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         for (int u = 0; u < 8; ++u)
             ck.w[u] = buf_load_u4(rw, voff_w + oob, (r0 + (u & 3) + 16 * (u >> 2)) * row_bytes);
     };
-    Chunk A, B;
-    fence();
-    load_chunk(c0 + wave, A);
-    fence();
-    load_chunk(c0 + wave + nw, B);
+    // Ring of D chunk buffers: the wave's chunks i = 0, 1, ... (chunk c0 + wave
+    // + i * nw) go to buffer i % D; chunk i + D is loaded right after chunk i
+    // is computed, so D - 1 chunks are in flight during each computation.
+    Chunk ring[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        fence();
+        load_chunk(c0 + wave + d * nw, ring[d]);
+    }
     fence();
 
 #pragma unroll
@@ -631,10 +643,51 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         for (int i = 0; i < 32; ++i) acc[m][i] = 0.f;
     const uint32_t ones = 0x3C003C00u;  // fp16 (1, 1)
 
+    // MFMA form: A = x rows (zero for lanes c4 >= M), S = row sums of x.
+    auto compute_mfma = [&](const Chunk& ck, int c) {
+        const int cl = c - c0;
+        u32x4 av = {0u, 0u, 0u, 0u};
+        if (c4 < MR) {
+            const u32x2 lo = *reinterpret_cast<const u32x2*>(lx + (size_t)c4 * nc * 32 + cl * 32 + 4 * rq);
+            const u32x2 hi = *reinterpret_cast<const u32x2*>(lx + (size_t)c4 * nc * 32 + cl * 32 + 16 + 4 * rq);
+            av = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+        const half8_t xa = __builtin_bit_cast(half8_t, av);
+        const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
+        const floatx4 S = mfma16x16x32(xa, __builtin_bit_cast(half8_t, u32x4{ones, ones, ones, ones}), zero4);
+        const int gi = c / 4 - g_lo;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            uint32_t kp[4][8];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) kpairs_magic_x16(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp[2 * h + i]);
+#pragma unroll
+            for (int cc = 0; cc < 8; cc += 2) {
+                const floatx4 v = lc[(gi * 16 + (8 * p + cc) / 2) * 16 + c4];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int col = 8 * p + cc + e;
+                    const floatx4 Cv = mfma16x16x32(
+                        xa, __builtin_bit_cast(half8_t, u32x4{kp[0][cc + e], kp[1][cc + e], kp[2][cc + e], kp[3][cc + e]}),
+                        zero4);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m)
+                        acc[m][col] = __builtin_fmaf(-v[2 * e + 1], S[m], __builtin_fmaf(v[2 * e], Cv[m], acc[m][col]));
+                }
+            }
+        }
+    };
+
     // The first row pair of a chunk starts each sum from zero without a
     // register clear (dot2_from_zero), and the fold is two fused
     // multiply-adds per column.
     auto compute = [&](const Chunk& ck, int c) {
+        if constexpr (MM) {
+            compute_mfma(ck, c);
+            return;
+        }
         const int cl = c - c0;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -676,29 +729,30 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         }
     };
 
-    // A holds chunk c, B chunk c + nw at the top of each iteration.
-    for (int c = c0 + wave; c < c1; c += 2 * nw) {
-        fence();
-        compute(A, c);
-        fence();
-        load_chunk(c + 2 * nw, A);
-        fence();
-        if (c + nw < c1) compute(B, c + nw);
-        fence();
-        load_chunk(c + 3 * nw, B);
+    for (int c = c0 + wave; c < c1; c += D * nw) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            fence();
+            if (c + d * nw < c1) compute(ring[d], c + d * nw);
+            fence();
+            load_chunk(c + (d + D) * nw, ring[d]);
+        }
         fence();
     }
 
-    // Row slots rq = 0..3 of a column quad sit in lanes l, l^16, l^32, l^48.
+    // Row slots rq = 0..3 of a column quad sit in lanes l, l^16, l^32, l^48
+    // (the MFMA form has already summed them).
+    if constexpr (!MM) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+        for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            float v = acc[m][i];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            acc[m][i] = v;
-        }
+            for (int i = 0; i < 32; ++i) {
+                float v = acc[m][i];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                acc[m][i] = v;
+            }
+    }
     __syncthreads();  // every wave is done with the staged consts: the LDS becomes the reduction buffer
     float* red = reinterpret_cast<float*>(lds);
     if (rq == 0) {
@@ -790,19 +844,33 @@ static hipError_t gemv_col_launch(const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int MR>
+template <int MR, bool MM, int D>
 static hipError_t gemv_quad_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
                                    hipStream_t stream) {
     unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
     const size_t lds = gemv_quad_lds_bytes(a.M, a.K, cfg.split_k, cfg.kw_count);
-    hipLaunchKernelGGL((awq_gemv_quad_kernel<MR>), dim3((unsigned)(gemv_strips(a.N) * cfg.split_k)),
+    hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, MM, D>), dim3((unsigned)(gemv_strips(a.N) * cfg.split_k)),
                        dim3(64 * cfg.kw_count), lds, stream, a, cfg.split_k, fix);
     return hipGetLastError();
 }
 
+template <bool MM>
+static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
+                                     hipStream_t stream) {
+    switch ((a.M <= 1 ? 10 : 20) + cfg.depth) {
+        case 12: return gemv_quad_launch<1, MM, 2>(a, cfg, counters, stream);
+        case 13: return gemv_quad_launch<1, MM, 3>(a, cfg, counters, stream);
+        case 14: return gemv_quad_launch<1, MM, 4>(a, cfg, counters, stream);
+        case 22: return gemv_quad_launch<2, MM, 2>(a, cfg, counters, stream);
+        case 23: return gemv_quad_launch<2, MM, 3>(a, cfg, counters, stream);
+        case 24: return gemv_quad_launch<2, MM, 4>(a, cfg, counters, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream) {
-    if (cfg.variant == 4) return a.M <= 1 ? gemv_quad_launch<1>(a, cfg, counters, stream)
-                                          : gemv_quad_launch<2>(a, cfg, counters, stream);
+    if (cfg.variant == 4) return gemv_quad_dispatch<false>(a, cfg, counters, stream);
+    if (cfg.variant == 5) return gemv_quad_dispatch<true>(a, cfg, counters, stream);
     if (cfg.variant == 3) {
         const int key3 = (a.M <= 1 ? 1 : 2) * 1000 + cfg.rows_per_wave * 10 + cfg.depth;
         switch (key3) {

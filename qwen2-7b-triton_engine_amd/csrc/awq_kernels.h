@@ -76,8 +76,10 @@ int64_t gemv_col_blocks(int N, int P);
 int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
 
 // Stream path (M <= 16, N % 32 == 0): the workspace after the counter block
-// holds M * N zeroed 64-bit fixed-point slots (left zero on return).
-hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, uint32_t* counters, hipStream_t stream);
+// holds M * N zeroed 64-bit fixed-point slots, or (partials) fp32 partials
+// [split_k, M, N] as launch_skinny's (both left zero on return).
+hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, bool partials, uint32_t* counters,
+                         hipStream_t stream);
 size_t stream_lds_bytes(int M, int K, int split_k, int k_waves);
 bool stream_fits(int K, int split_k, int k_waves);
 

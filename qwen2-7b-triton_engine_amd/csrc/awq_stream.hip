@@ -23,6 +23,8 @@
 // ((1024 + q') * f - (1024 + z') * f with f = 1 or 1/16, both exact) and one
 // packed multiply by the scale rounds once.  The staged constants are the
 // fp16 splats -(1024 + z') * f and s of every column.
+//
+// Split-K: see PART below.
 #include "awq_kernels.h"
 
 namespace awq {
@@ -32,8 +34,14 @@ constexpr int kStreamItemsPerThread = 4;  // prologue loads per thread
 constexpr uint32_t kSixteenth2 = 0x2C002C00u;  // fp16 pair (1/16, 1/16)
 }  // namespace
 
-template <int MP>  // rows of x covered by the finish: 4, 8 or 16 (>= M)
-__global__ __launch_bounds__(256) void awq_stream_kernel(GemmArgs a, int split_k, unsigned long long* fix) {
+// PART selects the split-K finish: false -- 64-bit fixed-point slots, one
+// atomic per output element per workgroup (one memory round trip; best when
+// M * N * split_k is small); true -- fp32 partials [split, M, N] stored with
+// device-scope stores, an arrival counter per strip, and the last workgroup
+// adds the partials in split order (three round trips, but no per-element
+// atomics, whose device-wide rate falls short at M >= 4).
+template <int MP, bool PART>  // MP: rows of x covered by the finish: 4, 8 or 16 (>= M)
+__global__ __launch_bounds__(256) void awq_stream_kernel(GemmArgs a, int split_k, uint32_t* counters) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -59,6 +67,7 @@ __global__ __launch_bounds__(256) void awq_stream_kernel(GemmArgs a, int split_k
     const uint32_t row_bytes = (uint32_t)pn * 4u;
     const uint32_t voff_w = (uint32_t)(4 * rq) * row_bytes + (uint32_t)jl * 4u;
     const uint32_t voff_x = (uint32_t)((c4 * a.K + 4 * rq) * 2);  // row c4 of x; rows >= M read 0
+    unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
 
     // Staged constants: u32x4 [n_g][16][16], piece i of lane quad c4 holds the
     // splats (nz, s) of its columns 2i and 2i+1 (one wave-wide read = 256
@@ -194,6 +203,43 @@ __global__ __launch_bounds__(256) void awq_stream_kernel(GemmArgs a, int split_k
     }
     __syncthreads();
 
+    if constexpr (PART) {
+        // This workgroup's partial of rows < M, columns of the strip.
+        __shared__ int last_flag;
+        const int ncols = min(512, a.N - strip * 512);
+        const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, part_bytes);
+        if (split_k > 1) {
+            for (int it = threadIdx.x; it < a.M * 128; it += nt) {
+                const int m = it / 128;
+                const int q = it % 128;  // column quad of the strip
+                if (4 * q >= ncols) continue;
+                floatx4 v = {0.f, 0.f, 0.f, 0.f};
+                for (int w = 0; w < nw; ++w) v += *reinterpret_cast<const floatx4*>(&red[(w * MP + m) * 512 + 4 * q]);
+                buf_store_f4_device(v, rp, (uint32_t)((((size_t)split * a.M + m) * a.N + strip * 512 + 4 * q) * 4));
+            }
+            wait_vm_stores();
+            __syncthreads();
+            if (threadIdx.x == 0)
+                last_flag = __hip_atomic_fetch_add(&counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                            (uint32_t)(split_k - 1);
+            __syncthreads();
+            if (!last_flag) return;
+            splitk_finish<4>(rp, a.out, a.M, a.N, 0, a.M, strip * 512, ncols, split_k, reinterpret_cast<floatx4*>(red));
+            if (threadIdx.x == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            for (int it = threadIdx.x; it < a.M * 512; it += nt) {
+                const int m = it / 512;
+                const int col = strip * 512 + it % 512;
+                if (col >= a.N) continue;
+                float sum = 0.f;
+                for (int w = 0; w < nw; ++w) sum += red[(w * MP + m) * 512 + it % 512];
+                a.out[(size_t)m * a.N + col] = (half_t)sum;
+            }
+        }
+        return;
+    }
+
     // Output items (m, column): all atomics of a batch are issued before
     // their returns are examined.
     const int items = min(a.M, MP) * 512;
@@ -253,20 +299,23 @@ bool stream_fits(int K, int split_k, int k_waves) {
     return stream_max_groups(K, split_k) * 64 <= kStreamItemsPerThread * 64 * (int64_t)k_waves;
 }
 
-template <int MP>
+template <int MP, bool PART>
 static hipError_t stream_launch(const GemmArgs& a, int split_k, int k_waves, uint32_t* counters, hipStream_t stream) {
-    unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
     const size_t lds = stream_lds_bytes(a.M, a.K, split_k, k_waves);
-    hipLaunchKernelGGL((awq_stream_kernel<MP>), dim3((unsigned)(gemv_strips(a.N) * split_k)), dim3(64 * k_waves),
-                       lds, stream, a, split_k, fix);
+    hipLaunchKernelGGL((awq_stream_kernel<MP, PART>), dim3((unsigned)(gemv_strips(a.N) * split_k)), dim3(64 * k_waves),
+                       lds, stream, a, split_k, counters);
     return hipGetLastError();
 }
 
-hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, uint32_t* counters, hipStream_t stream) {
-    switch (stream_rows(a.M)) {
-        case 4: return stream_launch<4>(a, split_k, k_waves, counters, stream);
-        case 8: return stream_launch<8>(a, split_k, k_waves, counters, stream);
-        default: return stream_launch<16>(a, split_k, k_waves, counters, stream);
+hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, bool partials, uint32_t* counters,
+                         hipStream_t stream) {
+    switch (stream_rows(a.M) * 2 + (partials ? 1 : 0)) {
+        case 8: return stream_launch<4, false>(a, split_k, k_waves, counters, stream);
+        case 9: return stream_launch<4, true>(a, split_k, k_waves, counters, stream);
+        case 16: return stream_launch<8, false>(a, split_k, k_waves, counters, stream);
+        case 17: return stream_launch<8, true>(a, split_k, k_waves, counters, stream);
+        case 32: return stream_launch<16, false>(a, split_k, k_waves, counters, stream);
+        default: return stream_launch<16, true>(a, split_k, k_waves, counters, stream);
     }
 }
 

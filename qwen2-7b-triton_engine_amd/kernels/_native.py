@@ -74,7 +74,7 @@ SIGNATURES = {
     "awq_w4a16_plan_tile": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_plan_narrow": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
                                              ctypes.POINTER(Plan)]),
-    "awq_w4a16_plan_stream": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_stream": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
     "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
     "awq_w4a16_validate": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
@@ -145,7 +145,7 @@ def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, varian
 def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant: int = 1, split_k: int = 0,
               depth: int | None = None, tile_n: int = 512, group_size: int = 128) -> Plan:
     if depth is None:
-        depth = 0 if variant in (1, 4) else 2
+        depth = 0 if variant == 1 else 2
     p = Plan()
     check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, variant, tile_n, rows_per_wave, k_waves, split_k, depth,
                                     ctypes.byref(p)), "awq_w4a16_plan_gemv")
@@ -163,10 +163,12 @@ def plan_narrow(M: int, N: int, K: int, rows_per_wave: int, split_k: int, depth:
     return p
 
 
-def plan_stream(M: int, N: int, K: int, k_waves: int, split_k: int, group_size: int = 128) -> Plan:
-    """Stream path (M <= 16): column quads, 16x16x32 MFMA, fixed-point split-K."""
+def plan_stream(M: int, N: int, K: int, k_waves: int, split_k: int, variant: int = 1,
+                group_size: int = 128) -> Plan:
+    """Stream path (M <= 16): column quads, 16x16x32 MFMA; split-K finish by
+    fixed-point slots (variant 1) or fp32 partials (variant 2)."""
     p = Plan()
-    check(lib().awq_w4a16_plan_stream(M, N, K, group_size, k_waves, split_k, ctypes.byref(p)),
+    check(lib().awq_w4a16_plan_stream(M, N, K, group_size, variant, k_waves, split_k, ctypes.byref(p)),
           "awq_w4a16_plan_stream")
     return p
 

@@ -270,17 +270,20 @@ def test_gemv_quad_plans_agree(gpu, m):
     x, qw, qz, s = O.make_inputs(m, k, n, seed=24)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)
     tried = 0
-    for split in (1, 2, 3, 5, 16, 37, 100, 112):
-        for kw in (1, 2, 3, 4, 8):
-            try:
-                p = _native.plan_gemv(m, n, k, 0, kw, variant=4, split_k=split)
-            except _native.AwqNativeError:
-                continue  # too many groups per workgroup for this wave count
-            print(f"gemv quad plan M={m} split={split} k_waves={kw}", flush=True)
-            y = _run(gpu, x, qw, qz, s, plan_obj=p)
-            _assert_close(y, y_ref, f"gemv quad M={m} split={split} kw={kw}")
-            tried += 1
-    assert tried >= 24
+    for variant in (4, 5):
+        for split in (1, 2, 3, 5, 16, 37, 100, 112):
+            for kw in (1, 2, 3, 4, 8):
+                for depth in (2, 3, 4):
+                    try:
+                        p = _native.plan_gemv(m, n, k, 0, kw, variant=variant, split_k=split, depth=depth)
+                    except _native.AwqNativeError:
+                        continue  # too many groups per workgroup for this wave count
+                    print(f"gemv quad plan M={m} variant={variant} split={split} k_waves={kw} depth={depth}",
+                          flush=True)
+                    y = _run(gpu, x, qw, qz, s, plan_obj=p)
+                    _assert_close(y, y_ref, f"gemv quad M={m} v={variant} split={split} kw={kw} d={depth}")
+                    tried += 1
+    assert tried >= 120
 
 
 @pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 9, 16])
@@ -292,17 +295,18 @@ def test_stream_plans_agree(gpu, m):
     x, qw, qz, s = O.make_inputs(m, k, n, seed=25 + m)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)
     tried = 0
-    for split in (1, 2, 3, 5, 16, 37, 100, 112):
-        for kw in (1, 2, 3, 4):
-            try:
-                p = _native.plan_stream(m, n, k, kw, split)
-            except _native.AwqNativeError:
-                continue  # too many groups per workgroup for this wave count
-            print(f"stream plan M={m} split={split} k_waves={kw}", flush=True)
-            y = _run(gpu, x, qw, qz, s, plan_obj=p)
-            _assert_close(y, y_ref, f"stream M={m} split={split} kw={kw}")
-            tried += 1
-    assert tried >= 20
+    for variant in (1, 2):
+        for split in (1, 2, 3, 5, 16, 37, 100, 112):
+            for kw in (1, 2, 3, 4):
+                try:
+                    p = _native.plan_stream(m, n, k, kw, split, variant=variant)
+                except _native.AwqNativeError:
+                    continue  # too many groups per workgroup for this wave count
+                print(f"stream plan M={m} variant={variant} split={split} k_waves={kw}", flush=True)
+                y = _run(gpu, x, qw, qz, s, plan_obj=p)
+                _assert_close(y, y_ref, f"stream M={m} v={variant} split={split} kw={kw}")
+                tried += 1
+    assert tried >= 40
 
 
 def test_stream_and_quad_one_hot_bit_exact(gpu):
@@ -317,9 +321,9 @@ def test_stream_and_quad_one_hot_bit_exact(gpu):
         rows = np.random.default_rng(m).integers(0, k, size=m)
         x = np.zeros((m, k), dtype=np.float16)
         x[np.arange(m), rows] = 1.0
-        plans = [_native.plan_stream(m, n, k, 4, sp) for sp in (1, 3, 16)]
+        plans = [_native.plan_stream(m, n, k, 4, sp, variant=v) for v in (1, 2) for sp in (1, 3, 16)]
         if m <= 2:
-            plans += [_native.plan_gemv(m, n, k, 0, 4, variant=4, split_k=sp) for sp in (1, 3, 16)]
+            plans += [_native.plan_gemv(m, n, k, 0, 4, variant=v, split_k=sp) for v in (4, 5) for sp in (1, 3, 16)]
         for p in plans:
             print(f"one-hot M={m} path={_native.PATH_NAMES[p.path]} split={p.split_k}", flush=True)
             y = _run(gpu, x, qw, qz, s, plan_obj=p)

@@ -88,7 +88,7 @@ def test_auto_plan_invariants(L, m, k, n):
         assert p.path == _native.PATH_TILE
     assert p.grid > 0 and p.block_threads % 64 == 0 and p.block_threads <= 1024
     if p.split_k > 1:
-        if p.path == _native.PATH_GEMV and p.variant == 4:
+        if (p.path == _native.PATH_GEMV and p.variant in (4, 5)) or (p.path == _native.PATH_STREAM and p.variant == 1):
             # one 64-bit fixed-point slot per output element
             assert p.workspace_bytes == _native.counter_bytes() + m * n * 8
             assert p.split_k <= 255
