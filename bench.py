@@ -78,6 +78,25 @@ def kernel_family(_native, m, n, k):
     return _native.PATH_NAMES[_native.plan_for(m, n, k).path]
 
 
+# Kernels each path family launches (a stream-path GEMM whose split-K partials
+# are added by a second launch runs awq_splitk_reduce_kernel after the main
+# kernel; both count as that GEMM's launch).
+FAMILY_KERNELS = {
+    "gemv": ("awq_gemv",),
+    "skinny": ("awq_skinny",),
+    "narrow": ("awq_narrow",),
+    "stream": ("awq_stream", "awq_splitk_reduce"),
+    "tile": ("awq_tile",),
+}
+FAMILY_NAMES = {
+    "gemv": "awq_gemv_quad_kernel",
+    "skinny": "awq_skinny_kernel",
+    "narrow": "awq_narrow_kernel",
+    "stream": "awq_stream_row_kernel / awq_stream_kernel (+ awq_splitk_reduce_kernel)",
+    "tile": "awq_tile_kernel",
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,15 +241,18 @@ def main():
     if os.path.exists(traffic_path):
         with open(traffic_path) as f:
             pmc = json.load(f)
-        prefix = {"gemv": "awq_gemv", "skinny": "awq_skinny", "tile": "awq_tile"}[dom]
+        prefixes = FAMILY_KERNELS[dom]
         keys = [(m, name) for m in DECODE_M for name, k, n in ENGINE_SHAPES if kernel_family(_native, m, n, k) == dom]
-        hits = {(e["M"], e["shape"]): e["fetch_bytes"] + e["write_bytes"] for e in pmc["launches"]
-                if e["kernel"].startswith(prefix)}
+        hits = {}
+        for e in pmc["launches"]:
+            if e["kernel"].startswith(prefixes):
+                key = (e["M"], e["shape"])
+                hits[key] = hits.get(key, 0) + e["fetch_bytes"] + e["write_bytes"]
         if keys and all(key in hits for key in keys):
             traffic = round(sum(hits[key] for key in keys) / len(keys))
     result["roofline"] = {
         "bound": "hbm",
-        "kernel": {"gemv": "awq_gemv_kernel", "skinny": "awq_skinny_kernel", "tile": "awq_tile_kernel"}[dom],
+        "kernel": FAMILY_NAMES[dom],
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_BPS / 1e9,
         "unit": "GB/s",

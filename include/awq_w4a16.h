@@ -53,7 +53,7 @@ typedef enum awq_w4a16_path {
     AWQ_PATH_TILE = 2,           /* prefill: LDS-tiled MFMA GEMM                            */
     AWQ_PATH_GEMV = 3,           /* decode: VALU dot2 GEMV (M <= 2)                         */
     AWQ_PATH_NARROW = 4,         /* decode: K-streaming 4x4x4 MFMA kernel (M <= 16)         */
-    AWQ_PATH_STREAM = 5          /* decode: column-quad streaming 16x16x32 MFMA kernel (M <= 16) */
+    AWQ_PATH_STREAM = 5          /* decode: streaming 16x16x32 MFMA kernels (M <= 16)         */
 } awq_w4a16_path;
 
 /* What the dispatcher will launch for a shape (host-side description). */
@@ -128,16 +128,25 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
                         int32_t depth, awq_w4a16_plan* plan);
 
 /* Host-only: a stream-path plan (M <= 16, N % 32 == 0): each 64-packed-
- * column strip's K/32 chunks of 32 rows are divided evenly among split_k
- * workgroups (1 .. min(K/32, 255)) of k_waves wavefronts (1 .. 4), which
- * take every k_waves-th chunk; v_mfma_f32_16x16x32_f16 on the reference's
- * exact fp16 weight.  Split-K finish: variant 1, 64-bit fixed-point
- * workspace slots (one atomic per output element per workgroup); variant 2,
- * fp32 partials and the last-arriving workgroup adds them.  Same
- * column-quad lane layout and work split as GEMV variant 4.  No reference
- * counterpart beyond the decode dispatch it serves (kernels/awq_gemm.py:251-282). */
-int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant,
-                          int32_t k_waves, int32_t split_k, awq_w4a16_plan* plan);
+ * column strip's K/128 groups are divided evenly among split_k workgroups
+ * (1 .. K/128) whose wavefronts take every k_waves-th group;
+ * v_mfma_f32_16x16x32_f16 sums x * (1024 + q) and x per group, zero and
+ * scale fold in once per group in fp32.  rows_per_wave 16: row layout
+ * (M <= 8), every load covers whole 256-byte row segments and the two
+ * column halves share one MFMA through the rows of A; k_waves wavefronts
+ * share every group: k_waves 1, 2, 4 or 8 with depth 2 chunk buffers per
+ * wavefront or 4 or 8 with depth 1.  rows_per_wave 32: half-strip layout (M <= 16),
+ * the two wavefronts of a pair read the two halves of each row segment;
+ * k_waves pairs, 1 .. 4 with depth 2, 1 .. 2 with depth 4 or 6.  Split-K
+ * finish: variant 1, 64-bit fixed-point workspace slots (one atomic per
+ * output element per workgroup; split_k <= 255); variant 2, fp32 partials
+ * added by the last-arriving workgroup of each strip; variant 3, fp32
+ * partials added by a second kernel launch on the same stream.  No
+ * reference counterpart beyond the decode dispatch it serves
+ * (kernels/awq_gemm.py:251-282). */
+int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
+                          int32_t variant, int32_t k_waves, int32_t split_k, int32_t depth,
+                          awq_w4a16_plan* plan);
 /* Host-only: a narrow-M plan (M <= 16): the K-streaming schedule of GEMV
  * variant 2 with v_mfma_f32_4x4x4_16b_f16 arithmetic.  rows_per_wave 16 or
  * 32 (128 / rows_per_wave waves per workgroup); split_k in 1 .. K/128 with

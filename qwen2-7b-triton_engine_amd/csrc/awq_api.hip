@@ -285,57 +285,85 @@ int narrow_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_narrow(M, N, K, 16, stream_split(N, K), 2, 0, p);
 }
 
-// Stream path (M <= 16): column quads, 16x16x32 MFMA, fixed-point split-K.
+// Stream path (M <= 16): 16x16x32 MFMA, zero/scale folded once per 128-row
+// group; row layout (M <= 8, whole 256-byte row segments per load) or
+// half-strip layout (M <= 16).
 constexpr int64_t kStreamMaxM = 16;
-constexpr uint64_t kStreamLdsBudget = 160 * 1024;
+constexpr uint64_t kStreamLdsBudget = 160 * 1024 - 64;
 
-// variant 1: fixed-point split-K finish; 2: fp32 partials and a last-arriving workgroup.
-int fill_stream(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t k_waves, int64_t split_k,
-                awq_w4a16_plan* p) {
-    if (M > kStreamMaxM || N % 32 != 0 || (variant != 1 && variant != 2)) return AWQ_ERR_PATH;
-    if (variant == 2 && split_k > 1 && gemv_strips((int)N) * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
-    if (k_waves < 1 || k_waves > 4 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
+// rows_per_wave: kStreamRowLayout (16) or kStreamHalfLayout (32).  variant 1:
+// fixed-point split-K finish; 2: fp32 partials, last-arriving workgroup per
+// strip; 3: fp32 partials added by a second launch.
+int fill_stream(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t variant, int64_t k_waves,
+                int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
+    if (M > kStreamMaxM || N % 32 != 0 || variant < 1 || variant > 3) return AWQ_ERR_PATH;
+    const bool row = rows_per_wave == kStreamRowLayout;
+    if (!row && rows_per_wave != kStreamHalfLayout) return AWQ_ERR_PATH;
+    if (row && M > 8) return AWQ_ERR_PATH;
+    if (row ? !((depth == 2 && (k_waves == 1 || k_waves == 2 || k_waves == 4 || k_waves == 8)) ||
+                (depth == 1 && (k_waves == 4 || k_waves == 8)))
+            : !((depth == 2 && k_waves <= 4) || ((depth == 4 || depth == 6) && k_waves <= 2)))
         return AWQ_ERR_PATH;
-    if (!stream_fits((int)K, (int)split_k, (int)k_waves)) return AWQ_ERR_PATH;
+    if (variant == 2 && split_k > 1 && gemv_strips((int)N) * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
+    if (variant == 1 && split_k > kFixMaxSplit) return AWQ_ERR_PATH;
+    if (k_waves < 1 || split_k < 1) return AWQ_ERR_PATH;
+    if (!stream_fits((int)M, (int)K, (int)split_k, (int)k_waves, (int)rows_per_wave)) return AWQ_ERR_PATH;
     p->path = AWQ_PATH_STREAM;
     p->variant = (int32_t)variant;
-    p->tile_m = 16;
+    p->tile_m = row ? 8 : 16;
     p->tile_n = 512;
-    p->rows_per_wave = 0;
+    p->rows_per_wave = (int32_t)rows_per_wave;
     p->k_waves = (int32_t)k_waves;
     p->split_k = (int32_t)split_k;
-    p->block_threads = (int32_t)(64 * k_waves);
-    p->factored_scale = 0;
-    p->depth = 0;
+    p->block_threads = (int32_t)stream_threads((int)rows_per_wave, (int)k_waves);
+    p->factored_scale = 1;
+    p->depth = (int32_t)depth;
     p->grid = gemv_strips((int)N) * split_k;
     p->workspace_bytes = split_k <= 1 ? 0u
                          : kCounterBytes + (uint64_t)M * (uint64_t)N * (variant == 1 ? 8u : 4u * (uint64_t)split_k);
-    p->lds_bytes = stream_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves);
+    p->lds_bytes = stream_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves, (int)rows_per_wave);
     if (p->lds_bytes > kStreamLdsBudget) return AWQ_ERR_PATH;
     if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
 }
 
-// Stream plan: as the column-quad GEMV's -- as many K splits as keep the
-// grid within one workgroup per CU, four waves (one per SIMD).
+// Stream plan (measured on the Qwen2-7B shapes): split K into whole groups
+// so that the grid fills the device with one workgroup per CU, keeping at
+// least two groups per workgroup.  M <= 8: row layout, eight waves sharing
+// every group, one chunk buffer; M <= 16: half-strip layout, four wave
+// pairs, two buffers.  Finish: fixed-point atomics for M <= 4 (one atomic
+// per output element and split: cheapest while M * N * split stays a few
+// hundred thousand); above, the last-arriving workgroup of a strip while the
+// partials it reads stay small (M * split <= 32), else a second launch that
+// adds the partials over the whole device.
 int stream_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (M > kStreamMaxM || N % 32 != 0) return AWQ_ERR_PATH;
+    const bool row = M <= 8;
+    const int64_t layout = row ? kStreamRowLayout : kStreamHalfLayout;
+    const int64_t kw = row ? 8 : 4;
+    const int64_t depth = row ? 1 : 2;
     const int64_t strips = gemv_strips((int)N);
-    const int64_t C = K / 32;
+    const int64_t groups = K / kGroup;
     int64_t split = kCUs / strips;
-    if (split > C) split = C;
-    if (split > kFixMaxSplit) split = kFixMaxSplit;
+    if (split > groups / 2) split = groups / 2;
     if (split < 1) split = 1;
-    int64_t w = C / split;
-    if (w > 4) w = 4;
-    if (w < 1) w = 1;
-    while (!stream_fits((int)K, (int)split, (int)w) ||
-           stream_lds_bytes((int)M, (int)K, (int)split, (int)w) > kStreamLdsBudget) {
-        if (w < 4 && stream_lds_bytes((int)M, (int)K, (int)split, (int)(w + 1)) <= kStreamLdsBudget) ++w;
-        else if (split < C && split < kFixMaxSplit) ++split;
-        else break;
-    }
-    return fill_stream(M, N, K, M <= 2 ? 1 : 2, w, split, p);
+    while (split < groups && (!stream_fits((int)M, (int)K, (int)split, (int)kw, (int)layout) ||
+                              stream_lds_bytes((int)M, (int)K, (int)split, (int)kw, (int)layout) > kStreamLdsBudget))
+        ++split;
+    int64_t variant = 1;
+    if (split > 1 && M > 4) variant = M * split <= 32 ? 2 : 3;
+    if (variant == 1 && split > kFixMaxSplit) variant = 3;
+    return fill_stream(M, N, K, layout, variant, kw, split, depth, p);
+}
+
+// AUTO between the stream path and skinny for 2 < M <= 16 (measured on the
+// Qwen2-7B shapes): the stream path for M <= 4 on every shape; above, where
+// the weight is wide (at least 16 strips of 512 columns) or deep (K >= 8192),
+// whose splits keep the partial sums small against the weight stream.
+bool auto_stream(int64_t M, int64_t N, int64_t K) {
+    if (M > kStreamMaxM || N % 32 != 0) return false;
+    if (M <= 4) return true;
+    return gemv_strips((int)N) >= 16 || K >= 8192;
 }
 
 int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k, awq_w4a16_plan* p) {
@@ -409,7 +437,7 @@ int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
         const int st = fill_narrow(M, N, K, p->rows_per_wave, p->split_k, p->depth, p->factored_scale, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_STREAM) {
-        const int st = fill_stream(M, N, K, p->variant, p->k_waves, p->split_k, &q);
+        const int st = fill_stream(M, N, K, p->rows_per_wave, p->variant, p->k_waves, p->split_k, p->depth, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_GEMV) {
         const int st = fill_gemv(M, N, K, p->variant, p->tile_n, p->rows_per_wave, p->k_waves,
@@ -464,10 +492,11 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
                                    : nullptr;
         e = launch_skinny(a, cfg, counters, s);
     } else if (p.path == AWQ_PATH_STREAM) {
-        a.partials = p.variant == 2 && p.split_k > 1
+        a.partials = p.variant >= 2 && p.split_k > 1
                          ? reinterpret_cast<float*>(static_cast<char*>(workspace) + skinny_counter_bytes())
                          : nullptr;
-        e = launch_stream(a, p.split_k, p.k_waves, p.variant == 2, static_cast<uint32_t*>(workspace), s);
+        e = launch_stream(a, p.split_k, p.k_waves, p.depth, p.rows_per_wave, p.variant - 1,
+                          static_cast<uint32_t*>(workspace), s);
     } else if (p.path == AWQ_PATH_NARROW) {
         NarrowConfig cfg;
         cfg.rows_per_wave = p.rows_per_wave;
@@ -557,12 +586,12 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
     return fill_gemv(M, N, K, variant, tile_n, rows_per_wave, k_waves, split_k, depth, plan);
 }
 
-int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant, int32_t k_waves,
-                          int32_t split_k, awq_w4a16_plan* plan) {
+int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
+                          int32_t variant, int32_t k_waves, int32_t split_k, int32_t depth, awq_w4a16_plan* plan) {
     if (!plan) return AWQ_ERR_NULL_POINTER;
     const int d = check_dims(M, N, K, group_size);
     if (d != AWQ_OK) return d;
-    return fill_stream(M, N, K, variant, k_waves, split_k, plan);
+    return fill_stream(M, N, K, rows_per_wave, variant, k_waves, split_k, depth, plan);
 }
 
 int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
@@ -581,6 +610,7 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
     switch (path) {
         case AWQ_PATH_AUTO:
             if (M <= kGemvMaxM) return gemv_plan(M, N, K, plan);
+            if (auto_stream(M, N, K) && stream_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             return auto_skinny(M, N) ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);
         case AWQ_PATH_SKINNY: return skinny_plan(M, N, K, plan);
         case AWQ_PATH_GEMV: return gemv_plan(M, N, K, plan);

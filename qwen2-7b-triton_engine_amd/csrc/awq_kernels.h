@@ -75,13 +75,22 @@ bool gemv_quad_fits(int M, int K, int split_k, int k_waves);
 int64_t gemv_col_blocks(int N, int P);
 int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
 
-// Stream path (M <= 16, N % 32 == 0): the workspace after the counter block
-// holds M * N zeroed 64-bit fixed-point slots, or (partials) fp32 partials
-// [split_k, M, N] as launch_skinny's (both left zero on return).
-hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, bool partials, uint32_t* counters,
-                         hipStream_t stream);
-size_t stream_lds_bytes(int M, int K, int split_k, int k_waves);
-bool stream_fits(int K, int split_k, int k_waves);
+// Stream path (M <= 16, N % 32 == 0, split_k <= K / 128).  layout:
+// kStreamRowLayout (M <= 8; 16-row chunks, k_waves waves) or
+// kStreamHalfLayout (32-row chunks, k_waves wave pairs).  depth: chunk
+// buffers per wave: row layout 2 (k_waves 1, 2, 4 or 8); half layout 2
+// (k_waves <= 4), 4 or 6 (k_waves <= 2).  finish 0: the workspace after the
+// counter block holds M * N zeroed 64-bit fixed-point slots; 1: fp32
+// partials [split_k, M, N] and one arrival counter per strip; 2: fp32
+// partials added by a second kernel launch.  The workspace is left zero on
+// return.
+constexpr int kStreamHalfLayout = 32;  // rows per chunk
+constexpr int kStreamRowLayout = 16;
+hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, int depth, int layout, int finish,
+                         uint32_t* counters, hipStream_t stream);
+size_t stream_lds_bytes(int M, int K, int split_k, int k_waves, int layout);
+bool stream_fits(int M, int K, int split_k, int k_waves, int layout);
+int64_t stream_threads(int layout, int k_waves);
 
 // Same workspace contract as launch_skinny; one arrival counter per 512-column strip.
 hipError_t launch_narrow(const GemmArgs& a, const NarrowConfig& cfg, uint32_t* counters, hipStream_t stream);

@@ -74,7 +74,8 @@ SIGNATURES = {
     "awq_w4a16_plan_tile": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
     "awq_w4a16_plan_narrow": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
                                              ctypes.POINTER(Plan)]),
-    "awq_w4a16_plan_stream": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
+    "awq_w4a16_plan_stream": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32,
+                                              ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
     "awq_w4a16_workspace_bytes_ex": (ctypes.c_size_t, [_I64, _I64, _I64, _I32, _I32]),
     "awq_w4a16_validate": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
@@ -163,12 +164,19 @@ def plan_narrow(M: int, N: int, K: int, rows_per_wave: int, split_k: int, depth:
     return p
 
 
-def plan_stream(M: int, N: int, K: int, k_waves: int, split_k: int, variant: int = 1,
-                group_size: int = 128) -> Plan:
-    """Stream path (M <= 16): column quads, 16x16x32 MFMA; split-K finish by
-    fixed-point slots (variant 1) or fp32 partials (variant 2)."""
+def plan_stream(M: int, N: int, K: int, k_waves: int, split_k: int, variant: int = 1, depth: int = 2,
+                layout: str = "half", group_size: int = 128) -> Plan:
+    """Stream path (M <= 16): 16x16x32 MFMA, zero and scale folded once per
+    group.  ``layout`` "row" (M <= 8: whole 256-byte row segments per load,
+    ``k_waves`` waves sharing every group, 1, 2, 4 or 8 with depth 2 or 4 or
+    8 with depth 1) or "half" (M <= 16: wave pairs on the two halves of each
+    row segment, ``k_waves`` pairs, 1 .. 4 with depth 2, 1 .. 2 with depth 4
+    or 6); split-K finish by fixed-point slots (variant 1), fp32 partials
+    added by the last-arriving workgroup of a strip (2) or by a second launch
+    (3)."""
+    rows = {"row": 16, "half": 32}[layout]
     p = Plan()
-    check(lib().awq_w4a16_plan_stream(M, N, K, group_size, variant, k_waves, split_k, ctypes.byref(p)),
+    check(lib().awq_w4a16_plan_stream(M, N, K, group_size, rows, variant, k_waves, split_k, depth, ctypes.byref(p)),
           "awq_w4a16_plan_stream")
     return p
 

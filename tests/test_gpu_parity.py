@@ -288,32 +288,40 @@ def test_gemv_quad_plans_agree(gpu, m):
 
 @pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 9, 16])
 def test_stream_plans_agree(gpu, m):
-    """Stream path (column quads, 16x16x32 MFMA, fixed-point split-K): split
-    counts from 1 up to one 32-row chunk per workgroup, every wave count, on
-    an N whose last 512-column strip holds a single quad."""
+    """Stream path (16x16x32 MFMA, zero/scale folded per group), both layouts
+    (row: whole row segments per load, M <= 8; half-strip wave pairs): every
+    split-K finish (fixed-point slots, last-arriving workgroup, second reduce
+    launch), split counts from 1 to one group per workgroup, wave counts and
+    ring depths, on an N whose last 512-column strip holds a single packed-
+    column pair of each half."""
     k, n = 3584, 1056
     x, qw, qz, s = O.make_inputs(m, k, n, seed=25 + m)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)
     tried = 0
-    for variant in (1, 2):
-        for split in (1, 2, 3, 5, 16, 37, 100, 112):
-            for kw in (1, 2, 3, 4):
+    shapes = [("half", kw, d) for kw, d in ((1, 2), (2, 2), (3, 2), (4, 2), (1, 4), (2, 4), (1, 6), (2, 6))]
+    if m <= 8:
+        shapes += [("row", kw, 2) for kw in (1, 2, 4, 8)] + [("row", kw, 1) for kw in (4, 8)]
+    for variant in (1, 2, 3):
+        for split in (1, 2, 3, 5, 9, 14, 28):
+            for layout, kw, depth in shapes:
                 try:
-                    p = _native.plan_stream(m, n, k, kw, split, variant=variant)
+                    p = _native.plan_stream(m, n, k, kw, split, variant=variant, depth=depth, layout=layout)
                 except _native.AwqNativeError:
                     continue  # too many groups per workgroup for this wave count
-                print(f"stream plan M={m} variant={variant} split={split} k_waves={kw}", flush=True)
+                what = f"stream M={m} {layout} v={variant} split={split} k_waves={kw} depth={depth}"
+                print(what, flush=True)
                 y = _run(gpu, x, qw, qz, s, plan_obj=p)
-                _assert_close(y, y_ref, f"stream M={m} v={variant} split={split} kw={kw}")
+                _assert_close(y, y_ref, what)
                 tried += 1
-    assert tried >= 40
+    assert tried >= (170 if m <= 8 else 120)
 
 
 def test_stream_and_quad_one_hot_bit_exact(gpu):
     """One-hot rows of x reproduce the dequantised rows bit for bit through the
-    stream kernel (the reference's fp16 weight into the MFMA) and the
-    column-quad GEMV, with and without split-K (the fixed-point finish is exact
-    for every fp16 value)."""
+    stream kernel and the column-quad GEMV, with and without split-K: with one
+    nonzero x the group sums are 1024 + q' and 1, the folded result
+    s' (1024 + q') - s' (1024 + z') = s (q - z) is exact in fp32, and the
+    fixed-point and partial finishes add exact zeros."""
     k, n = 512, 288
     _, qw, qz, s = O.make_inputs(1, k, n, seed=33)
     w = O.dequant_awq(qw, qz, s)
@@ -321,11 +329,15 @@ def test_stream_and_quad_one_hot_bit_exact(gpu):
         rows = np.random.default_rng(m).integers(0, k, size=m)
         x = np.zeros((m, k), dtype=np.float16)
         x[np.arange(m), rows] = 1.0
-        plans = [_native.plan_stream(m, n, k, 4, sp, variant=v) for v in (1, 2) for sp in (1, 3, 16)]
+        plans = [_native.plan_stream(m, n, k, kw, sp, variant=v, depth=d) for v in (1, 2, 3) for sp in (1, 2, 4)
+                 for kw, d in ((1, 2), (4, 2), (2, 4), (2, 6))]
+        if m <= 8:
+            plans += [_native.plan_stream(m, n, k, kw, sp, variant=v, depth=d, layout="row") for v in (1, 2, 3)
+                      for sp in (1, 2, 4) for kw, d in ((1, 2), (8, 2), (4, 2), (8, 1))]
         if m <= 2:
             plans += [_native.plan_gemv(m, n, k, 0, 4, variant=v, split_k=sp) for v in (4, 5) for sp in (1, 3, 16)]
         for p in plans:
-            print(f"one-hot M={m} path={_native.PATH_NAMES[p.path]} split={p.split_k}", flush=True)
+            print(f"one-hot M={m} path={_native.PATH_NAMES[p.path]} v={p.variant} split={p.split_k}", flush=True)
             y = _run(gpu, x, qw, qz, s, plan_obj=p)
             assert np.array_equal(y.view(np.uint16), w[rows].view(np.uint16)), (m, p.path, p.split_k)
 
@@ -336,17 +348,22 @@ def test_split_k_workspace_left_zero(gpu):
     for the next call of any path and for graph replays."""
     from kernels import awq_gemm as G
     k, n = 3584, 4608
-    for m, path in ((1, _native.PATH_GEMV), (4, _native.PATH_SKINNY), (1, _native.PATH_NARROW),
-                    (100, _native.PATH_TILE), (16, _native.PATH_STREAM), (3, _native.PATH_STREAM)):
+    cases = [(m, _native.plan_for(m, n, k, path=path))
+             for m, path in ((1, _native.PATH_GEMV), (4, _native.PATH_SKINNY), (1, _native.PATH_NARROW),
+                             (100, _native.PATH_TILE), (16, _native.PATH_STREAM), (3, _native.PATH_STREAM))]
+    cases += [(m, _native.plan_stream(m, n, k, 4, sp, variant=v)) for m, v, sp in ((2, 1, 28), (4, 2, 8), (16, 2, 2))]
+    cases += [(m, _native.plan_stream(m, n, k, kw, sp, variant=v, layout="row", depth=d))
+              for m, v, sp, kw, d in ((3, 1, 28, 8, 1), (5, 2, 6, 8, 2), (8, 3, 28, 8, 1))]
+    for m, p in cases:
         x, qw, qz, s = O.make_inputs(m, k, n, seed=6)
-        p = _native.plan_for(m, n, k, path=path)
-        assert p.split_k > 1, (m, path)
-        print(f"workspace check M={m} path={_native.PATH_NAMES[path]} split={p.split_k}", flush=True)
-        y = _run(gpu, x, qw, qz, s, path=path)
+        assert p.split_k > 1, (m, p.path)
+        name = f"{_native.PATH_NAMES[p.path]} v={p.variant}"
+        print(f"workspace check M={m} path={name} split={p.split_k}", flush=True)
+        y = _run(gpu, x, qw, qz, s, plan_obj=p)
         ws = G._workspaces[gpu.index][-1]
-        assert int((ws.view(torch.int32) != 0).sum().item()) == 0, _native.PATH_NAMES[path]
-        y2 = _run(gpu, x, qw, qz, s, path=path)
-        assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
+        assert int((ws.view(torch.int32) != 0).sum().item()) == 0, name
+        y2 = _run(gpu, x, qw, qz, s, plan_obj=p)
+        assert np.array_equal(y.view(np.uint16), y2.view(np.uint16)), name
 
 
 def test_deterministic(gpu):

@@ -79,8 +79,14 @@ def test_plan_struct_matches_header():
 def test_auto_plan_invariants(L, m, k, n):
     p = _native.plan_for(m, n, k)
     wide = -(-(-(-n // 128)) // 2) >= 64   # 128-column tile pairs
+    strips = -(-(n // 8) // 64)            # 512-column strips of the stream path
+    stream = n % 32 == 0 and m <= 16 and (m <= 4 or strips >= 16 or k >= 8192)
     if m <= 2:
         assert p.path == _native.PATH_GEMV
+    elif stream:
+        assert p.path == _native.PATH_STREAM
+        assert p.tile_m >= m
+        assert p.split_k <= k // 128
     elif m <= 16 or (m <= 64 and wide):
         assert p.path == _native.PATH_SKINNY
         assert p.tile_m >= m
