@@ -377,8 +377,13 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->factored_scale = 0;
     p->depth = 0;
     p->lds_bytes = 0;
-    if (variant == 3) {
+    if (variant == 3 || variant == 4) {
         p->tile_m = 256;
+        p->block_threads = 512;
+    }
+    if (variant == 5) {
+        p->tile_m = 256;
+        p->tile_n = 256;
         p->block_threads = 512;
     }
     const int64_t tiles = tile_tiles((int)M, (int)N, (int)variant);
@@ -389,15 +394,17 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
         p->workspace_bytes = 0;
         return AWQ_OK;
     }
-    if ((variant != 2 && variant != 3) || split_k < 1) return AWQ_ERR_PATH;
-    // K range per split: a multiple of the 64-row k-step.
-    const int64_t steps = K / 64;
+    if (variant < 2 || variant > 5 || split_k < 1) return AWQ_ERR_PATH;
+    // K range per split: a multiple of the 64-row k-step (variant 5: of the
+    // 128-row group, two k-steps).
+    const int64_t unit = variant == 5 ? 128 : 64;
+    const int64_t steps = K / unit;
     const int64_t per = (steps + split_k - 1) / split_k;
     const int64_t s = (steps + per - 1) / per;
     if (s != split_k) return AWQ_ERR_PATH;
     if (split_k > 1 && tiles * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
     p->split_k = (int32_t)split_k;
-    p->rows_per_wave = (int32_t)(per * 64);  // K rows per split
+    p->rows_per_wave = (int32_t)(per * unit);  // K rows per split
     p->grid = tiles * split_k;
     p->workspace_bytes =
         split_k > 1 ? skinny_counter_bytes() + (uint64_t)split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
@@ -405,11 +412,29 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     return AWQ_OK;
 }
 
-// Variant 3 (its LDS allows one workgroup per CU); split-K only when the tile
-// grid leaves CUs idle: as many splits as fit in one pass over the CUs, at
-// least 8 k-steps per split.
+// Variant 5 (256 x 256 tiles, weights dequantised in registers) where its
+// tiles fill the device (at least 64 of them, split-K up to one pass over
+// the CUs with at least four groups per split); otherwise variant 4 (256 x
+// 128 tiles, dequant through LDS interleaved with the MFMAs), split-K when
+// the tile grid leaves CUs idle: as many splits as fit in one pass over the
+// CUs, at least 8 k-steps per split.  Measured on the Qwen2-7B prefill
+// shapes (gate||up and down at M = 2048, down at M = 512).
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    const int64_t tiles = tile_tiles((int)M, (int)N, 3);
+    const int64_t tiles5 = tile_tiles((int)M, (int)N, 5);
+    if (tiles5 >= 64) {
+        int64_t split = 1;
+        if (tiles5 < kCUs && tiles5 * 4 <= (int64_t)kCounterBytes) {
+            split = kCUs / tiles5;
+            const int64_t max_split = (K / kGroup) / 4;
+            if (split > max_split) split = max_split;
+            if (split < 1) split = 1;
+            const int64_t units = K / kGroup;
+            const int64_t per = (units + split - 1) / split;
+            split = (units + per - 1) / per;
+        }
+        if (fill_tile(M, N, K, 5, split, p) == AWQ_OK) return AWQ_OK;
+    }
+    const int64_t tiles = tile_tiles((int)M, (int)N, 4);
     int64_t split = 1;
     if (tiles < kCUs && tiles * 4 <= (int64_t)kCounterBytes) {
         split = kCUs / tiles;
@@ -420,7 +445,7 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
         const int64_t per = (steps + split - 1) / split;
         split = (steps + per - 1) / per;
     }
-    return fill_tile(M, N, K, 3, split, p);
+    return fill_tile(M, N, K, 4, split, p);
 }
 
 // Checks a caller-supplied plan against the shape: it must be exactly what

@@ -47,7 +47,8 @@ struct NarrowConfig {
 };
 
 struct TileConfig {
-    int variant;             // 1: 128x128x32; 2: 128x128x64, prefetch, XCD order, split-K; 3: 256x128x64, x ring in LDS
+    int variant;             // 1: 128x128x32; 2: 128x128x64, prefetch, XCD order, split-K; 3: 256x128x64, x ring in LDS;
+                             // 4: 3 with interleaved dequant; 5: 256x256x64, register dequant
     int tile_m, tile_n;
     int split_k;             // variant 2: workgroups along K per tile
     int k_per_split;         // variant 2: K rows per split (multiple of 64)

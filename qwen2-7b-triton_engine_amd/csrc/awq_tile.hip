@@ -435,6 +435,11 @@ __device__ __forceinline__ u32x4 raw_rsrc(const void* base, uint32_t num_bytes) 
 }
 }  // namespace
 
+// IL: variant 4 -- the next k-step's dequant (LDS reads issued first, VALU
+// and W^T stores) is interleaved with this k-step's MFMAs by scheduling
+// groups instead of following them, so the 8 waves, which meet at one
+// barrier per k-step, overlap dequant arithmetic with matrix work.
+template <bool IL>
 __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int split_k, int k_per_split,
                                                              uint32_t* counters) {
     __shared__ __attribute__((aligned(16))) half_t Xs[T3_XS][T3_BM * T3_BK];
@@ -566,25 +571,75 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
             issue_raw(min(kt + 3, last), (kt + 3) % T3_RS);
             const half_t* xs = Xs[kt % T3_XS];
             const half_t* wsb = Ws[kt & 1];
+            if constexpr (!IL) {
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                half8_t af[4], bfr[4];
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    half8_t af[4], bfr[4];
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    af[x] = *reinterpret_cast<const half8_t*>(
-                        &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
+                    for (int x = 0; x < 4; ++x)
+                        af[x] = *reinterpret_cast<const half8_t*>(
+                            &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
 #pragma unroll
-                for (int y = 0; y < 4; ++y) {
-                    const int r = 64 * wm + 16 * y + c16;
-                    const int phys = (4 * s2 + kq) ^ (r & 7);
-                    bfr[y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
+                    for (int y = 0; y < 4; ++y) {
+                        const int r = 64 * wm + 16 * y + c16;
+                        const int phys = (4 * s2 + kq) ^ (r & 7);
+                        bfr[y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
+                    }
+#pragma unroll
+                    for (int x = 0; x < 4; ++x)
+#pragma unroll
+                        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
                 }
+                if (kt + 1 < KT) dequant((kt + 1) % T3_RS, (kt + 1) & 1);
+            } else {
+                // Operands of the next k-step's dequant (its stage holds clamped
+                // data on the last step; the W^T buffer it writes is not read
+                // again).
+                const int rs1 = (kt + 1) % T3_RS;
+                const u32x2 wpair =
+                    *reinterpret_cast<const u32x2*>(&Wr[rs1][(rp >> 1) * T3_RAW_BLOCK + 4 * jj + 2 * (rp & 1)]);
+                const uint32_t zw = Zs[rs1][jj];
+                const half8_t s8 = *reinterpret_cast<const half8_t*>(&Zs[rs1][64 + 4 * jj]);
+                half8_t af[2][4], bfr[2][4];
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
+                for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
-                    for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+                    for (int x = 0; x < 4; ++x)
+                        af[s2][x] = *reinterpret_cast<const half8_t*>(
+                            &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
+#pragma unroll
+                    for (int y = 0; y < 4; ++y) {
+                        const int r = 64 * wm + 16 * y + c16;
+                        const int phys = (4 * s2 + kq) ^ (r & 7);
+                        bfr[s2][y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
+                    }
+                }
+                uint32_t kp[8];
+                kpairs_magic(wpair[0], wpair[1], kp);
+                uint32_t wv[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    wv[c] = as_u32((as_h2(kp[c]) - as_h2(zero_splat(zw, c))) * half2_t{s8[c], s8[c]});
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                    for (int x = 0; x < 4; ++x)
+#pragma unroll
+                        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[s2][x], bfr[s2][y], acc[x][y]);
+                half_t* wnext = Ws[(kt + 1) & 1];
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    *reinterpret_cast<uint32_t*>(&wnext[(8 * jj + c) * T3_WPITCH + 2 * rp]) = wok ? wv[c] : 0u;
+                // Order: all LDS reads, then MFMAs each followed by two VALU
+                // instructions of the dequant, the W^T stores last.
+                __builtin_amdgcn_sched_group_barrier(0x100, 19, 0);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);
             }
-            if (kt + 1 < KT) dequant((kt + 1) % T3_RS, (kt + 1) & 1);
             __builtin_amdgcn_s_waitcnt(kWaitVm7);
             __syncthreads();
         }
@@ -634,8 +689,245 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------
+// Variant 5: 256 x 256 tiles (x rows x output columns), BK = 64, eight waves
+// (two per SIMD) of 128 x rows x 64 output columns, weights dequantised
+// straight into MFMA operand registers -- never through LDS.
+//
+// Wave (wm, wn) = (wave >> 2, wave & 3); lane (n16 = l % 16, kb = l / 16)
+// owns packed column jw = n0/8 + 8 wn + (n16 & 7) and the half hh = n16 >> 3
+// of its 8 logical columns, and reads rows k + 32 h + 8 kb .. + 7 of each
+// 32-row half h of a k-step, one dword per row.  v_perm gathers the 8 rows'
+// half-words in pairs; for each of its 4 logical columns c = 4 hh + c' the
+// lane cuts the magic-number k-pairs (1024 + q) and forms (kp - (1024 + z))
+// * s per pair -- exact q - z, one rounding: the reference's fp16 weight --
+// which is the A fragment of v_mfma_f32_16x16x32_f16 for rows i = lane n16:
+// MFMA c' covers output columns 8 (n0/8 + 8 wn + (i & 7)) + 4 (i >> 3) + c'.
+// x goes through LDS (two stages of 256 x 64 fp16, rows XOR-swizzled in
+// 16-byte chunks, stored from registers loaded one k-step ahead) and gives
+// the B fragments, 8 per k-half for the wave's 128 rows: 32 MFMAs per
+// k-half per wave.  Zeros and scales of the lane's columns are loaded once
+// per 128-row group; a split's K range is a whole number of groups.
+constexpr int T5_BM = 256;  // x rows per tile
+constexpr int T5_BN = 256;  // output columns per tile
+constexpr int T5_BK = 64;
+constexpr int T5_GM = 4;    // M tiles per group of the tile order
+
+__global__ __launch_bounds__(512, 1) void awq_tile_kernel_v5(GemmArgs a, int split_k, int k_per_split,
+                                                             uint32_t* counters) {
+    __shared__ __attribute__((aligned(16))) half_t Xs[2][T5_BM * T5_BK];
+    __shared__ int last_flag;
+    floatx4* fin = reinterpret_cast<floatx4*>(&Xs[0][0]);  // split-K finish, after the main loop
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2;
+    const int wn = wave & 3;
+    const int n16 = lane & 15;
+    const int kb = lane >> 4;
+    const int hh = n16 >> 3;
+
+    // ---- work item: XCD-aware grouped tile order (as variants 2 and 3) ----
+    const int m_tiles = (a.M + T5_BM - 1) / T5_BM;
+    const int n_tiles = (a.N + T5_BN - 1) / T5_BN;
+    const int total = (int)gridDim.x;
+    const int xcd = blockIdx.x & 7;
+    const int xi = blockIdx.x >> 3;
+    const int per = (total + 7) >> 3;
+    const int rem = total & 7;
+    const int w = (rem == 0 || xcd < rem) ? xcd * per + xi : rem * per + (xcd - rem) * (per - 1) + xi;
+    const int tile = w / split_k;
+    const int split = w - tile * split_k;
+    const int in_group = T5_GM * n_tiles;
+    const int first_m = (tile / in_group) * T5_GM;
+    const int gm = min(m_tiles - first_m, T5_GM);
+    const int tm = first_m + (tile % in_group) % gm;
+    const int tn = (tile % in_group) / gm;
+    const int m0 = tm * T5_BM;
+    const int n0 = tn * T5_BN;
+    const int pn = a.N >> 3;
+    const int groups = a.K / kGroup;
+    const int k_begin = split * k_per_split;
+    const int k_end = min(a.K, k_begin + k_per_split);
+    const int KT = (k_end - k_begin) / T5_BK;  // even: whole groups
+
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.qzeros, (uint32_t)((size_t)groups * pn * 4));
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, (uint32_t)((size_t)groups * a.N * 2));
+
+    // x pieces: thread t moves 16-byte chunk t % 8 of rows t / 8 + 64 i (i = 0..3).
+    const int xrow0 = tid >> 3;
+    const int xchunk = tid & 7;
+    uint32_t x_voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = xrow0 + 64 * i;
+        x_voff[i] = m0 + r < a.M ? (uint32_t)(((size_t)(m0 + r) * a.K + 8 * xchunk) * 2) : 0x80000000u;
+    }
+    auto load_x = [&](int kt, u32x4 (&xv)[4]) {
+        const uint32_t soff = (uint32_t)(k_begin + kt * T5_BK) * 2u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xv[i] = buf_load_u4(rx, x_voff[i], soff);
+    };
+    auto store_x = [&](const u32x4 (&xv)[4], int stage) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = xrow0 + 64 * i;
+            *reinterpret_cast<u32x4*>(&Xs[stage][r * T5_BK + 8 * (xchunk ^ (r & 7))]) = xv[i];
+        }
+    };
+
+    // Weights: lane's packed column, rows k + 32 h + 8 kb + u.
+    const int jw = (n0 >> 3) + 8 * wn + (n16 & 7);
+    const bool col_ok = jw < pn;
+    const uint32_t w_voff = col_ok ? (uint32_t)((8 * kb * pn + jw) * 4) : 0x80000000u;
+    auto load_w = [&](int kt, uint32_t (&wv)[16]) {
+        const uint32_t r0 = (uint32_t)(k_begin + kt * T5_BK);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                wv[8 * h + u] = buf_load_b32(rw, w_voff, (r0 + 32 * h + u) * (uint32_t)pn * 4u);
+    };
+    // Zero word of the lane's packed column and the scales of its 4 columns.
+    const uint32_t z_voff = col_ok ? (uint32_t)jw * 4u : 0x80000000u;
+    const uint32_t s_voff = col_ok ? (uint32_t)(8 * jw + 4 * hh) * 2u : 0x80000000u;
+    auto load_zs = [&](int g, uint32_t& zw, u32x2& sv) {
+        zw = buf_load_b32(rz, z_voff, (uint32_t)g * (uint32_t)pn * 4u);
+        sv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, s_voff, (uint32_t)g * (uint32_t)a.N * 2u, 0));
+    };
+
+    // v_perm selectors (byte 0x0C reads as zero): byte hh of the low (even
+    // columns) or high (odd columns) half-word of row 2t (bytes 0..3 of the
+    // second source) and row 2t + 1 (bytes 4..7 of the first source).
+    const uint32_t sel_even = hh ? 0x0C050C01u : 0x0C040C00u;
+    const uint32_t sel_odd = hh ? 0x0C070C03u : 0x0C060C02u;
+
+    floatx4 acc[4][8];  // [logical column c' of the lane's half][16-row block of x]
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int f = 0; f < 8; ++f) acc[c][f] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // One k-step: x stage `xs` (already in LDS), weight words wv.  Per k-half
+    // the lane first forms its 4 A fragments (one per logical column), then
+    // streams the 8 B fragments of its x rows from LDS, 4 MFMAs each.
+    auto compute = [&](const uint32_t (&wv)[16], const half_t* xs, const uint32_t (&zsp)[4],
+                       const uint32_t (&ssp)[4]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // Rows (2t, 2t + 1): the lane's half hh of the 8 columns sits in byte
+            // hh of each half-word (nibbles 2 hh, 2 hh + 1); v_perm with a
+            // per-lane selector gathers that byte of the low half-words of both
+            // rows into bytes 0 and 2 (even columns) and of the high half-words
+            // (odd columns); the second nibble is the same value shifted by 4.
+            u32x4 af[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t ev = __builtin_amdgcn_perm(wv[8 * h + 2 * t + 1], wv[8 * h + 2 * t], sel_even);
+                const uint32_t od = __builtin_amdgcn_perm(wv[8 * h + 2 * t + 1], wv[8 * h + 2 * t], sel_odd);
+                const uint32_t src[4] = {ev, od, ev >> 4, od >> 4};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t kp = and_or(src[c], 0x000F000Fu, kMagic2);
+                    af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < 8; ++f) {
+                const int r = 128 * wm + 16 * f + n16;
+                const half8_t bf = *reinterpret_cast<const half8_t*>(&xs[r * T5_BK + 8 * ((4 * h + kb) ^ (r & 7))]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, af[c]), bf, acc[c][f]);
+            }
+        }
+    };
+
+    if (KT > 0) {
+        const int last = KT - 1;
+        u32x4 xv[4];
+        uint32_t wa[16], wb[16];
+        uint32_t zw;
+        u32x2 sv;
+        load_x(0, xv);
+        load_w(0, wa);
+        load_zs(k_begin / kGroup, zw, sv);
+        store_x(xv, 0);
+        __syncthreads();
+        for (int kt = 0; kt < KT; kt += 2) {
+            // This group's splats; then the next group's zeros and scales.
+            uint32_t zsp[4], ssp[4];
+            const half4_t s4 = __builtin_bit_cast(half4_t, sv);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                zsp[c] = zero_splat(zw, 4 * hh + c);
+                ssp[c] = as_u32(half2_t{s4[c], s4[c]});
+            }
+            load_zs(min(k_begin / kGroup + kt / 2 + 1, groups - 1), zw, sv);
+            // step kt: x and weights of step kt + 1 in flight
+            load_x(kt + 1, xv);
+            load_w(kt + 1, wb);
+            compute(wa, Xs[0], zsp, ssp);
+            store_x(xv, 1);
+            __syncthreads();
+            // step kt + 1
+            load_x(min(kt + 2, last), xv);
+            load_w(min(kt + 2, last), wa);
+            compute(wb, Xs[1], zsp, ssp);
+            store_x(xv, 0);
+            __syncthreads();
+        }
+    }
+
+    // acc[c][f] lane value r: out[m0 + 128 wm + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
+    const int pc0 = (n0 >> 3) + 8 * wn + 4 * (kb & 1);
+    const int coff = 4 * (kb >> 1);
+    if (split_k == 1) {
+#pragma unroll
+        for (int f = 0; f < 8; ++f) {
+            const int m = m0 + 128 * wm + 16 * f + n16;
+            if (m >= a.M) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (pc0 + r >= pn) continue;
+                const half4_t h = {(half_t)acc[0][f][r], (half_t)acc[1][f][r], (half_t)acc[2][f][r],
+                                   (half_t)acc[3][f][r]};
+                *reinterpret_cast<half4_t*>(a.out + (size_t)m * a.N + 8 * (pc0 + r) + coff) = h;
+            }
+        }
+        return;
+    }
+
+    const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
+    const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+        const int m = m0 + 128 * wm + 16 * f + n16;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (pc0 + r >= pn) continue;
+            const uint32_t off = (uint32_t)((((size_t)split * a.M + m) * a.N + 8 * (pc0 + r) + coff) * 4);
+            buf_store_f4_device(floatx4{acc[0][f][r], acc[1][f][r], acc[2][f][r], acc[3][f][r]}, rp_, off);
+        }
+    }
+    wait_vm_stores();
+    __syncthreads();
+    if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)(split_k - 1);
+    __syncthreads();
+    if (!last_flag) return;
+    splitk_finish<16>(rp_, a.out, a.M, a.N, m0, min(T5_BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin);
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 int64_t tile_tiles(int M, int N, int variant) {
-    if (variant == 3) return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
+    if (variant == 5) return (int64_t)((M + T5_BM - 1) / T5_BM) * ((N + T5_BN - 1) / T5_BN);
+    if (variant >= 3) return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
     return (int64_t)((M + T2_BM - 1) / T2_BM) * ((N + T2_BN - 1) / T2_BN);
 }
 
@@ -655,10 +947,21 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
                            cfg.k_per_split, counters);
         return hipGetLastError();
     }
-    if (cfg.variant == 3) {
+    if (cfg.variant == 3 || cfg.variant == 4) {
         const int64_t blocks = tile_tiles(a.M, a.N, 3) * cfg.split_k;
         if (blocks == 0) return hipSuccess;
-        hipLaunchKernelGGL(awq_tile_kernel_v3, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
+        if (cfg.variant == 3)
+            hipLaunchKernelGGL(awq_tile_kernel_v3<false>, dim3((unsigned)blocks), dim3(512), 0, stream, a,
+                               cfg.split_k, cfg.k_per_split, counters);
+        else
+            hipLaunchKernelGGL(awq_tile_kernel_v3<true>, dim3((unsigned)blocks), dim3(512), 0, stream, a,
+                               cfg.split_k, cfg.k_per_split, counters);
+        return hipGetLastError();
+    }
+    if (cfg.variant == 5) {
+        const int64_t blocks = tile_tiles(a.M, a.N, 5) * cfg.split_k;
+        if (blocks == 0) return hipSuccess;
+        hipLaunchKernelGGL(awq_tile_kernel_v5, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
                            cfg.k_per_split, counters);
         return hipGetLastError();
     }
