@@ -102,12 +102,14 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
  * 128x128x64 tiles with prefetch; variant 3: 256x128x64 tiles, x streamed
  * into a 3-stage LDS ring by direct loads, weights dequantised once per
  * k-step into an LDS W^T buffer; variant 4: variant 3 with the next k-step's
- * dequant interleaved with this k-step's MFMAs; variant 5: 256x256x64
- * tiles, eight wavefronts of 128 x rows x 64 columns, weights dequantised
- * straight into MFMA operand registers, x through a 2-stage LDS buffer;
- * variants 2..5 take split_k >= 1 workgroups along K, variant 5 in whole
- * 128-row groups).  For variants 2..5 the plan's rows_per_wave holds the K
- * rows per split. */
+ * dequant interleaved with this k-step's MFMAs; variants 5 and 6: 256x256x64
+ * (eight wavefronts, one workgroup per CU) and 128x256x64 (four wavefronts,
+ * two workgroups per CU) tiles, each wavefront 128 x rows x 64 columns,
+ * weights dequantised straight into MFMA operand registers, x, raw weights
+ * and zeros/scales brought by direct global->LDS loads two k-steps ahead
+ * into a 3-stage ring; variants 2..6 take split_k >= 1 workgroups along K,
+ * variants 5 and 6 in whole 128-row groups).  For variants 2..6 the plan's
+ * rows_per_wave holds the K rows per split. */
 int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 

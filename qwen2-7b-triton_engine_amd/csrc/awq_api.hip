@@ -381,10 +381,10 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
         p->tile_m = 256;
         p->block_threads = 512;
     }
-    if (variant == 5) {
-        p->tile_m = 256;
+    if (variant == 5 || variant == 6) {
+        p->tile_m = variant == 5 ? 256 : 128;
         p->tile_n = 256;
-        p->block_threads = 512;
+        p->block_threads = variant == 5 ? 512 : 256;
     }
     const int64_t tiles = tile_tiles((int)M, (int)N, (int)variant);
     if (variant == 1) {
@@ -394,10 +394,10 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
         p->workspace_bytes = 0;
         return AWQ_OK;
     }
-    if (variant < 2 || variant > 5 || split_k < 1) return AWQ_ERR_PATH;
-    // K range per split: a multiple of the 64-row k-step (variant 5: of the
-    // 128-row group, two k-steps).
-    const int64_t unit = variant == 5 ? 128 : 64;
+    if (variant < 2 || variant > 6 || split_k < 1) return AWQ_ERR_PATH;
+    // K range per split: a multiple of the 64-row k-step (variants 5, 6: of
+    // the 128-row group, two k-steps).
+    const int64_t unit = variant >= 5 ? 128 : 64;
     const int64_t steps = K / unit;
     const int64_t per = (steps + split_k - 1) / split_k;
     const int64_t s = (steps + per - 1) / per;
@@ -412,33 +412,30 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     return AWQ_OK;
 }
 
-// Variant 5 (256 x 256 tiles, weights dequantised in registers) where its
-// tiles fill the device (at least 64 of them, split-K up to one pass over
-// the CUs with at least four groups per split); otherwise variant 4 (256 x
-// 128 tiles, dequant through LDS interleaved with the MFMAs), split-K when
-// the tile grid leaves CUs idle: as many splits as fit in one pass over the
-// CUs, at least 8 k-steps per split.  Measured on the Qwen2-7B prefill
-// shapes (gate||up and down at M = 2048, down at M = 512).
+// Variant 6 (128 x 256 tiles, two workgroups per CU) when, with split-K up
+// to one pass over its 2 * kCUs workgroup slots and at least 4096 rows of K
+// per split, it has at least one workgroup per CU; otherwise variant 4
+// (256 x 128 tiles, one workgroup per CU) with split-K filling one pass over
+// the CUs, at least 16 k-steps per split.  Measured on the Qwen2-7B prefill
+// GEMMs (qkv, o, gate||up, down) at M = 256 .. 2048.
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    const int64_t tiles5 = tile_tiles((int)M, (int)N, 5);
-    if (tiles5 >= 64) {
-        int64_t split = 1;
-        if (tiles5 < kCUs && tiles5 * 4 <= (int64_t)kCounterBytes) {
-            split = kCUs / tiles5;
-            const int64_t max_split = (K / kGroup) / 4;
-            if (split > max_split) split = max_split;
-            if (split < 1) split = 1;
-            const int64_t units = K / kGroup;
-            const int64_t per = (units + split - 1) / split;
-            split = (units + per - 1) / per;
-        }
-        if (fill_tile(M, N, K, 5, split, p) == AWQ_OK) return AWQ_OK;
+    const int64_t tiles6 = tile_tiles((int)M, (int)N, 6);
+    int64_t split6 = 1;
+    if (tiles6 > 0 && tiles6 < 2 * kCUs && tiles6 * 4 <= (int64_t)kCounterBytes) {
+        split6 = (2 * kCUs) / tiles6;
+        const int64_t max_split = K / 4096;
+        if (split6 > max_split) split6 = max_split;
+        if (split6 < 1) split6 = 1;
+        const int64_t units = K / kGroup;
+        const int64_t per = (units + split6 - 1) / split6;
+        split6 = (units + per - 1) / per;
     }
+    if (tiles6 * split6 >= kCUs && fill_tile(M, N, K, 6, split6, p) == AWQ_OK) return AWQ_OK;
     const int64_t tiles = tile_tiles((int)M, (int)N, 4);
     int64_t split = 1;
     if (tiles < kCUs && tiles * 4 <= (int64_t)kCounterBytes) {
         split = kCUs / tiles;
-        const int64_t max_split = (K / 64) / 8;
+        const int64_t max_split = (K / 64) / 16;
         if (split > max_split) split = max_split;
         if (split < 1) split = 1;
         const int64_t steps = K / 64;

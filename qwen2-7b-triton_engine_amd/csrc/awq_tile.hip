@@ -690,46 +690,70 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
 }
 
 // ---------------------------------------------------------------------------
-// Variant 5: 256 x 256 tiles (x rows x output columns), BK = 64, eight waves
-// (two per SIMD) of 128 x rows x 64 output columns, weights dequantised
-// straight into MFMA operand registers -- never through LDS.
+// Variants 5 and 6: 256 output columns per tile, each wave 64 columns x 128
+// x rows, weights dequantised straight into MFMA A registers (never written
+// back to LDS), every global load a direct global->LDS load issued two
+// k-steps ahead into a 3-stage ring.  No VGPR holds data in flight and the
+// compiler sees no global load inside the main loop, so nothing waits on a
+// load before the step that consumes it: the kernel waits itself, once per
+// k-step, right before the barrier (vmcnt = the loads issued since).
 //
-// Wave (wm, wn) = (wave >> 2, wave & 3); lane (n16 = l % 16, kb = l / 16)
-// owns packed column jw = n0/8 + 8 wn + (n16 & 7) and the half hh = n16 >> 3
-// of its 8 logical columns, and reads rows k + 32 h + 8 kb .. + 7 of each
-// 32-row half h of a k-step, one dword per row.  v_perm gathers the 8 rows'
-// half-words in pairs; for each of its 4 logical columns c = 4 hh + c' the
-// lane cuts the magic-number k-pairs (1024 + q) and forms (kp - (1024 + z))
-// * s per pair -- exact q - z, one rounding: the reference's fp16 weight --
-// which is the A fragment of v_mfma_f32_16x16x32_f16 for rows i = lane n16:
-// MFMA c' covers output columns 8 (n0/8 + 8 wn + (i & 7)) + 4 (i >> 3) + c'.
-// x goes through LDS (two stages of 256 x 64 fp16, rows XOR-swizzled in
-// 16-byte chunks, stored from registers loaded one k-step ahead) and gives
-// the B fragments, 8 per k-half for the wave's 128 rows: 32 MFMAs per
-// k-half per wave.  Zeros and scales of the lane's columns are loaded once
-// per 128-row group; a split's K range is a whole number of groups.
-constexpr int T5_BM = 256;  // x rows per tile
-constexpr int T5_BN = 256;  // output columns per tile
+// A stage holds one k-step (64 rows):
+//   * x: BM rows of 128 B, 16-byte chunk p of row r holding k-chunk
+//     p ^ (r & 7) (as variant 5); a wave's dwordx4 load writes 8 rows.
+//   * packed weights: 64 rows x 32 packed columns, dword
+//     ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h + 8 kb + 4 ub + u
+//     of column j, so the lane that owns column j and rows 8 kb .. + 7 of
+//     half h reads them as two 16-byte words; one dword load covers 4 rows x
+//     16 columns (64-byte row segments).
+//   * the group's zero words (32 dwords) and scales (256 halves).
+// WM: waves along M -- 2: 256-row tiles, 8 waves, one workgroup per CU;
+// 1: 128-row tiles, 4 waves, two workgroups per CU.
+namespace {
 constexpr int T5_BK = 64;
-constexpr int T5_GM = 4;    // M tiles per group of the tile order
+constexpr int T5_BN = 256;
+constexpr int T5_STAGES = 3;
+constexpr int T5_W_BYTES = 64 * 32 * 4;       // packed weights of one k-step
+constexpr int T5_ZS_BYTES = 768;              // 256 B zero words (128 used) + 512 B scales
+constexpr int T5_GM = 4;
 
-__global__ __launch_bounds__(512, 1) void awq_tile_kernel_v5(GemmArgs a, int split_k, int k_per_split,
-                                                             uint32_t* counters) {
-    __shared__ __attribute__((aligned(16))) half_t Xs[2][T5_BM * T5_BK];
+template <int WM>
+struct T5Layout {
+    static constexpr int BM = 128 * WM;
+    static constexpr int X_BYTES = BM * T5_BK * 2;
+    static constexpr int STAGE = X_BYTES + T5_W_BYTES + T5_ZS_BYTES;
+    static constexpr int THREADS = 256 * WM;
+    static constexpr int WAVES = 4 * WM;
+    static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;   // dwordx4 loads per wave per stage (4)
+    static constexpr int W_LOADS = T5_W_BYTES / 256 / WAVES;  // dword loads per wave per stage
+    // Loads a wave issues per stage, not counting the zero/scale load that
+    // waves 0..2 add (issued first, so a wait that leaves this many
+    // outstanding also covers it).
+    static constexpr int LOADS = X_LOADS + W_LOADS;
+};
+}  // namespace
+
+template <int WM>
+__global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs a, int split_k, int k_per_split,
+                                                                        uint32_t* counters) {
+    using L = T5Layout<WM>;
+    constexpr int BM = L::BM;
+    static_assert(L::LOADS <= 63, "vmcnt holds 6 bits");
+    __shared__ __attribute__((aligned(16))) unsigned char smem[T5_STAGES * L::STAGE];
     __shared__ int last_flag;
-    floatx4* fin = reinterpret_cast<floatx4*>(&Xs[0][0]);  // split-K finish, after the main loop
+    floatx4* fin = reinterpret_cast<floatx4*>(smem);  // split-K finish, after the main loop
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2;
+    const int wm = WM == 2 ? wave >> 2 : 0;
     const int wn = wave & 3;
     const int n16 = lane & 15;
     const int kb = lane >> 4;
     const int hh = n16 >> 3;
 
-    // ---- work item: XCD-aware grouped tile order (as variants 2 and 3) ----
-    const int m_tiles = (a.M + T5_BM - 1) / T5_BM;
+    // ---- work item: XCD-aware grouped tile order (as variants 2 .. 6) ----
+    const int m_tiles = (a.M + BM - 1) / BM;
     const int n_tiles = (a.N + T5_BN - 1) / T5_BN;
     const int total = (int)gridDim.x;
     const int xcd = blockIdx.x & 7;
@@ -744,94 +768,111 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v5(GemmArgs a, int spl
     const int gm = min(m_tiles - first_m, T5_GM);
     const int tm = first_m + (tile % in_group) % gm;
     const int tn = (tile % in_group) / gm;
-    const int m0 = tm * T5_BM;
+    const int m0 = tm * BM;
     const int n0 = tn * T5_BN;
     const int pn = a.N >> 3;
-    const int groups = a.K / kGroup;
     const int k_begin = split * k_per_split;
     const int k_end = min(a.K, k_begin + k_per_split);
     const int KT = (k_end - k_begin) / T5_BK;  // even: whole groups
 
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
-    const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.qzeros, (uint32_t)((size_t)groups * pn * 4));
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, (uint32_t)((size_t)groups * a.N * 2));
+    const u32x4 rx = raw_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
+    const u32x4 rw = raw_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
+    const u32x4 rz = raw_rsrc(a.qzeros, (uint32_t)((size_t)(a.K / kGroup) * pn * 4));
+    const u32x4 rs = raw_rsrc(a.scales, (uint32_t)((size_t)(a.K / kGroup) * a.N * 2));
+    const uint32_t lds0 = lds_addr(smem);
 
-    // x pieces: thread t moves 16-byte chunk t % 8 of rows t / 8 + 64 i (i = 0..3).
-    const int xrow0 = tid >> 3;
-    const int xchunk = tid & 7;
-    uint32_t x_voff[4];
+    // x: load i of wave w writes rows 8 (X_LOADS w + i) .. + 7; lane l brings
+    // row 8 b + l / 8, k-chunk (l % 8) ^ (l / 8) to LDS chunk position l % 8.
+    uint32_t x_voff[L::X_LOADS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = xrow0 + 64 * i;
-        x_voff[i] = m0 + r < a.M ? (uint32_t)(((size_t)(m0 + r) * a.K + 8 * xchunk) * 2) : 0x80000000u;
+    for (int i = 0; i < L::X_LOADS; ++i) {
+        const int r = 8 * (L::X_LOADS * wave + i) + (lane >> 3);
+        const int q = (lane & 7) ^ (lane >> 3);
+        x_voff[i] = m0 + r < a.M ? (uint32_t)(((size_t)(m0 + r) * a.K + 8 * q) * 2) : 0x80000000u;
     }
-    auto load_x = [&](int kt, u32x4 (&xv)[4]) {
-        const uint32_t soff = (uint32_t)(k_begin + kt * T5_BK) * 2u;
+    // Packed weights: load i of wave w fills 64-dword block B = W_LOADS w + i
+    // = ((h * 4 + kb) * 2 + ub) * 2 + jh: lane l brings row 32 h + 8 kb + 4 ub
+    // + l % 4 of packed column 16 jh + l / 4.
+    uint32_t w_voff[L::W_LOADS];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xv[i] = buf_load_u4(rx, x_voff[i], soff);
-    };
-    auto store_x = [&](const u32x4 (&xv)[4], int stage) {
+    for (int i = 0; i < L::W_LOADS; ++i) {
+        const int B = L::W_LOADS * wave + i;
+        const int jh = B & 1, ub = (B >> 1) & 1, bk = (B >> 2) & 3, bh = B >> 4;
+        const int r = 32 * bh + 8 * bk + 4 * ub + (lane & 3);
+        const int jc = (n0 >> 3) + 16 * jh + (lane >> 2);
+        w_voff[i] = jc < pn ? (uint32_t)((r * pn + jc) * 4) : 0x80000000u;
+    }
+    // Zero words (wave 0: lanes 0..31 useful, the rest repeat them into the
+    // padding) and scales (waves 1, 2: 128 columns each).
+    uint32_t zs_voff = 0x80000000u;
+    if (wave == 0) {
+        const int jc = (n0 >> 3) + (lane & 31);
+        zs_voff = jc < pn ? (uint32_t)jc * 4u : 0x80000000u;
+    } else if (wave <= 2) {
+        const int c = n0 + 128 * (wave - 1) + 2 * lane;
+        zs_voff = c < a.N ? (uint32_t)c * 2u : 0x80000000u;
+    }
+
+    auto issue = [&](int kt, int stage) {
+        const uint32_t base = lds0 + (uint32_t)(stage * L::STAGE);
+        const int k0 = k_begin + kt * T5_BK;
+        const int g = k0 / kGroup;
+        if (wave == 0)
+            buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
+                               base + L::X_BYTES + T5_W_BYTES);
+        else if (wave <= 2)
+            buffer_load_lds_x1(rs, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
+                               base + L::X_BYTES + T5_W_BYTES + 256 * wave);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = xrow0 + 64 * i;
-            *reinterpret_cast<u32x4*>(&Xs[stage][r * T5_BK + 8 * (xchunk ^ (r & 7))]) = xv[i];
-        }
+        for (int i = 0; i < L::X_LOADS; ++i)
+            buffer_load_lds_x4(rx, x_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * 2u),
+                               base + 1024u * (uint32_t)(L::X_LOADS * wave + i));
+#pragma unroll
+        for (int i = 0; i < L::W_LOADS; ++i)
+            buffer_load_lds_x1(rw, w_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * (uint32_t)pn * 4u),
+                               base + L::X_BYTES + 256u * (uint32_t)(L::W_LOADS * wave + i));
     };
 
-    // Weights: lane's packed column, rows k + 32 h + 8 kb + u.
-    const int jw = (n0 >> 3) + 8 * wn + (n16 & 7);
-    const bool col_ok = jw < pn;
-    const uint32_t w_voff = col_ok ? (uint32_t)((8 * kb * pn + jw) * 4) : 0x80000000u;
-    auto load_w = [&](int kt, uint32_t (&wv)[16]) {
-        const uint32_t r0 = (uint32_t)(k_begin + kt * T5_BK);
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                wv[8 * h + u] = buf_load_b32(rw, w_voff, (r0 + 32 * h + u) * (uint32_t)pn * 4u);
-    };
-    // Zero word of the lane's packed column and the scales of its 4 columns.
-    const uint32_t z_voff = col_ok ? (uint32_t)jw * 4u : 0x80000000u;
-    const uint32_t s_voff = col_ok ? (uint32_t)(8 * jw + 4 * hh) * 2u : 0x80000000u;
-    auto load_zs = [&](int g, uint32_t& zw, u32x2& sv) {
-        zw = buf_load_b32(rz, z_voff, (uint32_t)g * (uint32_t)pn * 4u);
-        sv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, s_voff, (uint32_t)g * (uint32_t)a.N * 2u, 0));
-    };
-
-    // v_perm selectors (byte 0x0C reads as zero): byte hh of the low (even
-    // columns) or high (odd columns) half-word of row 2t (bytes 0..3 of the
-    // second source) and row 2t + 1 (bytes 4..7 of the first source).
+    // v_perm selectors (byte 0x0C reads as zero), as variant 5.
     const uint32_t sel_even = hh ? 0x0C050C01u : 0x0C040C00u;
     const uint32_t sel_odd = hh ? 0x0C070C03u : 0x0C060C02u;
+    const int jl = 8 * wn + (n16 & 7);  // lane's packed column within the tile
 
-    floatx4 acc[4][8];  // [logical column c' of the lane's half][16-row block of x]
+    floatx4 acc[4][8];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int f = 0; f < 8; ++f) acc[c][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // One k-step: x stage `xs` (already in LDS), weight words wv.  Per k-half
-    // the lane first forms its 4 A fragments (one per logical column), then
-    // streams the 8 B fragments of its x rows from LDS, 4 MFMAs each.
-    auto compute = [&](const uint32_t (&wv)[16], const half_t* xs, const uint32_t (&zsp)[4],
-                       const uint32_t (&ssp)[4]) {
+    // One k-step from stage memory `st`: per k-half, two 16-byte reads give
+    // the lane's 8 weight words, 4 A fragments are formed (second nibble
+    // masked in place: columns 2, 3 carry 16 (q - z) s, scaled back at the
+    // end), then the 8 B fragments of the wave's x rows, 4 MFMAs each.
+    auto compute = [&](const unsigned char* st) {
+        const half_t* xs = reinterpret_cast<const half_t*>(st);
+        const uint32_t* ws = reinterpret_cast<const uint32_t*>(st + L::X_BYTES);
+        const unsigned char* zs = st + L::X_BYTES + T5_W_BYTES;
+        const uint32_t zw = *reinterpret_cast<const uint32_t*>(zs + 4 * jl);
+        const half4_t s4 = *reinterpret_cast<const half4_t*>(zs + 256 + 2 * (8 * jl + 4 * hh));
+        uint32_t zsp[4], ssp[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            zsp[c] = c & 2 ? zero_splat_x16(zw, 4 * hh + c) : zero_splat(zw, 4 * hh + c);
+            ssp[c] = as_u32(half2_t{s4[c], s4[c]});
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            // Rows (2t, 2t + 1): the lane's half hh of the 8 columns sits in byte
-            // hh of each half-word (nibbles 2 hh, 2 hh + 1); v_perm with a
-            // per-lane selector gathers that byte of the low half-words of both
-            // rows into bytes 0 and 2 (even columns) and of the high half-words
-            // (odd columns); the second nibble is the same value shifted by 4.
+            const u32x4 w0 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 0) * 32 + jl) * 4]);
+            const u32x4 w1 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 1) * 32 + jl) * 4]);
+            const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
             u32x4 af[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const uint32_t ev = __builtin_amdgcn_perm(wv[8 * h + 2 * t + 1], wv[8 * h + 2 * t], sel_even);
-                const uint32_t od = __builtin_amdgcn_perm(wv[8 * h + 2 * t + 1], wv[8 * h + 2 * t], sel_odd);
-                const uint32_t src[4] = {ev, od, ev >> 4, od >> 4};
+                const uint32_t ev = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_even);
+                const uint32_t od = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_odd);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const uint32_t kp = and_or(src[c], 0x000F000Fu, kMagic2);
+                    const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, kMagic2);
                     af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
                 }
             }
@@ -847,40 +888,34 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v5(GemmArgs a, int spl
     };
 
     if (KT > 0) {
-        const int last = KT - 1;
-        u32x4 xv[4];
-        uint32_t wa[16], wb[16];
-        uint32_t zw;
-        u32x2 sv;
-        load_x(0, xv);
-        load_w(0, wa);
-        load_zs(k_begin / kGroup, zw, sv);
-        store_x(xv, 0);
+        // Prologue: steps 0 and 1 in flight (KT is even, so >= 2); wait for step 0.
+        issue(0, 0);
+        issue(1, 1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::LOADS) : "memory");
         __syncthreads();
-        for (int kt = 0; kt < KT; kt += 2) {
-            // This group's splats; then the next group's zeros and scales.
-            uint32_t zsp[4], ssp[4];
-            const half4_t s4 = __builtin_bit_cast(half4_t, sv);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                zsp[c] = zero_splat(zw, 4 * hh + c);
-                ssp[c] = as_u32(half2_t{s4[c], s4[c]});
-            }
-            load_zs(min(k_begin / kGroup + kt / 2 + 1, groups - 1), zw, sv);
-            // step kt: x and weights of step kt + 1 in flight
-            load_x(kt + 1, xv);
-            load_w(kt + 1, wb);
-            compute(wa, Xs[0], zsp, ssp);
-            store_x(xv, 1);
+        int stage = 0;
+        for (int kt = 0; kt < KT; ++kt) {
+            const bool ahead = kt + 2 < KT;
+            const int st2 = stage == 0 ? 2 : stage - 1;  // (kt + 2) % 3
+            if (ahead) issue(kt + 2, st2);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(smem + stage * L::STAGE);
+            // Step kt + 1's loads (issued two steps back) must have landed
+            // before the barrier; those of step kt + 2 stay in flight.
+            if (ahead)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::LOADS) : "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            // step kt + 1
-            load_x(min(kt + 2, last), xv);
-            load_w(min(kt + 2, last), wa);
-            compute(wb, Xs[1], zsp, ssp);
-            store_x(xv, 0);
-            __syncthreads();
+            stage = stage == 2 ? 0 : stage + 1;
         }
     }
+
+    // Columns 2, 3 of each half were computed 16 times too large (exact in fp32).
+#pragma unroll
+    for (int c = 2; c < 4; ++c)
+#pragma unroll
+        for (int f = 0; f < 8; ++f) acc[c][f] *= 0.0625f;
 
     // acc[c][f] lane value r: out[m0 + 128 wm + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
     const int pc0 = (n0 >> 3) + 8 * wn + 4 * (kb & 1);
@@ -893,9 +928,9 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v5(GemmArgs a, int spl
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (pc0 + r >= pn) continue;
-                const half4_t h = {(half_t)acc[0][f][r], (half_t)acc[1][f][r], (half_t)acc[2][f][r],
-                                   (half_t)acc[3][f][r]};
-                *reinterpret_cast<half4_t*>(a.out + (size_t)m * a.N + 8 * (pc0 + r) + coff) = h;
+                const half4_t hv = {(half_t)acc[0][f][r], (half_t)acc[1][f][r], (half_t)acc[2][f][r],
+                                    (half_t)acc[3][f][r]};
+                *reinterpret_cast<half4_t*>(a.out + (size_t)m * a.N + 8 * (pc0 + r) + coff) = hv;
             }
         }
         return;
@@ -921,12 +956,13 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v5(GemmArgs a, int spl
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<16>(rp_, a.out, a.M, a.N, m0, min(T5_BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin);
+    splitk_finish<16>(rp_, a.out, a.M, a.N, m0, min(BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin);
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 int64_t tile_tiles(int M, int N, int variant) {
-    if (variant == 5) return (int64_t)((M + T5_BM - 1) / T5_BM) * ((N + T5_BN - 1) / T5_BN);
+    if (variant == 5) return (int64_t)((M + 255) / 256) * ((N + T5_BN - 1) / T5_BN);
+    if (variant == 6) return (int64_t)((M + 127) / 128) * ((N + T5_BN - 1) / T5_BN);
     if (variant >= 3) return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
     return (int64_t)((M + T2_BM - 1) / T2_BM) * ((N + T2_BN - 1) / T2_BN);
 }
@@ -958,11 +994,15 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
                                cfg.split_k, cfg.k_per_split, counters);
         return hipGetLastError();
     }
-    if (cfg.variant == 5) {
-        const int64_t blocks = tile_tiles(a.M, a.N, 5) * cfg.split_k;
+    if (cfg.variant == 5 || cfg.variant == 6) {
+        const int64_t blocks = tile_tiles(a.M, a.N, cfg.variant) * cfg.split_k;
         if (blocks == 0) return hipSuccess;
-        hipLaunchKernelGGL(awq_tile_kernel_v5, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
-                           cfg.k_per_split, counters);
+        if (cfg.variant == 5)
+            hipLaunchKernelGGL(awq_tile_kernel_v5<2>, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
+                               cfg.k_per_split, counters);
+        else
+            hipLaunchKernelGGL(awq_tile_kernel_v5<1>, dim3((unsigned)blocks), dim3(256), 0, stream, a, cfg.split_k,
+                               cfg.k_per_split, counters);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;

@@ -250,7 +250,7 @@ def test_tile_plans_agree(gpu, m, k, n):
     """Every tile variant, and split-K counts from 1 up, give the same result."""
     x, qw, qz, s = O.make_inputs(m, k, n, seed=15)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)
-    plans = [(1, 1)] + [(v, sk) for v in (2, 3, 4, 5) for sk in (1, 2, 3, 5, 8)]
+    plans = [(1, 1)] + [(v, sk) for v in (2, 3, 4, 5, 6) for sk in (1, 2, 3, 5, 8)]
     for variant, sk in plans:
         try:
             p = _native.plan_tile(m, n, k, variant, sk)

@@ -108,9 +108,9 @@ def test_auto_plan_invariants(L, m, k, n):
 @pytest.mark.parametrize("k,n", SHAPES)
 def test_tile_plans_cover_k_exactly(L, k, n):
     """Every split-K plan gives each split a whole number of 64-row k-steps
-    (variant 5: of 128-row groups) and covers K exactly; the tile count fits
+    (variants 5 and 6: of 128-row groups) and covers K exactly; the tile count fits
     the arrival-counter block."""
-    for variant in (2, 3, 4, 5):
+    for variant in (2, 3, 4, 5, 6):
         for split in (1, 2, 3, 4, 5, 8):
             try:
                 p = _native.plan_tile(512, n, k, variant, split)
@@ -118,10 +118,10 @@ def test_tile_plans_cover_k_exactly(L, k, n):
                 assert e.status == _native.AWQ_ERR_PATH
                 continue
             per = p.rows_per_wave
-            assert per % (128 if variant == 5 else 64) == 0
+            assert per % (128 if variant >= 5 else 64) == 0
             assert (split - 1) * per < k <= split * per
-            tm = 256 if variant >= 3 else 128
-            tn = 256 if variant == 5 else 128
+            tm = 256 if 3 <= variant <= 5 else 128
+            tn = 256 if variant >= 5 else 128
             tiles = -(-512 // tm) * -(-n // tn)
             assert p.grid == tiles * split
             if split > 1:
