@@ -12,8 +12,6 @@ namespace {
 
 // Largest M the skinny path serves (4 MFMA blocks of 16 rows).
 constexpr int64_t kSkinnyMaxM = 64;
-// M above which AUTO never picks the skinny kernel.
-constexpr int64_t kAutoSkinnyMaxM = 64;
 // LDS the skinny dispatcher allows one workgroup for its K reduction.
 constexpr uint64_t kSkinnyLdsBudget = 64 * 1024;
 
@@ -106,14 +104,10 @@ int skinny_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_skinny(M, N, K, r, kw, variant, mb == 4 ? 0 : 1, p);
 }
 
-// AUTO between skinny and tile for 16 < M <= 64: the tile kernel's 256-row
-// tiles waste MFMA work at such M but read the weights with far fewer,
-// larger workgroups; it wins for narrow N, the skinny kernel for wide N
-// (measured at M = 32 .. 64 on the Qwen2-7B shapes).
-bool auto_skinny(int64_t M, int64_t N) {
-    if (M <= 16) return true;
-    return M <= kAutoSkinnyMaxM && skinny_pairs((int)N) >= 64;
-}
+// AUTO takes the skinny kernel up to M = 16 (where the stream path does not
+// serve); above, the tile planner's 32- and 64-row tiles are faster on every
+// Qwen2-7B shape (measured at M = 32 and 64).
+bool auto_skinny(int64_t M, int64_t /*N*/) { return M <= 16; }
 
 // Largest M the GEMV path serves.
 constexpr int64_t kGemvMaxM = 2;
@@ -381,8 +375,8 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
         p->tile_m = 256;
         p->block_threads = 512;
     }
-    if (variant == 5 || variant == 6) {
-        p->tile_m = variant == 5 ? 256 : 128;
+    if (variant >= 5 && variant <= kTileVariants) {
+        p->tile_m = tile5_rows((int)variant);
         p->tile_n = 256;
         p->block_threads = variant == 5 ? 512 : 256;
     }
@@ -394,8 +388,8 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
         p->workspace_bytes = 0;
         return AWQ_OK;
     }
-    if (variant < 2 || variant > 6 || split_k < 1) return AWQ_ERR_PATH;
-    // K range per split: a multiple of the 64-row k-step (variants 5, 6: of
+    if (variant < 2 || variant > kTileVariants || split_k < 1) return AWQ_ERR_PATH;
+    // K range per split: a multiple of the 64-row k-step (variants 5 and up: of
     // the 128-row group, two k-steps).
     const int64_t unit = variant >= 5 ? 128 : 64;
     const int64_t steps = K / unit;
@@ -412,14 +406,63 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     return AWQ_OK;
 }
 
-// Variant 6 (128 x 256 tiles, two workgroups per CU) when, with split-K up
-// to one pass over its 2 * kCUs workgroup slots and at least 4096 rows of K
-// per split, it has at least one workgroup per CU; otherwise variant 4
-// (256 x 128 tiles, one workgroup per CU) with split-K filling one pass over
-// the CUs, at least 16 k-steps per split.  Measured on the Qwen2-7B prefill
-// GEMMs (qkv, o, gate||up, down) at M = 256 .. 2048.
+// Predicted time (microseconds) of a reduce-finish register-dequant tile
+// plan (variants 7, 8, 9: 128-, 64- and 32-row tiles).  A workgroup alone on
+// its CU takes t1 per k-step (its 4 waves expose their own latency: LDS,
+// dependent VALU, barrier); each further workgroup on the CU slows every
+// step by eta; the grid runs in rounds of (2, 3, 4) x kCUs workgroup slots;
+// a fixed launch/prologue/epilogue cost; the reduce launch moves
+// split x M x N x 8 bytes (partials written, read, cleared).  Fitted to
+// 1300 timings of the Qwen2-7B GEMMs at M = 32 .. 1024 (MI355X, random
+// operands, warm clocks): 7 % rms error, its choice within 3 % of the
+// measured best on average.
+double tile_cost(int64_t M, int64_t N, int64_t K, int variant, int64_t split) {
+    static const double t1[3] = {1.285, 0.933, 0.741};
+    static const double eta[3] = {0.199, 0.262, 0.246};
+    const int i = variant - 7;
+    const int64_t wg = tile_tiles((int)M, (int)N, variant) * split;
+    const int64_t slots = (int64_t)(2 + i) * kCUs;
+    const int64_t groups = K / kGroup;
+    const int64_t steps = 2 * ((groups + split - 1) / split);
+    const int64_t rounds = (wg + slots - 1) / slots;
+    const double c = (double)(wg < slots ? wg : slots) / (double)kCUs;
+    const double share = 1.0 + eta[i] * (c - 1.0);
+    double t = 7.84 + (double)rounds * (double)steps * t1[i] * (share > 1.0 ? share : 1.0);
+    if (split > 1) t += 0.31 + (double)split * (double)M * (double)N * 8.0 / 2.12e6;
+    return t;
+}
+
+// Large M (above 1024, or where variant 6's grid already covers two
+// workgroups per CU): variant 6 (128 x 256 tiles, two workgroups per CU)
+// when, with split-K up to one pass over its 2 * kCUs slots and at least
+// 4096 rows of K per split, it has at least one workgroup per CU; otherwise
+// variant 4 (256 x 128 tiles, one workgroup per CU) with split-K filling one
+// pass over the CUs, at least 16 k-steps per split.  Smaller M: the
+// reduce-finish tile (variant 7, 8 or 9) and split count of least
+// tile_cost, split only as far as 7/4 workgroups per CU.  Measured on the
+// Qwen2-7B prefill GEMMs (qkv, o, gate||up, down) at M = 32 .. 2048.
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t tiles6 = tile_tiles((int)M, (int)N, 6);
+    if (M <= 1024 && tiles6 < 2 * kCUs) {
+        const int64_t groups = K / kGroup;
+        double best = 0.0;
+        int64_t best_v = 0, best_s = 0;
+        for (int v = 7; v <= 9; ++v) {
+            for (int64_t sp = 1; sp <= groups && sp <= 32; ++sp) {
+                awq_w4a16_plan q;
+                if (fill_tile(M, N, K, v, sp, &q) != AWQ_OK) continue;
+                // Splitting beyond 7/4 workgroups per CU never measured faster.
+                if (sp > 1 && q.grid * 4 > 7 * kCUs) continue;
+                const double t = tile_cost(M, N, K, v, sp);
+                if (best_v == 0 || t < best) {
+                    best = t;
+                    best_v = v;
+                    best_s = sp;
+                }
+            }
+        }
+        if (best_v != 0 && fill_tile(M, N, K, best_v, best_s, p) == AWQ_OK) return AWQ_OK;
+    }
     int64_t split6 = 1;
     if (tiles6 > 0 && tiles6 < 2 * kCUs && tiles6 * 4 <= (int64_t)kCounterBytes) {
         split6 = (2 * kCUs) / tiles6;

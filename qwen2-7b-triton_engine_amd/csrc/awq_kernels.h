@@ -46,9 +46,16 @@ struct NarrowConfig {
     bool factored;           // zero and scale per group sum (M <= 8) or per weight
 };
 
+// Tile variants 5 .. kTileVariants: weights dequantised into MFMA registers,
+// every load a direct global->LDS load into a ring (x rows per tile, stages).
+constexpr int kTileVariants = 9;
+constexpr int tile5_rows(int variant) {
+    return variant == 5 ? 256 : (variant == 6 || variant == 7) ? 128 : variant == 8 ? 64 : 32;
+}
+
 struct TileConfig {
     int variant;             // 1: 128x128x32; 2: 128x128x64, prefetch, XCD order, split-K; 3: 256x128x64, x ring in LDS;
-                             // 4: 3 with interleaved dequant; 5: 256x256x64, register dequant
+                             // 4: 3 with interleaved dequant; 5 .. kTileVariants: register dequant, N tile 256
     int tile_m, tile_n;
     int split_k;             // variant 2: workgroups along K per tile
     int k_per_split;         // variant 2: K rows per split (multiple of 64)
@@ -87,6 +94,9 @@ int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
 // return.
 constexpr int kStreamHalfLayout = 32;  // rows per chunk
 constexpr int kStreamRowLayout = 16;
+// awq_splitk_reduce_kernel over a.partials [split_k][M][N] fp32 -> a.out,
+// zeroing the partials it reads.
+hipError_t splitk_reduce_launch(const GemmArgs& a, int split_k, hipStream_t stream);
 hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, int depth, int layout, int finish,
                          uint32_t* counters, hipStream_t stream);
 size_t stream_lds_bytes(int M, int K, int split_k, int k_waves, int layout);

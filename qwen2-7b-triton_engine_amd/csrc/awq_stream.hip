@@ -534,13 +534,15 @@ int64_t stream_reduce_blocks(int M, int N, int split_k) {
     return ((int64_t)M * N / 4 + qpb - 1) / qpb;
 }
 
-namespace {
-hipError_t reduce_launch(const GemmArgs& a, int split_k, hipStream_t stream) {
+hipError_t splitk_reduce_launch(const GemmArgs& a, int split_k, hipStream_t stream) {
     const int P = stream_reduce_parts(split_k);
     hipLaunchKernelGGL(awq_splitk_reduce_kernel, dim3((unsigned)stream_reduce_blocks(a.M, a.N, split_k)), dim3(256), 0,
                        stream, a.partials, a.out, a.M, a.N, split_k, P);
     return hipGetLastError();
 }
+
+namespace {
+hipError_t reduce_launch(const GemmArgs& a, int split_k, hipStream_t stream) { return splitk_reduce_launch(a, split_k, stream); }
 
 template <int MP, int FIN, int R>
 hipError_t half_launch(const GemmArgs& a, int split_k, int k_waves, uint32_t* counters, hipStream_t stream) {

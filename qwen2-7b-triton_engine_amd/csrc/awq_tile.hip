@@ -707,24 +707,35 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
 //     half h reads them as two 16-byte words; one dword load covers 4 rows x
 //     16 columns (64-byte row segments).
 //   * the group's zero words (32 dwords) and scales (256 halves).
-// WM: waves along M -- 2: 256-row tiles, 8 waves, one workgroup per CU;
-// 1: 128-row tiles, 4 waves, two workgroups per CU.
+// WM: waves along M -- 2: 8 waves, one workgroup per CU; 1: 4 waves.
+// FM: 16-row blocks per wave (8: 128 x rows per wave; 4: 64; 2: 32).
+// Variant 5 = (2, 8): 256 x 256 tiles; 6 = (1, 8): 128 x 256 tiles, two
+// workgroups per CU, last-arriver split-K finish; 7, 8, 9 = (1, 8), (1, 4),
+// (1, 2): 128, 64 and 32 x 256 tiles (two, three, four workgroups per CU)
+// with the reduce-launch finish -- the smaller tiles for M up to about a
+// thousand, where the larger ones would leave MFMA rows idle or the CUs
+// short of work.
 namespace {
 constexpr int T5_BK = 64;
 constexpr int T5_BN = 256;
-constexpr int T5_STAGES = 3;
 constexpr int T5_W_BYTES = 64 * 32 * 4;       // packed weights of one k-step
 constexpr int T5_ZS_BYTES = 768;              // 256 B zero words (128 used) + 512 B scales
 constexpr int T5_GM = 4;
 
-template <int WM>
+template <int WM, int FM, int S>
 struct T5Layout {
-    static constexpr int BM = 128 * WM;
+    static constexpr int RW = 16 * FM;  // x rows per wave
+    static constexpr int BM = RW * WM;
     static constexpr int X_BYTES = BM * T5_BK * 2;
     static constexpr int STAGE = X_BYTES + T5_W_BYTES + T5_ZS_BYTES;
     static constexpr int THREADS = 256 * WM;
     static constexpr int WAVES = 4 * WM;
-    static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;   // dwordx4 loads per wave per stage (4)
+    static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;   // dwordx4 loads per wave per stage (FM / 2)
+    // Workgroups per CU: by registers (accumulators 4 * FM float4 per lane)
+    // and by LDS (S stages).
+    static constexpr int PER_CU_REG = WM == 2 ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
+    static constexpr int PER_CU_LDS = (160 * 1024) / (S * (X_BYTES + T5_W_BYTES + T5_ZS_BYTES) + 64);
+    static constexpr int PER_CU = PER_CU_REG < PER_CU_LDS ? PER_CU_REG : PER_CU_LDS;
     static constexpr int W_LOADS = T5_W_BYTES / 256 / WAVES;  // dword loads per wave per stage
     // Loads a wave issues per stage, not counting the zero/scale load that
     // waves 0..2 add (issued first, so a wait that leaves this many
@@ -733,13 +744,37 @@ struct T5Layout {
 };
 }  // namespace
 
-template <int WM>
-__global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs a, int split_k, int k_per_split,
-                                                                        uint32_t* counters) {
-    using L = T5Layout<WM>;
+// s_waitcnt vmcnt(n * LOADS) for a wave-uniform n in 0 .. N (immediate
+// operands only, hence the chain).
+template <int LOADS, int N>
+__device__ __forceinline__ void wait_batches(int n) {
+    if constexpr (N > 0) {
+        if (n >= N) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N * LOADS) : "memory");
+            return;
+        }
+        wait_batches<LOADS, N - 1>(n);
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
+// FIN (split_k > 1): 0 -- the last workgroup of a tile to arrive adds the
+// partials; 1 -- partials with plain stores, summed by a second launch of
+// awq_splitk_reduce_kernel over the whole device (for small tiles, whose
+// last arrivers would each read split x tile bytes alone).
+template <int WM, int FM, int S, int FIN>
+__global__ __launch_bounds__(256 * WM, (T5Layout<WM, FM, S>::PER_CU)) void awq_tile_kernel_v5(GemmArgs a, int split_k,
+                                                                                          int k_per_split,
+                                                                                          uint32_t* counters) {
+    using L = T5Layout<WM, FM, S>;
     constexpr int BM = L::BM;
-    static_assert(L::LOADS <= 63, "vmcnt holds 6 bits");
-    __shared__ __attribute__((aligned(16))) unsigned char smem[T5_STAGES * L::STAGE];
+    constexpr int RW = L::RW;
+    static_assert(S >= 3, "the ring needs a stage being read, one landing, one being filled");
+    static_assert((S - 2) * L::LOADS <= 63, "vmcnt holds 6 bits");
+    static_assert(FM % 2 == 0 && L::X_LOADS >= 1, "a wave loads whole 8-row blocks of x");
+    static_assert(L::PER_CU >= 1 && L::PER_CU * S * L::STAGE <= 160 * 1024, "LDS per CU");
+    __shared__ __attribute__((aligned(16))) unsigned char smem[S * L::STAGE];
     __shared__ int last_flag;
     floatx4* fin = reinterpret_cast<floatx4*>(smem);  // split-K finish, after the main loop
 
@@ -838,11 +873,11 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs 
     const uint32_t sel_odd = hh ? 0x0C070C03u : 0x0C060C02u;
     const int jl = 8 * wn + (n16 & 7);  // lane's packed column within the tile
 
-    floatx4 acc[4][8];
+    floatx4 acc[4][FM];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int f = 0; f < 8; ++f) acc[c][f] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int f = 0; f < FM; ++f) acc[c][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // One k-step from stage memory `st`: per k-half, two 16-byte reads give
     // the lane's 8 weight words, 4 A fragments are formed (second nibble
@@ -877,8 +912,8 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs 
                 }
             }
 #pragma unroll
-            for (int f = 0; f < 8; ++f) {
-                const int r = 128 * wm + 16 * f + n16;
+            for (int f = 0; f < FM; ++f) {
+                const int r = RW * wm + 16 * f + n16;
                 const half8_t bf = *reinterpret_cast<const half8_t*>(&xs[r * T5_BK + 8 * ((4 * h + kb) ^ (r & 7))]);
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
@@ -888,26 +923,24 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs 
     };
 
     if (KT > 0) {
-        // Prologue: steps 0 and 1 in flight (KT is even, so >= 2); wait for step 0.
-        issue(0, 0);
-        issue(1, 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::LOADS) : "memory");
+        // Prologue: steps 0 .. S - 2 in flight; wait for step 0.
+#pragma unroll
+        for (int j = 0; j < S - 1; ++j)
+            if (j < KT) issue(j, j);
+        wait_batches<L::LOADS, S - 2>(min(S - 2, KT - 1));
         __syncthreads();
         int stage = 0;
         for (int kt = 0; kt < KT; ++kt) {
-            const bool ahead = kt + 2 < KT;
-            const int st2 = stage == 0 ? 2 : stage - 1;  // (kt + 2) % 3
-            if (ahead) issue(kt + 2, st2);
+            // Step kt + S - 1 into the stage step kt - 1 used (read before the
+            // previous barrier).
+            if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
             __builtin_amdgcn_sched_barrier(0);
             compute(smem + stage * L::STAGE);
-            // Step kt + 1's loads (issued two steps back) must have landed
-            // before the barrier; those of step kt + 2 stay in flight.
-            if (ahead)
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::LOADS) : "memory");
-            else
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            // Step kt + 1's loads must have landed before the barrier; those
+            // of steps kt + 2 .. kt + S - 1 that were issued stay in flight.
+            wait_batches<L::LOADS, S - 2>(max(0, min(S - 2, KT - 2 - kt)));
             __syncthreads();
-            stage = stage == 2 ? 0 : stage + 1;
+            stage = stage == S - 1 ? 0 : stage + 1;
         }
     }
 
@@ -915,15 +948,15 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs 
 #pragma unroll
     for (int c = 2; c < 4; ++c)
 #pragma unroll
-        for (int f = 0; f < 8; ++f) acc[c][f] *= 0.0625f;
+        for (int f = 0; f < FM; ++f) acc[c][f] *= 0.0625f;
 
-    // acc[c][f] lane value r: out[m0 + 128 wm + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
+    // acc[c][f] lane value r: out[m0 + RW wm + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
     const int pc0 = (n0 >> 3) + 8 * wn + 4 * (kb & 1);
     const int coff = 4 * (kb >> 1);
     if (split_k == 1) {
 #pragma unroll
-        for (int f = 0; f < 8; ++f) {
-            const int m = m0 + 128 * wm + 16 * f + n16;
+        for (int f = 0; f < FM; ++f) {
+            const int m = m0 + RW * wm + 16 * f + n16;
             if (m >= a.M) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -939,8 +972,8 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs 
     const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
     const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
 #pragma unroll
-    for (int f = 0; f < 8; ++f) {
-        const int m = m0 + 128 * wm + 16 * f + n16;
+    for (int f = 0; f < FM; ++f) {
+        const int m = m0 + RW * wm + 16 * f + n16;
         if (m >= a.M) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -949,6 +982,7 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs 
             buf_store_f4_device(floatx4{acc[0][f][r], acc[1][f][r], acc[2][f][r], acc[3][f][r]}, rp_, off);
         }
     }
+    if constexpr (FIN == 1) return;
     wait_vm_stores();
     __syncthreads();
     if (tid == 0)
@@ -961,8 +995,10 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void awq_tile_kernel_v5(GemmArgs 
 }
 
 int64_t tile_tiles(int M, int N, int variant) {
-    if (variant == 5) return (int64_t)((M + 255) / 256) * ((N + T5_BN - 1) / T5_BN);
-    if (variant == 6) return (int64_t)((M + 127) / 128) * ((N + T5_BN - 1) / T5_BN);
+    if (variant >= 5 && variant <= kTileVariants) {
+        const int bm = tile5_rows(variant);
+        return (int64_t)((M + bm - 1) / bm) * ((N + T5_BN - 1) / T5_BN);
+    }
     if (variant >= 3) return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
     return (int64_t)((M + T2_BM - 1) / T2_BM) * ((N + T2_BN - 1) / T2_BN);
 }
@@ -994,15 +1030,22 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
                                cfg.split_k, cfg.k_per_split, counters);
         return hipGetLastError();
     }
-    if (cfg.variant == 5 || cfg.variant == 6) {
+    if (cfg.variant >= 5 && cfg.variant <= kTileVariants) {
         const int64_t blocks = tile_tiles(a.M, a.N, cfg.variant) * cfg.split_k;
         if (blocks == 0) return hipSuccess;
-        if (cfg.variant == 5)
-            hipLaunchKernelGGL(awq_tile_kernel_v5<2>, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
-                               cfg.k_per_split, counters);
-        else
-            hipLaunchKernelGGL(awq_tile_kernel_v5<1>, dim3((unsigned)blocks), dim3(256), 0, stream, a, cfg.split_k,
-                               cfg.k_per_split, counters);
+        const dim3 grid((unsigned)blocks);
+        bool reduce = false;
+        switch (cfg.variant) {
+            case 5: hipLaunchKernelGGL((awq_tile_kernel_v5<2, 8, 3, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 6: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 3, 0>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 7: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 3, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 8: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 4, 3, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 9: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 2, 3, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            default: return hipErrorInvalidValue;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess || !reduce || cfg.split_k <= 1) return e;
+        return splitk_reduce_launch(a, cfg.split_k, stream);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;
