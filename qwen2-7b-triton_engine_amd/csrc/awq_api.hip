@@ -378,7 +378,7 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     if (variant >= 5 && variant <= kTileVariants) {
         p->tile_m = tile5_rows((int)variant);
         p->tile_n = 256;
-        p->block_threads = variant == 5 ? 512 : 256;
+        p->block_threads = tile5_threads((int)variant);
     }
     const int64_t tiles = tile_tiles((int)M, (int)N, (int)variant);
     if (variant == 1) {
@@ -406,57 +406,69 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     return AWQ_OK;
 }
 
-// Predicted time (microseconds) of a reduce-finish register-dequant tile
-// plan (variants 7, 8, 9: 128-, 64- and 32-row tiles).  A workgroup alone on
-// its CU takes t1 per k-step (its 4 waves expose their own latency: LDS,
-// dependent VALU, barrier); each further workgroup on the CU slows every
-// step by eta; the grid runs in rounds of (2, 3, 4) x kCUs workgroup slots;
-// a fixed launch/prologue/epilogue cost; the reduce launch moves
-// split x M x N x 8 bytes (partials written, read, cleared).  Fitted to
-// 1300 timings of the Qwen2-7B GEMMs at M = 32 .. 1024 (MI355X, random
-// operands, warm clocks): 7 % rms error, its choice within 3 % of the
-// measured best on average.
-double tile_cost(int64_t M, int64_t N, int64_t K, int variant, int64_t split) {
-    static const double t1[3] = {1.285, 0.933, 0.741};
-    static const double eta[3] = {0.199, 0.262, 0.246};
-    const int i = variant - 7;
-    const int64_t wg = tile_tiles((int)M, (int)N, variant) * split;
-    const int64_t slots = (int64_t)(2 + i) * kCUs;
-    const int64_t groups = K / kGroup;
-    const int64_t steps = 2 * ((groups + split - 1) / split);
+// Register-dequant tile variants (tile rows, workgroups per CU, a lone
+// workgroup's time per k-step in microseconds, slowdown per further
+// workgroup on the CU, finish: 1 reduce launch / 0 last arriver).  Variants
+// 10 .. 12 pair a second wave per SIMD from the same workgroup (k-halves),
+// so a lone workgroup's step is shorter.
+struct TileModel {
+    int variant, rows, per_cu;
+    double t1, eta;
+    int reduce;
+};
+constexpr TileModel kTileModels[] = {
+    {6, 128, 2, 1.285, 0.199, 0}, {7, 128, 2, 1.285, 0.199, 1}, {8, 64, 3, 0.933, 0.262, 1},
+    {9, 32, 4, 0.741, 0.246, 1},  {10, 128, 1, 1.032, 0.0, 0},  {11, 128, 1, 1.032, 0.0, 1},
+    {12, 64, 1, 0.700, 0.0, 1},
+};
+
+// Predicted time (microseconds) of a tile plan: a workgroup alone on its CU
+// takes t1 per k-step (its waves expose their own latency: LDS, dependent
+// VALU, barrier); each further workgroup on the CU slows every step by eta;
+// the grid runs in rounds of per_cu x kCUs slots; a fixed launch, prologue
+// and epilogue cost; the reduce launch moves split x M x N x 8 bytes
+// (partials written, read, cleared).  Fitted to timings of the four Qwen2-7B
+// GEMMs at M = 32 .. 2048 (MI355X, random operands, warm clocks): its
+// choices are on average 3.6 % slower than the best measured configuration.
+double tile_cost(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
+    const int64_t wg = tile_tiles((int)M, (int)N, t.variant) * split;
+    const int64_t slots = (int64_t)t.per_cu * kCUs;
+    const int64_t steps = 2 * ((K / kGroup + split - 1) / split);
     const int64_t rounds = (wg + slots - 1) / slots;
     const double c = (double)(wg < slots ? wg : slots) / (double)kCUs;
-    const double share = 1.0 + eta[i] * (c - 1.0);
-    double t = 7.84 + (double)rounds * (double)steps * t1[i] * (share > 1.0 ? share : 1.0);
-    if (split > 1) t += 0.31 + (double)split * (double)M * (double)N * 8.0 / 2.12e6;
-    return t;
+    const double share = 1.0 + t.eta * (c - 1.0);
+    double time = 7.84 + (double)rounds * (double)steps * t.t1 * (share > 1.0 ? share : 1.0);
+    if (split > 1) time += 0.31 + (double)split * (double)M * (double)N * 8.0 / 2.12e6;
+    return time;
 }
 
-// Large M (above 1024, or where variant 6's grid already covers two
-// workgroups per CU): variant 6 (128 x 256 tiles, two workgroups per CU)
-// when, with split-K up to one pass over its 2 * kCUs slots and at least
-// 4096 rows of K per split, it has at least one workgroup per CU; otherwise
-// variant 4 (256 x 128 tiles, one workgroup per CU) with split-K filling one
-// pass over the CUs, at least 16 k-steps per split.  Smaller M: the
-// reduce-finish tile (variant 7, 8 or 9) and split count of least
-// tile_cost, split only as far as 7/4 workgroups per CU.  Measured on the
-// Qwen2-7B prefill GEMMs (qkv, o, gate||up, down) at M = 32 .. 2048.
+// Where variant 6's grid covers two workgroups per CU (gate||up at M >= 512):
+// variant 6.  Above M = 1024 otherwise: variant 6 when, with split-K up to
+// one pass over its 2 * kCUs slots and at least 4096 rows of K per split, it
+// has at least one workgroup per CU; else the k-half pair tile (variant 10)
+// when its tiles fit one pass over the CUs; else variant 4 (256 x 128 tiles)
+// with split-K filling one pass over the CUs, >= 16 k-steps per split.
+// M <= 1024: the variant and split count of least tile_cost (last-arriver
+// variants unsplit only; split no further than 7/4 workgroups per CU).
+// Measured on the Qwen2-7B prefill GEMMs (qkv, o, gate||up, down) at
+// M = 32 .. 2048.
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t tiles6 = tile_tiles((int)M, (int)N, 6);
     if (M <= 1024 && tiles6 < 2 * kCUs) {
         const int64_t groups = K / kGroup;
         double best = 0.0;
         int64_t best_v = 0, best_s = 0;
-        for (int v = 7; v <= 9; ++v) {
+        for (const TileModel& t : kTileModels) {
             for (int64_t sp = 1; sp <= groups && sp <= 32; ++sp) {
+                if (!t.reduce && sp > 1) break;
                 awq_w4a16_plan q;
-                if (fill_tile(M, N, K, v, sp, &q) != AWQ_OK) continue;
+                if (fill_tile(M, N, K, t.variant, sp, &q) != AWQ_OK) continue;
                 // Splitting beyond 7/4 workgroups per CU never measured faster.
                 if (sp > 1 && q.grid * 4 > 7 * kCUs) continue;
-                const double t = tile_cost(M, N, K, v, sp);
-                if (best_v == 0 || t < best) {
-                    best = t;
-                    best_v = v;
+                const double time = tile_cost(t, M, N, K, sp);
+                if (best_v == 0 || time < best) {
+                    best = time;
+                    best_v = t.variant;
                     best_s = sp;
                 }
             }
@@ -474,6 +486,7 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
         split6 = (units + per - 1) / per;
     }
     if (tiles6 * split6 >= kCUs && fill_tile(M, N, K, 6, split6, p) == AWQ_OK) return AWQ_OK;
+    if (tiles6 <= kCUs && fill_tile(M, N, K, 10, 1, p) == AWQ_OK) return AWQ_OK;
     const int64_t tiles = tile_tiles((int)M, (int)N, 4);
     int64_t split = 1;
     if (tiles < kCUs && tiles * 4 <= (int64_t)kCounterBytes) {

@@ -48,10 +48,11 @@ struct NarrowConfig {
 
 // Tile variants 5 .. kTileVariants: weights dequantised into MFMA registers,
 // every load a direct global->LDS load into a ring (x rows per tile, stages).
-constexpr int kTileVariants = 9;
+constexpr int kTileVariants = 12;
 constexpr int tile5_rows(int variant) {
-    return variant == 5 ? 256 : (variant == 6 || variant == 7) ? 128 : variant == 8 ? 64 : 32;
+    return variant == 5 ? 256 : (variant == 8 || variant == 12) ? 64 : variant == 9 ? 32 : 128;
 }
+constexpr int tile5_threads(int variant) { return (variant == 5 || variant >= 10) ? 512 : 256; }
 
 struct TileConfig {
     int variant;             // 1: 128x128x32; 2: 128x128x64, prefetch, XCD order, split-K; 3: 256x128x64, x ring in LDS;

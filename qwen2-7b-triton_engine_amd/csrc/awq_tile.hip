@@ -709,6 +709,11 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
 //   * the group's zero words (32 dwords) and scales (256 halves).
 // WM: waves along M -- 2: 8 waves, one workgroup per CU; 1: 4 waves.
 // FM: 16-row blocks per wave (8: 128 x rows per wave; 4: 64; 2: 32).
+// KW: 2 -- a second wave per SIMD from the same workgroup: waves w and w + 4
+// take k-half 0 and 1 of every k-step for the same columns and rows (each
+// dequantises only its half) and add their accumulators through LDS at the
+// end; for grids too small to give each CU two workgroups, where a lone
+// wave per SIMD would expose its own latency.
 // Variant 5 = (2, 8): 256 x 256 tiles; 6 = (1, 8): 128 x 256 tiles, two
 // workgroups per CU, last-arriver split-K finish; 7, 8, 9 = (1, 8), (1, 4),
 // (1, 2): 128, 64 and 32 x 256 tiles (two, three, four workgroups per CU)
@@ -721,19 +726,21 @@ constexpr int T5_BN = 256;
 constexpr int T5_W_BYTES = 64 * 32 * 4;       // packed weights of one k-step
 constexpr int T5_ZS_BYTES = 768;              // 256 B zero words (128 used) + 512 B scales
 constexpr int T5_GM = 4;
+constexpr int T5_STAGES = 3;
 
-template <int WM, int FM, int S>
+template <int WM, int FM, int KW>
 struct T5Layout {
+    static constexpr int S = T5_STAGES;
     static constexpr int RW = 16 * FM;  // x rows per wave
     static constexpr int BM = RW * WM;
     static constexpr int X_BYTES = BM * T5_BK * 2;
     static constexpr int STAGE = X_BYTES + T5_W_BYTES + T5_ZS_BYTES;
-    static constexpr int THREADS = 256 * WM;
-    static constexpr int WAVES = 4 * WM;
+    static constexpr int THREADS = 256 * WM * KW;
+    static constexpr int WAVES = 4 * WM * KW;
     static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;   // dwordx4 loads per wave per stage (FM / 2)
     // Workgroups per CU: by registers (accumulators 4 * FM float4 per lane)
     // and by LDS (S stages).
-    static constexpr int PER_CU_REG = WM == 2 ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
+    static constexpr int PER_CU_REG = (WM == 2 || KW == 2) ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
     static constexpr int PER_CU_LDS = (160 * 1024) / (S * (X_BYTES + T5_W_BYTES + T5_ZS_BYTES) + 64);
     static constexpr int PER_CU = PER_CU_REG < PER_CU_LDS ? PER_CU_REG : PER_CU_LDS;
     static constexpr int W_LOADS = T5_W_BYTES / 256 / WAVES;  // dword loads per wave per stage
@@ -763,14 +770,14 @@ __device__ __forceinline__ void wait_batches(int n) {
 // partials; 1 -- partials with plain stores, summed by a second launch of
 // awq_splitk_reduce_kernel over the whole device (for small tiles, whose
 // last arrivers would each read split x tile bytes alone).
-template <int WM, int FM, int S, int FIN>
-__global__ __launch_bounds__(256 * WM, (T5Layout<WM, FM, S>::PER_CU)) void awq_tile_kernel_v5(GemmArgs a, int split_k,
-                                                                                          int k_per_split,
-                                                                                          uint32_t* counters) {
-    using L = T5Layout<WM, FM, S>;
+template <int WM, int FM, int KW, int FIN>
+__global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void awq_tile_kernel_v5(
+    GemmArgs a, int split_k, int k_per_split, uint32_t* counters) {
+    using L = T5Layout<WM, FM, KW>;
     constexpr int BM = L::BM;
     constexpr int RW = L::RW;
-    static_assert(S >= 3, "the ring needs a stage being read, one landing, one being filled");
+    constexpr int S = L::S;
+    static_assert(KW == 1 || (KW == 2 && WM == 1), "k-half wave pairs only with one wave row");
     static_assert((S - 2) * L::LOADS <= 63, "vmcnt holds 6 bits");
     static_assert(FM % 2 == 0 && L::X_LOADS >= 1, "a wave loads whole 8-row blocks of x");
     static_assert(L::PER_CU >= 1 && L::PER_CU * S * L::STAGE <= 160 * 1024, "LDS per CU");
@@ -782,6 +789,7 @@ __global__ __launch_bounds__(256 * WM, (T5Layout<WM, FM, S>::PER_CU)) void awq_t
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = WM == 2 ? wave >> 2 : 0;
+    const int kh = KW == 2 ? wave >> 2 : 0;  // k-half of each step this wave computes (KW = 2)
     const int wn = wave & 3;
     const int n16 = lane & 15;
     const int kb = lane >> 4;
@@ -896,7 +904,8 @@ __global__ __launch_bounds__(256 * WM, (T5Layout<WM, FM, S>::PER_CU)) void awq_t
             ssp[c] = as_u32(half2_t{s4[c], s4[c]});
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int hs = 0; hs < 3 - KW; ++hs) {
+            const int h = KW == 2 ? kh : hs;
             const u32x4 w0 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 0) * 32 + jl) * 4]);
             const u32x4 w1 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 1) * 32 + jl) * 4]);
             const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
@@ -944,6 +953,30 @@ __global__ __launch_bounds__(256 * WM, (T5Layout<WM, FM, S>::PER_CU)) void awq_t
         }
     }
 
+    // KW = 2: wave w + 4 hands its k-half sums to wave w through LDS (two
+    // rounds of two columns; the ring is idle after the last barrier).
+    if constexpr (KW == 2) {
+        floatx4* xch = reinterpret_cast<floatx4*>(smem);
+        static_assert(2 * FM * 4 * 64 * 16 <= S * L::STAGE, "exchange fits the ring");
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            if (kh == 1) {
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                    for (int f = 0; f < FM; ++f) xch[((cc * FM + f) * 4 + wn) * 64 + lane] = acc[2 * r + cc][f];
+            }
+            __syncthreads();
+            if (kh == 0) {
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                    for (int f = 0; f < FM; ++f) acc[2 * r + cc][f] += xch[((cc * FM + f) * 4 + wn) * 64 + lane];
+            }
+            __syncthreads();
+        }
+    }
+
     // Columns 2, 3 of each half were computed 16 times too large (exact in fp32).
 #pragma unroll
     for (int c = 2; c < 4; ++c)
@@ -954,6 +987,7 @@ __global__ __launch_bounds__(256 * WM, (T5Layout<WM, FM, S>::PER_CU)) void awq_t
     const int pc0 = (n0 >> 3) + 8 * wn + 4 * (kb & 1);
     const int coff = 4 * (kb >> 1);
     if (split_k == 1) {
+        if (kh != 0) return;  // KW = 2: the sums are in waves 0..3
 #pragma unroll
         for (int f = 0; f < FM; ++f) {
             const int m = m0 + RW * wm + 16 * f + n16;
@@ -974,7 +1008,7 @@ __global__ __launch_bounds__(256 * WM, (T5Layout<WM, FM, S>::PER_CU)) void awq_t
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
         const int m = m0 + RW * wm + 16 * f + n16;
-        if (m >= a.M) continue;
+        if (m >= a.M || kh != 0) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if (pc0 + r >= pn) continue;
@@ -1036,11 +1070,14 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
         const dim3 grid((unsigned)blocks);
         bool reduce = false;
         switch (cfg.variant) {
-            case 5: hipLaunchKernelGGL((awq_tile_kernel_v5<2, 8, 3, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 6: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 3, 0>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 7: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 3, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 8: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 4, 3, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 9: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 2, 3, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 5: hipLaunchKernelGGL((awq_tile_kernel_v5<2, 8, 1, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 6: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 1, 0>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 7: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 8: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 4, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 9: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 2, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 10: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 2, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 11: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 12: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 4, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
             default: return hipErrorInvalidValue;
         }
         const hipError_t e = hipGetLastError();

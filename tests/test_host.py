@@ -92,7 +92,9 @@ def test_auto_plan_invariants(L, m, k, n):
     else:
         assert p.path == _native.PATH_TILE
         if m <= 1024 and -(-m // 128) * -(-n // 256) < 512:
-            assert p.variant in (7, 8, 9)   # the reduce-finish tiles, by the cost model
+            assert p.variant >= 6           # the register-dequant tiles, by the cost model
+            if p.variant in (6, 10):
+                assert p.split_k == 1       # last-arriver variants only unsplit
     assert p.grid > 0 and p.block_threads % 64 == 0 and p.block_threads <= 1024
     if p.split_k > 1:
         if (p.path == _native.PATH_GEMV and p.variant in (4, 5)) or (p.path == _native.PATH_STREAM and p.variant == 1):
@@ -111,7 +113,7 @@ def test_tile_plans_cover_k_exactly(L, k, n):
     """Every split-K plan gives each split a whole number of 64-row k-steps
     (variants 5..9: of 128-row groups) and covers K exactly; the tile count fits
     the arrival-counter block."""
-    for variant in range(2, 10):
+    for variant in range(2, 13):
         for split in (1, 2, 3, 4, 5, 8):
             try:
                 p = _native.plan_tile(512, n, k, variant, split)
@@ -121,7 +123,7 @@ def test_tile_plans_cover_k_exactly(L, k, n):
             per = p.rows_per_wave
             assert per % (128 if variant >= 5 else 64) == 0
             assert (split - 1) * per < k <= split * per
-            tm = {3: 256, 4: 256, 5: 256, 6: 128, 7: 128, 8: 64, 9: 32}.get(variant, 128)
+            tm = {3: 256, 4: 256, 5: 256, 6: 128, 7: 128, 8: 64, 9: 32, 12: 64}.get(variant, 128)
             tn = 256 if variant >= 5 else 128
             tiles = -(-512 // tm) * -(-n // tn)
             assert p.grid == tiles * split
@@ -155,7 +157,7 @@ def test_skinny_and_gemv_plan_rejections():
     with pytest.raises(_native.AwqNativeError):
         _native.plan_tile(512, 512, 3584, 1, 2)         # variant 1 has no split-K
     with pytest.raises(_native.AwqNativeError):
-        _native.plan_tile(512, 512, 3584, 10, 1)
+        _native.plan_tile(512, 512, 3584, 13, 1)
 
 
 def test_planned_call_rejects_altered_plan(L):
