@@ -34,6 +34,7 @@ for _p in (PKG, ROOT):
 METRIC = "W4A16 AWQ GEMM: decode HBM GB/s vs peak; prefill TFLOPS vs MFMA peak"
 LAYERS = 28
 HIDDEN, INTER = 3584, 18944
+VOCAB = 152064
 ENGINE_SHAPES = (("qkv_proj", HIDDEN, 4608), ("o_proj", HIDDEN, HIDDEN),
                  ("gate_up_proj", HIDDEN, 2 * INTER), ("down_proj", INTER, HIDDEN))
 DECODE_M = (1, 4, 16)
@@ -296,6 +297,29 @@ def main():
 
         result["prefill_gate_up"] = mfma_point(2048, HIDDEN, 2 * INTER, 4)
         result["down_m_sweep"] = [mfma_point(m, INTER, HIDDEN, 4 if m >= 512 else 16) for m in (1, 8, 64, 512, 2048)]
+
+        # fp16 lm_head GEMV (vocab x hidden, 1.09 GB per token), next to torch's own F.linear
+        from kernels.lm_head import lm_head_forward
+        import torch.nn.functional as F
+
+        lm_ws = [(torch.randn((VOCAB, HIDDEN), device=dev) * 0.02).half() for _ in range(3)]
+        lm_bytes = VOCAB * HIDDEN * 2
+        lm = []
+        for m in (1, 4):
+            xl = torch.randn((m, HIDDEN), device=dev).half()
+            row = {"M": m, "K": HIDDEN, "N": VOCAB}
+            for key, fn in (("us", lambda w: lm_head_forward(xl, w)), ("torch_linear_us", lambda w: F.linear(xl, w))):
+                fn(lm_ws[0])
+                g = graph_of(torch, lambda: [fn(w) for w in lm_ws])
+                g.replay()
+                t = min(time_graph(torch, g, 5) for _ in range(3)) / len(lm_ws)
+                row[key] = round(t * 1e6, 2)
+                del g
+            row["GBps"] = round(lm_bytes / (row["us"] * 1e-6) / 1e9, 1)
+            row["hbm_frac"] = round(lm_bytes / (row["us"] * 1e-6) / HBM_PEAK_BPS, 3)
+            lm.append(row)
+        result["lm_head_fp16_gemv"] = lm
+        del lm_ws
 
     # ---- CPU baseline: the reference's dequant + matmul on the host --------
     if not args.no_cpu_baseline:

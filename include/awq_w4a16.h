@@ -107,9 +107,14 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
  * two workgroups per CU) tiles, each wavefront 128 x rows x 64 columns,
  * weights dequantised straight into MFMA operand registers, x, raw weights
  * and zeros/scales brought by direct global->LDS loads two k-steps ahead
- * into a 3-stage ring; variants 2..6 take split_k >= 1 workgroups along K,
- * variants 5 and 6 in whole 128-row groups).  For variants 2..6 the plan's
- * rows_per_wave holds the K rows per split. */
+ * into a 3-stage ring; variants 7, 8, 9: 128-, 64- and 32-row tiles of the
+ * same kernel (two, three, four workgroups per CU) whose split-K partials are
+ * summed by a second, whole-device launch; variants 10, 11, 12: 128-, 128-
+ * and 64-row tiles with two wavefronts per SIMD from one workgroup, each
+ * taking one k-half of every k-step (10: last-arriver split-K finish, 11 and
+ * 12: the second launch); variants 2..12 take split_k >= 1 workgroups along
+ * K, variants 5 and up in whole 128-row groups).  For variants 2..12 the
+ * plan's rows_per_wave holds the K rows per split. */
 int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 
@@ -220,6 +225,17 @@ int awq_w4a16_gemm_planned(const void* x, const int32_t* qweight, const int32_t*
  * it runs the same unpack/dequant device code as the GEMM kernels. */
 int awq_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales,
                       void* w_out, int64_t N, int64_t K, int32_t group_size, void* stream);
+
+/* out[M,N] = x[M,K] @ weight[N,K]^T in fp16 with fp32 accumulation: the
+ * fp16 output projection (lm_head) of model/qwen2.py:253,280
+ * (nn.Linear(hidden_size, vocab_size, bias=False), applied at :280), at
+ * decode sizes.  weight is nn.Linear's row-major [out_features, in_features]
+ * fp16.  M in 0 .. 8 (AWQ_ERR_PATH above: greedy decoding needs the last
+ * position only); K % 8 == 0 and K <= 4096 (AWQ_ERR_BAD_DIMS /
+ * AWQ_ERR_TOO_LARGE); x and weight 16-byte aligned.
+ * No workspace; M == 0 is a valid no-op. */
+int awq_fp16_linear(const void* x, const void* weight, void* out, int64_t M, int64_t N, int64_t K,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,8 @@ constexpr uint64_t kSkinnyLdsBudget = 64 * 1024;
 
 // Compute units of an MI355X.
 constexpr int64_t kCUs = 256;
+// Largest M awq_fp16_linear serves (decode: the last position's logits).
+constexpr int64_t kFp16LinearMaxM = 8;
 
 constexpr int64_t kIndexLimit = (int64_t)1 << 30;
 // K bound that keeps every 32-bit buffer offset in range, including the rows
@@ -771,6 +773,21 @@ int awq_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void*
                                         reinterpret_cast<const uint32_t*>(qzeros),
                                         static_cast<const half_t*>(scales), static_cast<half_t*>(w_out),
                                         (int)N, (int)K, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
+}
+
+int awq_fp16_linear(const void* x, const void* weight, void* out, int64_t M, int64_t N, int64_t K, void* stream) {
+    if (M < 0 || N <= 0 || K <= 0 || K % 8 != 0) return AWQ_ERR_BAD_DIMS;
+    if (M > kFp16LinearMaxM) return AWQ_ERR_PATH;
+    if (K > fp16_gemv_max_k() || N > (int64_t)1 << 30 ||
+        (uint64_t)N * (uint64_t)K * 2u >= ((uint64_t)1 << 31))
+        return AWQ_ERR_TOO_LARGE;
+    if (M == 0) return AWQ_OK;
+    if (!x || !weight || !out) return AWQ_ERR_NULL_POINTER;
+    if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, 2)) return AWQ_ERR_MISALIGNED;
+    const hipError_t e = launch_fp16_gemv(static_cast<const half_t*>(x), static_cast<const half_t*>(weight),
+                                          static_cast<half_t*>(out), (int)M, (int)N, (int)K,
+                                          static_cast<hipStream_t>(stream));
     return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
 }
 

@@ -62,6 +62,12 @@ struct TileConfig {
     int k_per_split;         // variant 2: K rows per split (multiple of 64)
 };
 
+// out[M, N] = x[M, K] @ w[N, K]^T, fp16 weights (the output projection);
+// M <= 8, K % 8 == 0, K <= fp16_gemv_max_k(), M * K * 2 <= 64 KiB.
+hipError_t launch_fp16_gemv(const half_t* x, const half_t* w, half_t* out, int M, int N, int K, hipStream_t stream);
+int fp16_gemv_max_k();
+int fp16_gemv_blocks(int N);
+
 hipError_t launch_dequant(const uint32_t* qweight, const uint32_t* qzeros, const half_t* scales,
                           half_t* w, int N, int K, hipStream_t stream);
 

@@ -40,7 +40,7 @@ def L():
 def _declared_symbols():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(awq_w4a16_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(awq_(?:w4a16|fp16)_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -296,3 +296,15 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 2
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_fp16_linear_argument_checks(L):
+    """awq_fp16_linear rejects bad calls before any launch (no GPU needed)."""
+    f = L.awq_fp16_linear
+    assert f(None, None, None, 0, 100, 3584, None) == _native.AWQ_OK            # M == 0: no-op
+    assert f(None, None, None, 9, 100, 3584, None) == _native.AWQ_ERR_PATH      # decode sizes only
+    assert f(None, None, None, 1, 100, 12, None) == _native.AWQ_ERR_BAD_DIMS    # K % 8
+    assert f(None, None, None, 1, 0, 3584, None) == _native.AWQ_ERR_BAD_DIMS
+    assert f(None, None, None, -1, 100, 3584, None) == _native.AWQ_ERR_BAD_DIMS
+    assert f(None, None, None, 1, 100, 8192, None) == _native.AWQ_ERR_TOO_LARGE  # K > 4096
+    assert f(None, None, None, 1, 152064, 3584, None) == _native.AWQ_ERR_NULL_POINTER
