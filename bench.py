@@ -106,6 +106,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of timed CPU work")
     ap.add_argument("--no-extras", action="store_true", help="headline only (for profiling runs)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the end-to-end decode extra (its ~230k kernel launches swamp a kernel trace)")
     ap.add_argument("--counter-pass", action="store_true",
                     help="for rocprofv3 --pmc runs: a 64 MiB device copy (calibrates the byte counters), "
                          "then one eager launch of every engine shape at M in {1,4,16}; no timing output")
@@ -320,6 +322,27 @@ def main():
             lm.append(row)
         result["lm_head_fp16_gemv"] = lm
         del lm_ws
+
+    if not args.no_extras and not args.no_e2e:
+        # end-to-end Qwen2-7B-shaped greedy decoding (28 layers, random-init AWQ weights,
+        # 1024-token random prompt, 128 new tokens; torch for the non-GEMM ops)
+        from engine.qwen2_decode import QWEN2_7B, Qwen2AwqDecoder
+
+        torch.cuda.empty_cache()
+        e2e = Qwen2AwqDecoder(QWEN2_7B, max_seq_len=1024 + 128, seed=0, device=dev)
+        prompt = torch.randint(0, QWEN2_7B.vocab_size, (1024,), generator=torch.Generator().manual_seed(1))
+        e2e.generate(prompt, 128)                      # capture + warm-up
+        r = e2e.generate(prompt, 128)
+        result["e2e_decode"] = {
+            "layers": QWEN2_7B.num_layers, "prompt_tokens": 1024, "new_tokens": 128,
+            "prefill_ms": round(r["prefill_s"] * 1e3, 2),
+            "decode_ms_per_token": round(r["decode_s"] / 127 * 1e3, 3),
+            "decode_tokens_per_s": round(r["decode_tokens_per_s"], 1),
+            "note": "greedy, batch 1, one HIP graph replay per token; AWQ linears and lm_head on this "
+                    "build's kernels, the other ops torch",
+        }
+        del e2e
+        torch.cuda.empty_cache()
 
     # ---- CPU baseline: the reference's dequant + matmul on the host --------
     if not args.no_cpu_baseline:
