@@ -77,28 +77,42 @@ class Qwen2AwqDecoder:
     """Random-init Qwen2-shaped model; ``layers`` dicts hold the packed operands."""
 
     def __init__(self, shape: Qwen2Shape = QWEN2_7B, max_seq_len: int = 2048, seed: int = 0,
-                 device: torch.device | str = "cuda:0"):
+                 device: torch.device | str = "cuda:0", weights: dict | None = None):
+        """Random-init weights (seeded), or `weights` as produced by
+        ``engine.awq_checkpoint.load_qwen2_awq`` (embed, lm_head, final_norm,
+        layers: list of dicts with ln1, ln2, qkv, qkv_bias, o, gate_up, down;
+        the AWQ entries are (qweight, qzeros, scales) tuples)."""
         self.s = shape
         self.dev = torch.device(device)
         self.max_seq_len = max_seq_len
-        g = torch.Generator(device=self.dev)
-        g.manual_seed(seed)
         H, I = shape.hidden_size, shape.intermediate_size
         qkv_n = (shape.num_heads + 2 * shape.num_kv_heads) * shape.head_dim
-        self.embed = (torch.randn((shape.vocab_size, H), generator=g, device=self.dev) * 0.02).half()
-        self.lm_head = (torch.randn((shape.vocab_size, H), generator=g, device=self.dev) * 0.02).half()
-        self.final_norm = torch.ones(H, dtype=torch.float16, device=self.dev)
-        self.layers = []
-        for _ in range(shape.num_layers):
-            self.layers.append({
-                "ln1": (1.0 + 0.1 * torch.randn(H, generator=g, device=self.dev)).half(),
-                "ln2": (1.0 + 0.1 * torch.randn(H, generator=g, device=self.dev)).half(),
-                "qkv": _awq_tensors(H, qkv_n, g, self.dev),
-                "qkv_bias": (torch.randn(qkv_n, generator=g, device=self.dev) * 0.02).half(),
-                "o": _awq_tensors(H, H, g, self.dev),
-                "gate_up": _awq_tensors(H, 2 * I, g, self.dev),
-                "down": _awq_tensors(I, H, g, self.dev),
-            })
+        if weights is not None:
+            mv = lambda t: t.to(self.dev)  # noqa: E731
+            self.embed = mv(weights["embed"])
+            self.lm_head = mv(weights["lm_head"])
+            self.final_norm = mv(weights["final_norm"])
+            self.layers = [{k: (tuple(mv(t) for t in v) if isinstance(v, tuple) else mv(v)) for k, v in lw.items()}
+                           for lw in weights["layers"]]
+        else:
+            g = torch.Generator(device=self.dev)
+            g.manual_seed(seed)
+            self.embed = (torch.randn((shape.vocab_size, H), generator=g, device=self.dev) * 0.02).half()
+            self.lm_head = (torch.randn((shape.vocab_size, H), generator=g, device=self.dev) * 0.02).half()
+            self.final_norm = torch.ones(H, dtype=torch.float16, device=self.dev)
+            self.layers = []
+            for _ in range(shape.num_layers):
+                self.layers.append({
+                    "ln1": (1.0 + 0.1 * torch.randn(H, generator=g, device=self.dev)).half(),
+                    "ln2": (1.0 + 0.1 * torch.randn(H, generator=g, device=self.dev)).half(),
+                    "qkv": _awq_tensors(H, qkv_n, g, self.dev),
+                    "qkv_bias": (torch.randn(qkv_n, generator=g, device=self.dev) * 0.02).half(),
+                    "o": _awq_tensors(H, H, g, self.dev),
+                    "gate_up": _awq_tensors(H, 2 * I, g, self.dev),
+                    "down": _awq_tensors(I, H, g, self.dev),
+                })
+        if len(self.layers) != shape.num_layers:
+            raise ValueError(f"{len(self.layers)} layers of weights for a {shape.num_layers}-layer shape")
         hd = shape.head_dim
         inv = 1.0 / (shape.rope_theta ** (torch.arange(0, hd, 2, device=self.dev, dtype=torch.float32) / hd))
         t = torch.arange(max_seq_len, device=self.dev, dtype=torch.float32)

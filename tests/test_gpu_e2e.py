@@ -141,3 +141,20 @@ def test_e2e_greedy_tokens_follow_reference(gpu):
         if margin > 2e-2:    # the reference's choice is clear at the kernels' error level
             assert tok == int(torch.argmax(lr)), f"token {i}"
         ids.append(tok)
+
+
+def test_e2e_from_checkpoint_matches_in_memory_model(gpu, tmp_path):
+    """A model written as an AutoAWQ checkpoint and read back by the loader
+    gives the same logits and greedy tokens, bit for bit."""
+    from engine.awq_checkpoint import load_qwen2_awq, save_qwen2_awq
+
+    m = Qwen2AwqDecoder(TINY, max_seq_len=64, seed=21, device=gpu)
+    w = {"embed": m.embed, "lm_head": m.lm_head, "final_norm": m.final_norm, "layers": m.layers}
+    save_qwen2_awq(str(tmp_path), TINY, w, shard_layers=1)
+    shape, w2, unused = load_qwen2_awq(str(tmp_path))
+    assert shape == TINY and unused == []
+    m2 = Qwen2AwqDecoder(shape, max_seq_len=64, device=gpu, weights=w2)
+    prompt = torch.randint(0, TINY.vocab_size, (19,), generator=torch.Generator().manual_seed(4))
+    print("e2e tiny: checkpoint round trip", flush=True)
+    assert torch.equal(m.prefill(prompt), m2.prefill(prompt))
+    assert m.generate(prompt, 6)["tokens"].tolist() == m2.generate(prompt, 6)["tokens"].tolist()
