@@ -226,6 +226,29 @@ int awq_w4a16_gemm_planned(const void* x, const int32_t* qweight, const int32_t*
 int awq_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales,
                       void* w_out, int64_t N, int64_t K, int32_t group_size, void* stream);
 
+/* The GEMM with the reference's elementwise follow-ups fused into its final
+ * store: out = fp16(x @ W), then + bias[n] when bias is non-NULL, then
+ * + residual[m, n] when residual is non-NULL, each add done in fp32 and
+ * rounded to fp16 -- bit-identical to awq_w4a16_gemm followed by the
+ * reference's `out + bias` (QKV bias, model/qwen2.py:45-46,108-109) and
+ * `residual + out` (after o_proj / down_proj, :219-227) on torch fp16
+ * tensors, without their two extra passes over [M, N].  bias is fp16 [N],
+ * residual fp16 [M, N] (2-byte aligned; residual may alias out).  plan NULL
+ * = the AUTO plan (as awq_w4a16_gemm), else a plan from awq_w4a16_plan_*
+ * checked against the shape (as awq_w4a16_gemm_planned). */
+int awq_w4a16_gemm_epilogue(const void* x, const int32_t* qweight, const int32_t* qzeros,
+                            const void* scales, const void* bias, const void* residual, void* out,
+                            int64_t M, int64_t N, int64_t K, int32_t group_size, void* workspace,
+                            size_t workspace_bytes, const awq_w4a16_plan* plan, void* stream);
+
+/* out[m, i] = fp16(silu(g) * u), g = gate_up[m, i], u = gate_up[m, I + i], in
+ * fp32 with one rounding: the reference's silu_mul (kernels/silu_mul.py:17-39)
+ * over the fused gate||up projection read in place, replacing its two
+ * .contiguous() copies and the silu_mul pass (model/qwen2.py:187-194) by one
+ * pass.  gate_up fp16 [M, 2I], out fp16 [M, I], both 16-byte aligned,
+ * I % 8 == 0. */
+int awq_silu_mul(const void* gate_up, void* out, int64_t M, int64_t I, void* stream);
+
 /* out[M,N] = x[M,K] @ weight[N,K]^T in fp16 with fp32 accumulation: the
  * fp16 output projection (lm_head) of model/qwen2.py:253,280
  * (nn.Linear(hidden_size, vocab_size, bias=False), applied at :280), at

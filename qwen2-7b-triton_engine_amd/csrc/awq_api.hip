@@ -544,9 +544,11 @@ int check_pointers(const void* x, const void* qweight, const void* qzeros, const
 
 int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const void* scales,
              void* out, int64_t M, int64_t N, int64_t K, void* workspace, const awq_w4a16_plan& p,
-             void* stream) {
+             void* stream, const void* bias = nullptr, const void* residual = nullptr) {
     if (M == 0) return AWQ_OK;
     GemmArgs a;
+    a.bias = static_cast<const half_t*>(bias);
+    a.residual = static_cast<const half_t*>(residual);
     a.x = static_cast<const half_t*>(x);
     a.qweight = reinterpret_cast<const uint32_t*>(qweight);
     a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
@@ -773,6 +775,44 @@ int awq_w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const void*
                                         reinterpret_cast<const uint32_t*>(qzeros),
                                         static_cast<const half_t*>(scales), static_cast<half_t*>(w_out),
                                         (int)N, (int)K, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
+}
+
+int awq_w4a16_gemm_epilogue(const void* x, const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                            const void* bias, const void* residual, void* out, int64_t M, int64_t N, int64_t K,
+                            int32_t group_size, void* workspace, size_t workspace_bytes,
+                            const awq_w4a16_plan* plan, void* stream) {
+    if (M > 0 && ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 2)))) return AWQ_ERR_MISALIGNED;
+    awq_w4a16_plan p;
+    if (plan) {
+        int st = check_dims(M, N, K, group_size);
+        if (st != AWQ_OK) return st;
+        st = check_plan(M, N, K, plan);
+        if (st != AWQ_OK) return st;
+        st = check_pointers(x, qweight, qzeros, scales, out, M);
+        if (st != AWQ_OK) return st;
+        if (M > 0 && plan->workspace_bytes > 0) {
+            if (!workspace || workspace_bytes < plan->workspace_bytes) return AWQ_ERR_WORKSPACE;
+            if (!aligned(workspace, 16)) return AWQ_ERR_MISALIGNED;
+        }
+        p = *plan;
+    } else {
+        const int st = awq_w4a16_validate(x, qweight, qzeros, scales, out, M, N, K, group_size, workspace,
+                                          workspace_bytes, AWQ_PATH_AUTO);
+        if (st != AWQ_OK) return st;
+        awq_w4a16_plan_for(M, N, K, group_size, AWQ_PATH_AUTO, &p);
+    }
+    return run_plan(x, qweight, qzeros, scales, out, M, N, K, workspace, p, stream, bias, residual);
+}
+
+int awq_silu_mul(const void* gate_up, void* out, int64_t M, int64_t I, void* stream) {
+    if (M < 0 || I <= 0 || I % 8 != 0) return AWQ_ERR_BAD_DIMS;
+    if (M * 2 * I > kBytesLimit / 2) return AWQ_ERR_TOO_LARGE;
+    if (M == 0) return AWQ_OK;
+    if (!gate_up || !out) return AWQ_ERR_NULL_POINTER;
+    if (!aligned(gate_up, 16) || !aligned(out, 16)) return AWQ_ERR_MISALIGNED;
+    const hipError_t e = launch_silu_mul(static_cast<const half_t*>(gate_up), static_cast<half_t*>(out), (int)M,
+                                         (int)I, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
 }
 

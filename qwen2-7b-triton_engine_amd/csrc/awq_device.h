@@ -188,18 +188,48 @@ __device__ __forceinline__ unsigned long long fixed_point_word(float p) {
 // `now` = the slot's value after this workgroup's add (returned old value
 // plus its word): the last of split_k arrivals writes the output and clears
 // the slot.
+// The value stored for one output element: fp16 of the fp32 sum, then, when
+// given, + bias[n] and + residual[m, n], each add done in fp32 and rounded
+// to fp16 -- the reference's unfused sequence (out = awq_gemm_forward(...);
+// out + bias, model/qwen2.py:45-46,108-109; residual + out, :219-227; torch
+// adds fp16 tensors in fp32 and rounds), so a fused epilogue and the unfused
+// calls agree bit for bit.  bias_n / res point at the element (or are null).
+__device__ __forceinline__ half_t epi_round(float y, const half_t* bias_n, const half_t* res) {
+    half_t h = (half_t)y;
+    if (bias_n) h = (half_t)((float)h + (float)*bias_n);
+    if (res) h = (half_t)((float)*res + (float)h);
+    return h;
+}
+// V consecutive outputs out[m, n .. n+V-1] (V = 4 or 8, n % V == 0) as one
+// vector store, with the epilogue above.
+template <int V>
+__device__ __forceinline__ void store_out(half_t* out, const half_t* bias, const half_t* residual, int N, int m,
+                                          int n, const float (&y)[V]) {
+    typedef _Float16 hv_t __attribute__((ext_vector_type(V)));
+    hv_t h;
+    const size_t o = (size_t)m * N + n;
+    if (!bias && !residual) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) h[i] = (half_t)y[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) h[i] = epi_round(y[i], bias ? bias + n + i : nullptr, residual ? residual + o + i : nullptr);
+    }
+    *reinterpret_cast<hv_t*>(out + o) = h;
+}
 __device__ __forceinline__ void fixed_point_complete(unsigned long long now, unsigned long long* slot, half_t* out,
-                                                     int split_k) {
+                                                     int split_k, const half_t* bias_n, const half_t* res) {
     if ((int)(now & 0xFFull) == split_k) {
         const long long s = (long long)now >> 8;
-        *out = (half_t)((float)s * (1.0f / 16777216.0f));
+        *out = epi_round((float)s * (1.0f / 16777216.0f), bias_n, res);
         __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
-__device__ __forceinline__ void fixed_add_finish(float p, unsigned long long* slot, half_t* out, int split_k) {
+__device__ __forceinline__ void fixed_add_finish(float p, unsigned long long* slot, half_t* out, int split_k,
+                                                 const half_t* bias_n, const half_t* res) {
     const unsigned long long v = fixed_point_word(p);
     const unsigned long long old = __hip_atomic_fetch_add(slot, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    fixed_point_complete(old + v, slot, out, split_k);
+    fixed_point_complete(old + v, slot, out, split_k, bias_n, res);
 }
 
 // Last-arriving workgroup of a split-K output range: for rows row0 ..
@@ -220,7 +250,8 @@ __device__ __forceinline__ void fixed_add_finish(float p, unsigned long long* sl
 // zero slots, and both share the workspace).
 // `fin` holds blockDim.x float4.  Must be called by the whole workgroup.
 template <int U>
-__device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t* __restrict__ out, int M, int N,
+__device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t* __restrict__ out,
+                                              const half_t* bias, const half_t* residual, int M, int N,
                                               int row0, int nrows, int col0, int ncols, int split_k,
                                               floatx4* fin) {
     const int quads = ncols / 4;
@@ -235,8 +266,8 @@ __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t*
         return (uint32_t)(((size_t)m * N + n) * 4);
     };
     auto store = [&](int m, int n, floatx4 s) {
-        const half4_t h = {(half_t)s[0], (half_t)s[1], (half_t)s[2], (half_t)s[3]};
-        *reinterpret_cast<half4_t*>(out + (size_t)m * N + n) = h;
+        const float y[4] = {s[0], s[1], s[2], s[3]};
+        store_out<4>(out, bias, residual, N, m, n, y);
     };
     if (items < nt) {
         const int P = min(8, nt / items);

@@ -116,10 +116,7 @@ __global__ __launch_bounds__(512) void awq_gemv_kernel(GemmArgs a, int kw_count,
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             if (m >= a.M) break;
-            half8_t h;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) h[c] = (half_t)acc[m][c];
-            *reinterpret_cast<half8_t*>(a.out + (size_t)m * a.N + 8 * j) = h;
+            store_out<8>(a.out, a.bias, a.residual, a.N, m, 8 * j, acc[m]);
         }
         return;
     }
@@ -142,7 +139,7 @@ __global__ __launch_bounds__(512) void awq_gemv_kernel(GemmArgs a, int kw_count,
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<2>(rp, a.out, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
+    splitk_finish<2>(rp, a.out, a.bias, a.residual, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
     if (threadIdx.x == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -299,10 +296,7 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             if (m >= a.M) break;
-            half8_t h;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) h[c] = (half_t)acc[m][c];
-            *reinterpret_cast<half8_t*>(a.out + (size_t)m * a.N + 8 * j) = h;
+            store_out<8>(a.out, a.bias, a.residual, a.N, m, 8 * j, acc[m]);
         }
         return;
     }
@@ -325,7 +319,7 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<2>(rp, a.out, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
+    splitk_finish<2>(rp, a.out, a.bias, a.residual, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
     if (threadIdx.x == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -482,10 +476,7 @@ __global__ __launch_bounds__(1024) void awq_gemv_col_kernel(GemmArgs a) {
             for (int w = 0; w < 16; ++w)
 #pragma unroll
                 for (int c = 0; c < 8; ++c) o[c] += red[((w * MR + m) * P + pp) * 8 + c];
-            half8_t h;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) h[c] = (half_t)o[c];
-            *reinterpret_cast<half8_t*>(a.out + (size_t)m * a.N + 8 * jo) = h;
+            store_out<8>(a.out, a.bias, a.residual, a.N, m, 8 * jo, o);
         }
     }
 }
@@ -773,8 +764,10 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
             float sum = 0.f;
             for (int w = 0; w < nw; ++w) sum += red[(w * MR + m) * 512 + t];
             half_t* o = a.out + (size_t)m * a.N + col;
-            if (split_k == 1) *o = (half_t)sum;
-            else fixed_add_finish(sum, fix + (size_t)m * a.N + col, o, split_k);
+            const half_t* bn = a.bias ? a.bias + col : nullptr;
+            const half_t* rs = a.residual ? a.residual + (size_t)m * a.N + col : nullptr;
+            if (split_k == 1) *o = epi_round(sum, bn, rs);
+            else fixed_add_finish(sum, fix + (size_t)m * a.N + col, o, split_k, bn, rs);
         }
     }
 }

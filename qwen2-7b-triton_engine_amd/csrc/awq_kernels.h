@@ -17,6 +17,8 @@ struct GemmArgs {
     half_t* out;             // [M, N]
     float* partials;         // [split_k, M, N] when split_k > 1
     int M, N, K;
+    const half_t* bias = nullptr;      // [N] added to every row (epilogue), or null
+    const half_t* residual = nullptr;  // [M, N] added after the bias (epilogue), or null; may alias out
 };
 
 struct SkinnyConfig {
@@ -67,6 +69,9 @@ struct TileConfig {
 hipError_t launch_fp16_gemv(const half_t* x, const half_t* w, half_t* out, int M, int N, int K, hipStream_t stream);
 int fp16_gemv_max_k();
 int fp16_gemv_blocks(int N);
+
+// out[m, i] = fp16(silu(gate_up[m, i]) * gate_up[m, I + i]); I % 8 == 0.
+hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int M, int I, hipStream_t stream);
 
 hipError_t launch_dequant(const uint32_t* qweight, const uint32_t* qzeros, const half_t* scales,
                           half_t* w, int N, int K, hipStream_t stream);

@@ -211,10 +211,10 @@ __global__ __launch_bounds__(512) void awq_narrow_kernel(GemmArgs a, int chunks_
             for (int i = 0; i < 4; ++i) {
                 const int m = 4 * mb + i;
                 if (m >= a.M) continue;
-                half8_t h;
+                float y[8];
 #pragma unroll
-                for (int c = 0; c < 8; ++c) h[c] = (half_t)tot[mb][c][i];
-                *reinterpret_cast<half8_t*>(a.out + (size_t)m * a.N + 8 * j) = h;
+                for (int c = 0; c < 8; ++c) y[c] = tot[mb][c][i];
+                store_out<8>(a.out, a.bias, a.residual, a.N, m, 8 * j, y);
             }
         return;
     }
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(512) void awq_narrow_kernel(GemmArgs a, int chunks_
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<2>(rp, a.out, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
+    splitk_finish<2>(rp, a.out, a.bias, a.residual, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
     if (threadIdx.x == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

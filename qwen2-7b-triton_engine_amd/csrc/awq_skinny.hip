@@ -248,10 +248,10 @@ __global__ __launch_bounds__(512) void awq_skinny_kernel(GemmArgs a, int rows_pe
             for (int ii = 0; ii < 4; ++ii) {
                 const int m = 16 * b + 4 * kq + ii;
                 if (m >= a.M) continue;
-                half8_t h;
+                float y[8];
 #pragma unroll
-                for (int c = 0; c < 8; ++c) h[c] = (half_t)tot[b][c][ii];
-                *reinterpret_cast<half8_t*>(a.out + (size_t)m * a.N + 8 * j) = h;
+                for (int c = 0; c < 8; ++c) y[c] = tot[b][c][ii];
+                store_out<8>(a.out, a.bias, a.residual, a.N, m, 8 * j, y);
             }
         return;
     }
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(512) void awq_skinny_kernel(GemmArgs a, int rows_pe
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<4>(rp, a.out, a.M, a.N, 0, a.M, pair * 2 * kSkinnyCols, min(2 * kSkinnyCols, a.N - pair * 2 * kSkinnyCols),
+    splitk_finish<4>(rp, a.out, a.bias, a.residual, a.M, a.N, 0, a.M, pair * 2 * kSkinnyCols, min(2 * kSkinnyCols, a.N - pair * 2 * kSkinnyCols),
                   split_k, fin);
     if (threadIdx.x == 0) __hip_atomic_store(&counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

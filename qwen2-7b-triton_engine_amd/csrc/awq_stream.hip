@@ -177,7 +177,7 @@ __device__ __forceinline__ void stream_finish(const GemmArgs& a, int split_k, ui
                         (uint32_t)(split_k - 1);
         __syncthreads();
         if (!last_flag) return;
-        splitk_finish<2>(rp, a.out, a.M, a.N, 0, a.M, strip * 512, ncols, split_k, reinterpret_cast<floatx4*>(red));
+        splitk_finish<2>(rp, a.out, a.bias, a.residual, a.M, a.N, 0, a.M, strip * 512, ncols, split_k, reinterpret_cast<floatx4*>(red));
         if (threadIdx.x == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
@@ -204,7 +204,10 @@ __device__ __forceinline__ void stream_finish(const GemmArgs& a, int split_k, ui
         if (split_k == 1) {
 #pragma unroll
             for (int b = 0; b < BATCH; ++b)
-                if (ok[b]) a.out[(size_t)m[b] * a.N + col[b]] = (half_t)sum[b];
+                if (ok[b])
+                    a.out[(size_t)m[b] * a.N + col[b]] =
+                        epi_round(sum[b], a.bias ? a.bias + col[b] : nullptr,
+                                  a.residual ? a.residual + (size_t)m[b] * a.N + col[b] : nullptr);
             continue;
         }
         unsigned long long now[BATCH];
@@ -217,8 +220,10 @@ __device__ __forceinline__ void stream_finish(const GemmArgs& a, int split_k, ui
         }
 #pragma unroll
         for (int b = 0; b < BATCH; ++b)
-            if (ok[b]) fixed_point_complete(now[b], fix + (size_t)m[b] * a.N + col[b], a.out + (size_t)m[b] * a.N + col[b],
-                                            split_k);
+            if (ok[b])
+                fixed_point_complete(now[b], fix + (size_t)m[b] * a.N + col[b], a.out + (size_t)m[b] * a.N + col[b],
+                                     split_k, a.bias ? a.bias + col[b] : nullptr,
+                                     a.residual ? a.residual + (size_t)m[b] * a.N + col[b] : nullptr);
     }
 }
 }  // namespace
@@ -478,7 +483,8 @@ __global__ __launch_bounds__(R == 2 ? 512 : 256) void awq_stream_kernel(GemmArgs
 // partials read are overwritten with zeros, so the workspace is zero again
 // when the kernel ends.
 __global__ __launch_bounds__(256) void awq_splitk_reduce_kernel(float* __restrict__ partials, half_t* __restrict__ out,
-                                                               int M, int N, int split_k, int P) {
+                                                               const half_t* bias, const half_t* residual, int M,
+                                                               int N, int split_k, int P) {
     __shared__ floatx4 fin[256];
     const int qpb = 256 / P;  // output quads per workgroup
     const int t = threadIdx.x;
@@ -500,8 +506,9 @@ __global__ __launch_bounds__(256) void awq_splitk_reduce_kernel(float* __restric
     __syncthreads();
     if (valid && part == 0) {
         for (int i = 1; i < P; ++i) s += fin[i * qpb + t];
-        const half4_t h = {(half_t)s[0], (half_t)s[1], (half_t)s[2], (half_t)s[3]};
-        *reinterpret_cast<half4_t*>(out + (size_t)q * 4) = h;
+        const float y[4] = {s[0], s[1], s[2], s[3]};
+        const int m = (int)(((size_t)q * 4) / N);
+        store_out<4>(out, bias, residual, N, m, q * 4 - m * N, y);
     }
 }
 
@@ -537,7 +544,7 @@ int64_t stream_reduce_blocks(int M, int N, int split_k) {
 hipError_t splitk_reduce_launch(const GemmArgs& a, int split_k, hipStream_t stream) {
     const int P = stream_reduce_parts(split_k);
     hipLaunchKernelGGL(awq_splitk_reduce_kernel, dim3((unsigned)stream_reduce_blocks(a.M, a.N, split_k)), dim3(256), 0,
-                       stream, a.partials, a.out, a.M, a.N, split_k, P);
+                       stream, a.partials, a.out, a.bias, a.residual, a.M, a.N, split_k, P);
     return hipGetLastError();
 }
 

@@ -152,9 +152,8 @@ __global__ __launch_bounds__(256) void awq_tile_kernel_v1(GemmArgs a) {
         for (int x = 0; x < 4; ++x) {
             const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
             if (gn >= a.N) continue;
-            const half4_t h = {(half_t)acc[x][y][0], (half_t)acc[x][y][1], (half_t)acc[x][y][2],
-                               (half_t)acc[x][y][3]};
-            *reinterpret_cast<half4_t*>(a.out + (size_t)gm * a.N + gn) = h;
+            const float v[4] = {acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]};
+            store_out<4>(a.out, a.bias, a.residual, a.N, gm, gn, v);
         }
     }
 }
@@ -330,9 +329,8 @@ __global__ __launch_bounds__(256, 2) void awq_tile_kernel_v2(GemmArgs a, int spl
             for (int x = 0; x < 4; ++x) {
                 const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
                 if (gn >= a.N) continue;
-                const half4_t h = {(half_t)acc[x][y][0], (half_t)acc[x][y][1], (half_t)acc[x][y][2],
-                                   (half_t)acc[x][y][3]};
-                *reinterpret_cast<half4_t*>(a.out + (size_t)gm_ * a.N + gn) = h;
+                const float v[4] = {acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]};
+                store_out<4>(a.out, a.bias, a.residual, a.N, gm_, gn, v);
             }
         }
         return;
@@ -358,7 +356,7 @@ __global__ __launch_bounds__(256, 2) void awq_tile_kernel_v2(GemmArgs a, int spl
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<16>(rp, a.out, a.M, a.N, m0, min(T2_BM, a.M - m0), n0, min(T2_BN, a.N - n0), split_k, fin);
+    splitk_finish<16>(rp, a.out, a.bias, a.residual, a.M, a.N, m0, min(T2_BM, a.M - m0), n0, min(T2_BN, a.N - n0), split_k, fin);
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -657,9 +655,8 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
             for (int x = 0; x < 4; ++x) {
                 const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
                 if (gn >= a.N) continue;
-                const half4_t h = {(half_t)acc[x][y][0], (half_t)acc[x][y][1], (half_t)acc[x][y][2],
-                                   (half_t)acc[x][y][3]};
-                *reinterpret_cast<half4_t*>(a.out + (size_t)gm_ * a.N + gn) = h;
+                const float v[4] = {acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]};
+                store_out<4>(a.out, a.bias, a.residual, a.N, gm_, gn, v);
             }
         }
         return;
@@ -685,7 +682,7 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<16>(rp_, a.out, a.M, a.N, m0, min(T3_BM, a.M - m0), n0, min(T3_BN, a.N - n0), split_k, fin);
+    splitk_finish<16>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(T3_BM, a.M - m0), n0, min(T3_BN, a.N - n0), split_k, fin);
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -995,9 +992,8 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (pc0 + r >= pn) continue;
-                const half4_t hv = {(half_t)acc[0][f][r], (half_t)acc[1][f][r], (half_t)acc[2][f][r],
-                                    (half_t)acc[3][f][r]};
-                *reinterpret_cast<half4_t*>(a.out + (size_t)m * a.N + 8 * (pc0 + r) + coff) = hv;
+                const float v[4] = {acc[0][f][r], acc[1][f][r], acc[2][f][r], acc[3][f][r]};
+                store_out<4>(a.out, a.bias, a.residual, a.N, m, 8 * (pc0 + r) + coff, v);
             }
         }
         return;
@@ -1024,7 +1020,7 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<16>(rp_, a.out, a.M, a.N, m0, min(BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin);
+    splitk_finish<16>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin);
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -7,9 +7,11 @@ run by ``kernels.awq_gemm.awq_gemm_forward`` (fused QKV with the q/k/v biases,
 ``model/qwen2.py:79-85,104-113``; fused gate||up, ``:174-188``), the logits
 come from the fp16 lm_head GEMV (``kernels.lm_head``, ``:253,280``), and the
 non-GEMM work -- embedding, RMSNorm (``:15-22``), rotate-half RoPE
-(``kernels/rope.py:41-57``), GQA attention over a static KV cache,
-SiLU * up, residuals -- is plain torch (attention in fp32 on contiguous
-operands).  Logits are computed for the last position only, where the
+(``kernels/rope.py:41-57``), GQA attention over a static KV cache -- is
+plain torch (attention in fp32 on contiguous operands).  The QKV bias and
+the residual adds after o_proj and down_proj run in the GEMM's epilogue,
+and SiLU * up reads the fused gate||up output in one kernel
+(``kernels.silu_mul``).  Logits are computed for the last position only, where the
 reference computes them for every position and keeps the last
 (``inference/engine.py:93,127``).
 
@@ -27,8 +29,9 @@ import time
 
 import torch
 
-from kernels.awq_gemm import awq_gemm_forward
+from kernels.awq_gemm import awq_gemm_forward, awq_gemm_forward_ex
 from kernels.lm_head import lm_head_forward
+from kernels.silu_mul import silu_mul_gate_up
 
 __all__ = ["Qwen2Shape", "QWEN2_7B", "Qwen2AwqDecoder"]
 
@@ -125,8 +128,13 @@ class Qwen2AwqDecoder:
         self._graph = None
 
     # ---- linear layers: the path this build replaces -------------------------
-    def linear(self, x: torch.Tensor, op) -> torch.Tensor:
-        return awq_gemm_forward(x, *op)
+    def linear(self, x: torch.Tensor, op, bias: torch.Tensor | None = None,
+               residual: torch.Tensor | None = None) -> torch.Tensor:
+        """AWQ projection; ``bias`` and ``residual`` are added in the GEMM's
+        epilogue, rounded as torch's fp16 ``residual + (x @ W + bias)``."""
+        if bias is None and residual is None:
+            return awq_gemm_forward(x, *op)
+        return awq_gemm_forward_ex(x, *op, bias=bias, residual=residual)
 
     # ---- one decoder layer over positions `pos` (device int64 [S]) -------------
     def _layer(self, li: int, h: torch.Tensor, pos: torch.Tensor, causal: bool) -> torch.Tensor:
@@ -135,7 +143,7 @@ class Qwen2AwqDecoder:
         S = h.shape[0]
         nh, kvh, hd = s.num_heads, s.num_kv_heads, s.head_dim
         x = _rmsnorm(h, p["ln1"], s.rms_norm_eps)
-        qkv = self.linear(x, p["qkv"]) + p["qkv_bias"]
+        qkv = self.linear(x, p["qkv"], bias=p["qkv_bias"])
         q = qkv[:, :nh * hd].view(S, nh, hd).float()
         k = qkv[:, nh * hd:(nh + kvh) * hd].view(S, kvh, hd).float()
         v = qkv[:, (nh + kvh) * hd:].view(S, kvh, hd)
@@ -163,12 +171,10 @@ class Qwen2AwqDecoder:
         probs = torch.softmax(scores, dim=-1).view(kvh, groups * S, T)
         att = torch.matmul(probs, vv.contiguous()).view(nh, S, hd)            # [nh, S, hd]
         att = att.transpose(0, 1).reshape(S, nh * hd).half()
-        h = h + self.linear(att, p["o"])
+        h = self.linear(att, p["o"], residual=h)
         x = _rmsnorm(h, p["ln2"], s.rms_norm_eps)
-        gu = self.linear(x, p["gate_up"])
-        I = s.intermediate_size
-        inter = (torch.nn.functional.silu(gu[:, :I].float()) * gu[:, I:].float()).half()
-        return h + self.linear(inter, p["down"])
+        inter = silu_mul_gate_up(self.linear(x, p["gate_up"]))
+        return self.linear(inter, p["down"], residual=h)
 
     def _forward(self, ids: torch.Tensor, pos: torch.Tensor, causal: bool) -> torch.Tensor:
         h = torch.nn.functional.embedding(ids, self.embed)

@@ -88,6 +88,9 @@ SIGNATURES = {
                                               ctypes.c_size_t, ctypes.POINTER(Plan), _VP]),
     "awq_w4a16_dequant": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I32, _VP]),
     "awq_fp16_linear": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _VP]),
+    "awq_w4a16_gemm_epilogue": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
+                                               ctypes.c_size_t, ctypes.POINTER(Plan), _VP]),
+    "awq_silu_mul": (ctypes.c_int, [_VP, _VP, _I64, _I64, _VP]),
 }
 
 _lib = None

@@ -117,8 +117,11 @@ def _prepare(x, qweight, qzeros, scales, group_size):
     return in_shape, x_flat, qweight, qzeros, scales, K, N, dev
 
 
-def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=None, plan_obj=None):
+def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=None, plan_obj=None,
+            bias=None, residual=None):
     L = _native.lib()
+    if (bias is not None or residual is not None) and plan_obj is None:
+        plan_obj = _native.plan_for(M, N, K, group_size, _native.PATH_AUTO if path is None else path)
     if plan_obj is not None:
         ws_bytes = int(plan_obj.workspace_bytes)
     else:
@@ -130,7 +133,12 @@ def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path
     args = (_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out), M, N, K, group_size,
             _ptr(ws), ws_bytes)
     with torch.cuda.device(dev):
-        if plan_obj is not None:
+        if bias is not None or residual is not None:
+            st = L.awq_w4a16_gemm_epilogue(_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(bias),
+                                           _ptr(residual), _ptr(out), M, N, K, group_size, _ptr(ws), ws_bytes,
+                                           ctypes.byref(plan_obj), stream)
+            where = "awq_w4a16_gemm_epilogue"
+        elif plan_obj is not None:
             st = L.awq_w4a16_gemm_planned(*args, ctypes.byref(plan_obj), stream)
             where = "awq_w4a16_gemm_planned"
         elif path is None:
@@ -154,16 +162,30 @@ def awq_gemm_forward(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tenso
 
 def awq_gemm_forward_ex(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
                         scales: torch.Tensor, group_size: int = 128, path: int | None = None,
-                        plan_obj: "_native.Plan | None" = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                        plan_obj: "_native.Plan | None" = None, out: torch.Tensor | None = None,
+                        bias: torch.Tensor | None = None, residual: torch.Tensor | None = None) -> torch.Tensor:
     """``awq_gemm_forward`` with the kernel path forced (``_native.PATH_*``) or an
-    explicit plan (``_native.plan_skinny`` / ``plan``), optionally into ``out``."""
+    explicit plan (``_native.plan_skinny`` / ``plan``), optionally into ``out``,
+    and optionally with the reference's follow-up adds fused into the store:
+    ``bias`` fp16 ``[N]`` (``out + bias``, model/qwen2.py:45-46,108-109) and
+    ``residual`` fp16 ``[..., N]`` (``residual + out``, :219-227), bit-identical
+    to the unfused torch adds.  ``residual`` may be ``out`` itself."""
     in_shape, x_flat, qweight, qzeros, scales, K, N, dev = _prepare(x, qweight, qzeros, scales, group_size)
     M = x_flat.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
-    elif out.dtype != torch.float16 or tuple(out.shape) != (M, N) or not out.is_contiguous() or out.device != dev:
+    elif out.dtype != torch.float16 or out.numel() != M * N or not out.is_contiguous() or out.device != dev:
         raise ValueError("out must be a contiguous fp16 [M, N] tensor on the operands' device")
-    _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=path, plan_obj=plan_obj)
+    if bias is not None:
+        if bias.dtype != torch.float16 or bias.numel() != N or bias.device != dev:
+            raise ValueError(f"bias must be an fp16 [N={N}] tensor on {dev}")
+        bias = bias.contiguous()
+    if residual is not None:
+        if residual.dtype != torch.float16 or residual.numel() != M * N or residual.device != dev:
+            raise ValueError(f"residual must be an fp16 tensor of M*N = {M * N} elements on {dev}")
+        residual = residual.contiguous()
+    _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=path, plan_obj=plan_obj,
+            bias=bias, residual=residual)
     return out.view(*in_shape[:-1], N)
 
 

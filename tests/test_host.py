@@ -40,7 +40,7 @@ def L():
 def _declared_symbols():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(awq_(?:w4a16|fp16)_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(awq_(?:w4a16_|fp16_|silu_)[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol(L):
