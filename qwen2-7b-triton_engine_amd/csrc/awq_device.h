@@ -77,13 +77,21 @@ __device__ __forceinline__ void kpairs_magic(uint32_t a, uint32_t b, uint32_t kp
     }
 }
 
-// (x & mask) | magic in one VALU op.  gfx9 VOP3 encodings cannot carry two
-// literal constants, so the compiler splits this into v_and + v_or; spelling
-// v_and_or_b32 with the mask in an SGPR and the magic in a VGPR keeps it one.
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(magic));
-    return r;
+// (x & mask) | magic.  With the mask a literal (it goes to an SGPR) and the
+// magic in a VGPR the compiler does not know the value of, this is one
+// v_and_or_b32; with both literals it becomes v_and + v_or (gfx9 VOP3
+// encodings carry no literal).  Written in plain C, not inline asm: the
+// compiler inserts the wait states between a VALU write and an MFMA that
+// reads (or is still reading or writing) the same VGPRs only for
+// instructions it generated itself, never around an asm statement.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) { return (x & mask) | magic; }
+// kMagic2 in a VGPR, opaque to the optimiser: a DPP row shift whose
+// out-of-row lanes keep `old` (bound_ctrl off), with old = src = the
+// constant, so every lane holds it.  The compiler cannot fold the DPP move,
+// so and_or(x, mask, magic_vgpr()) stays one v_and_or_b32.
+__device__ __forceinline__ uint32_t magic_vgpr() {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)kMagic2, (int)kMagic2, 0x111 /* row_shr:1 */, 0xF, 0xF,
+                                                 false);
 }
 
 // As kpairs_magic, but without the shifts by 4: nibbles 1 and 3 of each
@@ -92,7 +100,7 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t m
 // out scaled by 16; the matching zero splat is (1024 + 16*z), the difference
 // 16*(q - z) is still exact in fp16, and the caller folds 1/16 into the scale.
 __device__ __forceinline__ void kpairs_magic_x16(uint32_t a, uint32_t b, uint32_t kp[8]) {
-    const uint32_t magic = kMagic2;
+    const uint32_t magic = magic_vgpr();
     const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
     const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
     const uint32_t lo8 = lo >> 8;
@@ -117,13 +125,9 @@ __device__ __forceinline__ uint32_t zero_splat_x16(uint32_t zw, int c) {
     return kMagic2 | zz | (zz << 16);
 }
 
-// a.lo * b.lo + a.hi * b.hi in fp32 from fp16 pairs, starting from zero: the
-// VOP3 form of v_dot2 with an inline-constant accumulator (the compiler
-// otherwise picks the VOP2 form and clears a register first).
+// a.lo * b.lo + a.hi * b.hi in fp32 from fp16 pairs, starting from zero.
 __device__ __forceinline__ float dot2_from_zero(uint32_t a, uint32_t b) {
-    float r;
-    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    return r;
+    return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), 0.0f, false);
 }
 
 __device__ __forceinline__ floatx4 mfma16x16x32(half8_t a, half8_t b, floatx4 c) {
@@ -217,19 +221,77 @@ __device__ __forceinline__ void store_out(half_t* out, const half_t* bias, const
     }
     *reinterpret_cast<hv_t*>(out + o) = h;
 }
+// epi_round with the bias / residual values already loaded (has_* says
+// which of them apply).
+__device__ __forceinline__ half_t epi_round_vals(float y, bool has_bias, half_t bias_v, bool has_res, half_t res_v) {
+    half_t h = (half_t)y;
+    if (has_bias) h = (half_t)((float)h + (float)bias_v);
+    if (has_res) h = (half_t)((float)res_v + (float)h);
+    return h;
+}
+// The sum held by a fixed-point slot value.
+__device__ __forceinline__ float fixed_point_sum(unsigned long long now) {
+    return (float)((long long)now >> 8) * (1.0f / 16777216.0f);
+}
 __device__ __forceinline__ void fixed_point_complete(unsigned long long now, unsigned long long* slot, half_t* out,
                                                      int split_k, const half_t* bias_n, const half_t* res) {
     if ((int)(now & 0xFFull) == split_k) {
-        const long long s = (long long)now >> 8;
-        *out = epi_round((float)s * (1.0f / 16777216.0f), bias_n, res);
+        *out = epi_round(fixed_point_sum(now), bias_n, res);
         __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
-__device__ __forceinline__ void fixed_add_finish(float p, unsigned long long* slot, half_t* out, int split_k,
-                                                 const half_t* bias_n, const half_t* res) {
-    const unsigned long long v = fixed_point_word(p);
-    const unsigned long long old = __hip_atomic_fetch_add(slot, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    fixed_point_complete(old + v, slot, out, split_k, bias_n, res);
+// The last step of B outputs of one thread (out[m[b], n[b]] for the b with
+// ok[b]): a direct store of the fp32 sum when split_k == 1, else the
+// fixed-point finish above, with every memory round trip in flight
+// together -- the bias / residual values are loaded first, then all B
+// atomics are issued, and only then are the returned values examined (a
+// returned value read before the next atomic is issued makes the wave wait
+// for it, and B outputs would cost B round trips).  The bias / residual
+// reads are range-checked buffer loads (a null operand gets a zero-size
+// range and reads 0), so no branch joins a loaded value with a default one,
+// which also makes the wave wait for the load.  Needs M * N * 2 < 2^32
+// (the callers serve M <= 16).
+template <int B>
+__device__ __forceinline__ void finish_batch(unsigned long long* fix, half_t* out, const half_t* bias,
+                                             const half_t* residual, int M, int N, int split_k, const float (&sum)[B],
+                                             const int (&m)[B], const int (&n)[B], const bool (&ok)[B]) {
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias, bias ? (uint32_t)N * 2u : 0u);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(residual, residual ? (uint32_t)((size_t)M * N * 2) : 0u);
+    half_t bv[B], rv[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        const uint32_t o = (uint32_t)m[b] * (uint32_t)N + (uint32_t)n[b];
+        bv[b] = __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(
+                                               rb, ok[b] ? (uint32_t)n[b] * 2u : 0x80000000u, 0, 0));
+        rv[b] = __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(rr, ok[b] ? o * 2u : 0x80000000u,
+                                                                                 0, 0));
+    }
+    if (split_k == 1) {
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+            if (ok[b])
+                out[(size_t)m[b] * N + n[b]] =
+                    epi_round_vals(sum[b], bias != nullptr, bv[b], residual != nullptr, rv[b]);
+        return;
+    }
+    unsigned long long word[B], old[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        word[b] = fixed_point_word(sum[b]);
+        old[b] = 0ull;
+        if (ok[b])
+            old[b] = __hip_atomic_fetch_add(fix + (size_t)m[b] * N + n[b], word[b], __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        const unsigned long long now = old[b] + word[b];
+        if (ok[b] && (int)(now & 0xFFull) == split_k) {
+            const size_t o = (size_t)m[b] * N + n[b];
+            out[o] = epi_round_vals(fixed_point_sum(now), bias != nullptr, bv[b], residual != nullptr, rv[b]);
+            __hip_atomic_store(fix + o, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // Last-arriving workgroup of a split-K output range: for rows row0 ..

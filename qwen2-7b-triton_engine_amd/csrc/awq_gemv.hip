@@ -755,21 +755,26 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
                     floatx4{acc[m][i], acc[m][i + 1], acc[m][i + 2], acc[m][i + 3]};
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < 512; t += blockDim.x) {
-        const int col = strip * 512 + t;
-        if (col >= a.N) break;
+    // Thread t finishes outputs t, t + nt, ... of the strip (at most 512 / 64
+    // = 8 per row of x) in one batch: one memory round trip per thread.
+    constexpr int kOwn = 512 / 64;
+    float fs[kOwn * MR];
+    int fm[kOwn * MR], fn[kOwn * MR];
+    bool fok[kOwn * MR];
+#pragma unroll
+    for (int i = 0; i < kOwn; ++i)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            if (m >= a.M) break;
-            float sum = 0.f;
-            for (int w = 0; w < nw; ++w) sum += red[(w * MR + m) * 512 + t];
-            half_t* o = a.out + (size_t)m * a.N + col;
-            const half_t* bn = a.bias ? a.bias + col : nullptr;
-            const half_t* rs = a.residual ? a.residual + (size_t)m * a.N + col : nullptr;
-            if (split_k == 1) *o = epi_round(sum, bn, rs);
-            else fixed_add_finish(sum, fix + (size_t)m * a.N + col, o, split_k, bn, rs);
+            const int t = threadIdx.x + i * nt;
+            float s = 0.f;
+            if (t < 512)
+                for (int w = 0; w < nw; ++w) s += red[(w * MR + m) * 512 + t];
+            fs[i * MR + m] = s;
+            fm[i * MR + m] = m;
+            fn[i * MR + m] = strip * 512 + t;
+            fok[i * MR + m] = t < 512 && strip * 512 + t < a.N && m < a.M;
         }
-    }
+    finish_batch<kOwn * MR>(fix, a.out, a.bias, a.residual, a.M, a.N, split_k, fs, fm, fn, fok);
 }
 
 // Groups a workgroup's chunk range can touch: at most ceil(per / 4) + 1.

@@ -182,11 +182,12 @@ __device__ __forceinline__ void stream_finish(const GemmArgs& a, int split_k, ui
         return;
     }
 
-    // Fixed-point finish (or the direct store when split_k == 1): all
-    // atomics of a batch are issued before their returns are examined.
+    // Fixed-point finish (or the direct store when split_k == 1): every
+    // output of the thread in one batch (512 threads: MP outputs each), all
+    // atomics in flight together.
     unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
     const int items = mrows * 512;
-    constexpr int BATCH = 4;
+    constexpr int BATCH = MP;
     for (int base = threadIdx.x; base < items; base += BATCH * nt) {
         float sum[BATCH];
         int col[BATCH], m[BATCH];
@@ -201,29 +202,7 @@ __device__ __forceinline__ void stream_finish(const GemmArgs& a, int split_k, ui
             if (ok[b])
                 for (int w = 0; w < nred; ++w) sum[b] += red[(w * MP + m[b]) * 512 + it % 512];
         }
-        if (split_k == 1) {
-#pragma unroll
-            for (int b = 0; b < BATCH; ++b)
-                if (ok[b])
-                    a.out[(size_t)m[b] * a.N + col[b]] =
-                        epi_round(sum[b], a.bias ? a.bias + col[b] : nullptr,
-                                  a.residual ? a.residual + (size_t)m[b] * a.N + col[b] : nullptr);
-            continue;
-        }
-        unsigned long long now[BATCH];
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const unsigned long long v = fixed_point_word(sum[b]);
-            now[b] = ok[b] ? __hip_atomic_fetch_add(fix + (size_t)m[b] * a.N + col[b], v, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT) + v
-                           : 0ull;
-        }
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b)
-            if (ok[b])
-                fixed_point_complete(now[b], fix + (size_t)m[b] * a.N + col[b], a.out + (size_t)m[b] * a.N + col[b],
-                                     split_k, a.bias ? a.bias + col[b] : nullptr,
-                                     a.residual ? a.residual + (size_t)m[b] * a.N + col[b] : nullptr);
+        finish_batch<BATCH>(fix, a.out, a.bias, a.residual, a.M, a.N, split_k, sum, m, col, ok);
     }
 }
 }  // namespace

@@ -874,6 +874,7 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
     };
 
     // v_perm selectors (byte 0x0C reads as zero), as variant 5.
+    const uint32_t magic = magic_vgpr();  // for one v_and_or_b32 per k-pair
     const uint32_t sel_even = hh ? 0x0C050C01u : 0x0C040C00u;
     const uint32_t sel_odd = hh ? 0x0C070C03u : 0x0C060C02u;
     const int jl = 8 * wn + (n16 & 7);  // lane's packed column within the tile
@@ -913,7 +914,7 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
                 const uint32_t od = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_odd);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, kMagic2);
+                    const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, magic);
                     af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
                 }
             }
