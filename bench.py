@@ -87,14 +87,14 @@ FAMILY_KERNELS = {
     "skinny": ("awq_skinny",),
     "narrow": ("awq_narrow",),
     "stream": ("awq_stream", "awq_splitk_reduce"),
-    "tile": ("awq_tile",),
+    "tile": ("awq_tile", "awq_splitk_reduce"),
 }
 FAMILY_NAMES = {
     "gemv": "awq_gemv_quad_kernel",
     "skinny": "awq_skinny_kernel",
     "narrow": "awq_narrow_kernel",
     "stream": "awq_stream_row_kernel / awq_stream_kernel (+ awq_splitk_reduce_kernel)",
-    "tile": "awq_tile_kernel",
+    "tile": "awq_tile_kernel (+ awq_splitk_reduce_kernel)",
 }
 
 
