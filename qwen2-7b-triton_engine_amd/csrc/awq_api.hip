@@ -349,6 +349,17 @@ int stream_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     int64_t variant = 1;
     if (split > 1 && M > 4) variant = M * split <= 32 ? 2 : 3;
     if (variant == 1 && split > kFixMaxSplit) variant = 3;
+    if (!row && split > 1) {
+        // Half layout (9 <= M <= 16), measured on 3584 x 37888 (split 3) and
+        // 18944 x 3584 (split 36) at M = 9, 12, 16: fewer wave pairs per
+        // workgroup -- two for a few splits, three for many -- and the reduce
+        // launch as the finish, 0.7 - 1.4 us faster than four pairs.
+        const int64_t kw_half = split <= 8 ? 2 : 3;
+        if (stream_fits((int)M, (int)K, (int)split, (int)kw_half, (int)layout) &&
+            stream_lds_bytes((int)M, (int)K, (int)split, (int)kw_half, (int)layout) <= kStreamLdsBudget &&
+            fill_stream(M, N, K, layout, 3, kw_half, split, depth, p) == AWQ_OK)
+            return AWQ_OK;
+    }
     return fill_stream(M, N, K, layout, variant, kw, split, depth, p);
 }
 
