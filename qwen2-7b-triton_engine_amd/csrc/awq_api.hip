@@ -465,16 +465,16 @@ double tile_cost(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t sp
 // variants unsplit only; split no further than 7/4 workgroups per CU).
 // Measured on the Qwen2-7B prefill GEMMs (qkv, o, gate||up, down) at
 // M = 32 .. 2048.
-// 8 <= M <= 16 on weights the stream path does not take (narrow and
+// 5 <= M <= 16 on weights the stream path does not take (narrow and
 // shallow: fewer than 16 strips of 512 columns, K < 8192): the 32-row
-// register-dequant tile (variant 9) split along K -- 28 ways at M = 8, 14
-// above, in whole 128-row units -- measured 0.5 - 2.4 us faster than the
-// skinny kernel on 3584 x 4608 and 3584 x 3584 (qkv and o of Qwen2-7B).
+// register-dequant tile (variant 9) split 14 ways along K (in whole 128-row
+// units) measured 1.0 - 3.3 us faster than the skinny kernel on 3584 x 4608
+// and 3584 x 3584 (qkv and o of Qwen2-7B), and faster than 28 or 7 splits.
 // Only where that grid covers at least half the CUs; else AWQ_ERR_PATH.
 int small_m_tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    if (M < 8 || M > 16) return AWQ_ERR_PATH;
+    if (M < 5 || M > 16) return AWQ_ERR_PATH;
     const int64_t units = K / kGroup;
-    int64_t split = M <= 8 ? 28 : 14;
+    int64_t split = 14;
     if (split > units) split = units;
     const int64_t per = (units + split - 1) / split;
     split = (units + per - 1) / per;

@@ -75,7 +75,7 @@ def test_plan_struct_matches_header():
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("k,n", SHAPES)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 8, 12, 16, 17, 33, 64, 65, 128, 512, 2048, 2049])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 12, 16, 17, 33, 64, 65, 128, 512, 2048, 2049])
 def test_auto_plan_invariants(L, m, k, n):
     p = _native.plan_for(m, n, k)
     strips = -(-(n // 8) // 64)            # 512-column strips of the stream path
@@ -87,12 +87,12 @@ def test_auto_plan_invariants(L, m, k, n):
         assert p.tile_m >= m
         assert p.split_k <= k // 128
     elif m <= 16:
-        # 8 <= M <= 16: the 32-row tile split along K where its grid covers
-        # half the CUs, else the skinny kernel
+        # 5 <= M <= 16: the 32-row tile split 14 ways along K where its grid
+        # covers half the CUs, else the skinny kernel
         units = k // 128
-        split = min(28 if m <= 8 else 14, units)
+        split = min(14, units)
         split = -(-units // -(-units // split))
-        small_tile = m >= 8 and -(-n // 256) * split * 2 >= 256
+        small_tile = m >= 5 and -(-n // 256) * split * 2 >= 256
         if small_tile:
             assert p.path == _native.PATH_TILE and p.variant == 9 and p.split_k == split
         else:
