@@ -317,3 +317,27 @@ def test_fp16_linear_argument_checks(L):
     assert f(None, None, None, -1, 100, 3584, None) == _native.AWQ_ERR_BAD_DIMS
     assert f(None, None, None, 1, 100, 8192, None) == _native.AWQ_ERR_TOO_LARGE  # K > 4096
     assert f(None, None, None, 1, 152064, 3584, None) == _native.AWQ_ERR_NULL_POINTER
+
+
+# ---------------------------------------------------------------------------
+# Kernel sources
+# ---------------------------------------------------------------------------
+
+def test_no_valu_inline_asm_in_kernels():
+    """No inline asm spells a vector ALU instruction.  The compiler inserts
+    the wait states between a VALU write and an MFMA that reads the same
+    registers (or between an MFMA and a VALU touching its operands) only
+    around instructions it generated itself; an asm v_and_or_b32 feeding an
+    MFMA has produced wrong output columns.  Scalar instructions and the
+    LDS-direct buffer loads (with their own s_nop after the M0 write) stay."""
+    csrc = os.path.join(ROOT, "qwen2-7b-triton_engine_amd", "csrc")
+    offenders = []
+    for name in sorted(os.listdir(csrc)):
+        if not name.endswith((".hip", ".h")):
+            continue
+        text = open(os.path.join(csrc, name)).read()
+        for m in re.finditer(r"\basm\s*(?:volatile\s*)?\((.*?)\)\s*;", text, re.S):
+            body = "".join(re.findall(r'"((?:[^"\\]|\\.)*)"', m.group(1).split(":")[0]))
+            if re.search(r"\bv_[a-z0-9_]+", body):
+                offenders.append(f"{name}: {body.strip()[:60]}")
+    assert offenders == [], offenders
