@@ -51,7 +51,7 @@ typedef enum awq_w4a16_path {
     AWQ_PATH_AUTO = 0,
     AWQ_PATH_SKINNY = 1,         /* decode: MFMA skinny-M streaming kernel (M <= 64)         */
     AWQ_PATH_TILE = 2,           /* prefill: LDS-tiled MFMA GEMM                            */
-    AWQ_PATH_GEMV = 3,           /* decode: VALU dot2 GEMV (M <= 2)                         */
+    AWQ_PATH_GEMV = 3,           /* decode: column-quad GEMV, MFMA or dot2 sums (M <= 2)    */
     AWQ_PATH_NARROW = 4,         /* decode: K-streaming 4x4x4 MFMA kernel (M <= 16)         */
     AWQ_PATH_STREAM = 5          /* decode: streaming 16x16x32 MFMA kernels (M <= 16)         */
 } awq_w4a16_path;
@@ -175,7 +175,7 @@ int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, i
  * workspace here holds, for split-K launches, a block of uint32 arrival
  * counters (first awq_w4a16_counter_bytes() bytes) followed by either the
  * fp32 partial sums [split_k, M, N] or one 64-bit fixed-point slot per
- * output element [M, N] (GEMV variant 4 and the stream path).  The whole
+ * output element [M, N] (GEMV variants 4, 5 and stream variant 1).  The whole
  * workspace must be zero-filled before it is first used; every call leaves
  * it zero again, so one zeroed workspace serves any number of calls of any
  * path, as long as calls that share it do not run concurrently.  Returns 0
