@@ -159,6 +159,25 @@ def test_gemm_decode_shapes(gpu, name, m):
         _assert_close(y, y_ref, f"{name} M={m} path={path}")
 
 
+@pytest.mark.parametrize("m,k,n,path,variant,k_waves", [
+    (5, 3584, 4608, "tile", 9, None), (8, 3584, 3592, "tile", 9, None), (13, 2048, 4104, "tile", 9, None),
+    (16, 1152, 6144, "tile", 9, None),
+    (9, 3584, 8224, "stream", 3, 3), (13, 8192, 1056, "stream", 3, 3), (12, 2048, 16384, "stream", 3, 2)])
+def test_auto_small_m_routes(gpu, m, k, n, path, variant, k_waves):
+    """The AUTO routes for 5 <= M <= 16: the 32-row tile split along K on
+    narrow shallow weights (N not a multiple of 256, splits that do not
+    divide K evenly), and the half-strip stream kernel with two or three
+    wave pairs on wide or deep ones; each against the oracle."""
+    p = _native.plan_for(m, n, k)
+    assert _native.PATH_NAMES[p.path] == path and p.variant == variant
+    if k_waves is not None:
+        assert p.k_waves == k_waves
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=m + n)
+    y_ref = x.astype(np.float64) @ O.dequant_awq_f32eval(qw, qz, s).astype(np.float64)
+    print(f"auto route M={m} K={k} N={n} {path} v{p.variant} split={p.split_k}", flush=True)
+    _assert_close(_run(gpu, x, qw, qz, s), y_ref, f"auto M={m} K={k} N={n}")
+
+
 @pytest.mark.parametrize("m", [1, 8, 64, 512, 2048])
 def test_gemm_down_m_sweep(gpu, m):
     k, n = _SHAPES["down_proj"]
