@@ -19,6 +19,21 @@
  * synchronises the host or keeps mutable global state, so every call is
  * reentrant and can be captured into a HIP graph.  Every entry point returns
  * AWQ_OK (0) or a negative awq_w4a16_status.
+ *
+ * A GEMM call is one kernel launch, or two on the same stream when its plan
+ * adds split-K partials in a second launch of a reduce kernel: tile
+ * variants 7, 8, 9, 11 and 12 and stream variant 3 with split_k > 1.
+ *
+ * Numerics.  Every path computes in fp32 from the exact integer q - z.  The
+ * tile paths and the per-weight skinny mode round each weight to fp16 as
+ * the reference does (fp16((q - z) * s), one rounding, for every fp16
+ * scale); the GEMV, stream and factored skinny paths multiply the fp32 sum
+ * of x * (q - z) over a 128-row group by the scale instead (no per-weight
+ * rounding: they stay finite where a reference weight would overflow).
+ * The fixed-point split-K finish (GEMV variants 4 and 5, stream variant 1)
+ * clamps each workgroup's partial sum to +-2^22 and turns a NaN partial
+ * into +2^22, so a NaN or an infinity in x gives +-inf (never NaN) on those
+ * paths; partials are added in 2^-24 steps.
  */
 #ifndef AWQ_W4A16_H
 #define AWQ_W4A16_H
@@ -30,7 +45,7 @@
 extern "C" {
 #endif
 
-#define AWQ_W4A16_ABI_VERSION 1
+#define AWQ_W4A16_ABI_VERSION 2
 
 typedef enum awq_w4a16_status {
     AWQ_OK = 0,
@@ -52,13 +67,12 @@ typedef enum awq_w4a16_path {
     AWQ_PATH_SKINNY = 1,         /* decode: MFMA skinny-M streaming kernel (M <= 64)         */
     AWQ_PATH_TILE = 2,           /* prefill: LDS-tiled MFMA GEMM                            */
     AWQ_PATH_GEMV = 3,           /* decode: column-quad GEMV, MFMA or dot2 sums (M <= 2)    */
-    AWQ_PATH_NARROW = 4,         /* decode: K-streaming 4x4x4 MFMA kernel (M <= 16)         */
-    AWQ_PATH_STREAM = 5          /* decode: streaming 16x16x32 MFMA kernels (M <= 16)         */
+    AWQ_PATH_STREAM = 5          /* decode: streaming 16x16x32 MFMA kernels (M <= 16)       */
 } awq_w4a16_path;
 
 /* What the dispatcher will launch for a shape (host-side description). */
 typedef struct awq_w4a16_plan {
-    int32_t path;                /* AWQ_PATH_SKINNY, _TILE, _GEMV, _NARROW or _STREAM      */
+    int32_t path;                /* AWQ_PATH_SKINNY, _TILE, _GEMV or _STREAM                */
     int32_t variant;             /* kernel variant inside the path                          */
     int32_t tile_m;              /* rows of x per work unit (skinny: 16, 32 or 64)          */
     int32_t tile_n;              /* output columns per work unit                            */
@@ -98,23 +112,22 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
                           int32_t rows_per_wave, int32_t k_waves, int32_t variant,
                           int32_t factored_scale, awq_w4a16_plan* plan);
 
-/* Host-only: a tile-path plan (variant 1: 128x128x32 tiles; variant 2:
- * 128x128x64 tiles with prefetch; variant 3: 256x128x64 tiles, x streamed
+/* Host-only: a tile-path plan.  Variant 4: 256x128x64 tiles, x streamed
  * into a 3-stage LDS ring by direct loads, weights dequantised once per
- * k-step into an LDS W^T buffer; variant 4: variant 3 with the next k-step's
- * dequant interleaved with this k-step's MFMAs; variants 5 and 6: 256x256x64
- * (eight wavefronts, one workgroup per CU) and 128x256x64 (four wavefronts,
- * two workgroups per CU) tiles, each wavefront 128 x rows x 64 columns,
- * weights dequantised straight into MFMA operand registers, x, raw weights
- * and zeros/scales brought by direct global->LDS loads two k-steps ahead
- * into a 3-stage ring; variants 7, 8, 9: 128-, 64- and 32-row tiles of the
- * same kernel (two, three, four workgroups per CU) whose split-K partials are
+ * k-step into an LDS W^T buffer, the next k-step's dequant interleaved with
+ * this k-step's MFMAs.  Variant 6: 128x256x64 tiles (four wavefronts, two
+ * workgroups per CU), each wavefront 128 x rows x 64 columns, weights
+ * dequantised straight into MFMA operand registers, x, raw weights and
+ * zeros/scales brought by direct global->LDS loads two k-steps ahead into a
+ * 3-stage ring; variants 7, 8, 9: 128-, 64- and 32-row tiles of the same
+ * kernel (two, three, four workgroups per CU) whose split-K partials are
  * summed by a second, whole-device launch; variants 10, 11, 12: 128-, 128-
  * and 64-row tiles with two wavefronts per SIMD from one workgroup, each
  * taking one k-half of every k-step (10: last-arriver split-K finish, 11 and
- * 12: the second launch); variants 2..12 take split_k >= 1 workgroups along
- * K, variants 5 and up in whole 128-row groups).  For variants 2..12 the
- * plan's rows_per_wave holds the K rows per split. */
+ * 12: the second launch).  Every variant takes split_k >= 1 workgroups
+ * along K (variants 6 and up in whole 128-row groups); the plan's
+ * rows_per_wave holds the K rows per split.  Other variant numbers:
+ * AWQ_ERR_PATH. */
 int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 
@@ -126,15 +139,11 @@ int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
  * chunk of the workgroup's share of K; split_k 1 .. min(K/32, 255) workgroups
  * share each strip's K evenly; split-K partials meet in 64-bit fixed-point
  * workspace slots.
- * variant 1 (all loads issued at once): tile_n 512; rows_per_wave 16, 32 or
- * 64; k_waves 1, 2, 4 or 8; split_k and depth must be 0 (split_k is derived).
  * variant 2 (K-streaming, one 128-row group per step): tile_n 512;
  * rows_per_wave 16 or 32, k_waves = 128 / rows_per_wave, split_k in
  * 1 .. K/128 with every split a whole number of groups, depth = chunks in
  * flight per wave (2 .. 4 for 16 rows per wave, 2 .. 3 for 32).
- * variant 3 (one workgroup per column strip over the whole K, no workspace):
- * tile_n 32, 64, 128 or 256 output columns per workgroup; rows_per_wave 0;
- * k_waves 16; split_k 1; depth 2 or 3 iterations in flight. */
+ * Other variants: AWQ_ERR_PATH. */
 int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t variant,
                         int32_t tile_n, int32_t rows_per_wave, int32_t k_waves, int32_t split_k,
                         int32_t depth, awq_w4a16_plan* plan);
@@ -159,16 +168,6 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
 int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
                           int32_t variant, int32_t k_waves, int32_t split_k, int32_t depth,
                           awq_w4a16_plan* plan);
-/* Host-only: a narrow-M plan (M <= 16): the K-streaming schedule of GEMV
- * variant 2 with v_mfma_f32_4x4x4_16b_f16 arithmetic.  rows_per_wave 16 or
- * 32 (128 / rows_per_wave waves per workgroup); split_k in 1 .. K/128 with
- * every split a whole number of 128-row groups; depth = groups in flight
- * per wave (2 or 3; 2 for 32 rows per wave); factored_scale 1 = zero and
- * scale applied to group sums (M <= 8), 0 = fp16 weight (q - z) * s formed
- * per weight as the reference does. */
-int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
-                          int32_t split_k, int32_t depth, int32_t factored_scale, awq_w4a16_plan* plan);
-
 /* Host-only: bytes of workspace awq_w4a16_gemm needs for this shape
  * (0 if none).  Replaces the module-global _dequant_buffer of
  * kernels/awq_gemm.py:234,255-262, which holds K*N fp16 values; the

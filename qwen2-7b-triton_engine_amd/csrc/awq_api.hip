@@ -116,12 +116,10 @@ constexpr int64_t kGemvMaxM = 2;
 // LDS the column-quad GEMV may stage per workgroup.
 constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 
-// Variants 1 and 2 use 512-column strips (tile_n = 512).  Variant 1:
-// split_k and depth are derived / unused (pass 0).  Variant 2: k_waves = 128 /
+// 512-column strips (tile_n = 512).  Variant 2: k_waves = 128 /
 // rows_per_wave, split_k in 1 .. K/128 with each split a whole number of
-// groups, depth 2 .. 4 chunk buffers (3 at most for 32 rows).  Variant 3:
-// tile_n 32 .. 256 columns per workgroup over the whole K, rows_per_wave 0,
-// k_waves 16, split_k 1, depth 2 or 3.
+// groups, depth 2 .. 4 chunk buffers (3 at most for 32 rows).  Variants 4
+// and 5: see below.
 int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, int64_t rows_per_wave,
               int64_t k_waves, int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
     if (M > kGemvMaxM) return AWQ_ERR_PATH;
@@ -134,18 +132,6 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
     p->block_threads = (int32_t)(64 * k_waves);
     p->factored_scale = 1;
     p->depth = 0;
-    if (variant == 3) {
-        // One workgroup of 16 waves per tile_n-column strip, whole K.
-        if (!(tile_n == 32 || tile_n == 64 || tile_n == 128 || tile_n == 256)) return AWQ_ERR_PATH;
-        if (rows_per_wave != 0 || k_waves != 16 || split_k != 1 || depth < 2 || depth > 3) return AWQ_ERR_PATH;
-        p->tile_n = (int32_t)tile_n;
-        p->split_k = 1;
-        p->depth = (int32_t)depth;
-        p->grid = gemv_col_blocks((int)N, (int)(tile_n / 8));
-        p->workspace_bytes = 0;
-        p->lds_bytes = 0;
-        return AWQ_OK;
-    }
     if (tile_n != 512) return AWQ_ERR_PATH;
     if (variant == 4 || variant == 5) {
         // Column quads (5: MFMA column sums): N % 32 == 0; rows_per_wave 0;
@@ -168,14 +154,7 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
         if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
         return AWQ_OK;
     }
-    if (variant == 1) {
-        if (split_k != 0 || depth != 0) return AWQ_ERR_PATH;
-        if (!(rows_per_wave == 16 || rows_per_wave == 32 || rows_per_wave == 64)) return AWQ_ERR_PATH;
-        if (!(k_waves == 1 || k_waves == 2 || k_waves == 4 || k_waves == 8)) return AWQ_ERR_PATH;
-        const int64_t rows_per_block = rows_per_wave * k_waves;
-        p->split_k = (int32_t)((K + rows_per_block - 1) / rows_per_block);
-        p->grid = gemv_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
-    } else if (variant == 2) {
+    if (variant == 2) {
         if (!(rows_per_wave == 16 || rows_per_wave == 32) || k_waves * rows_per_wave != kGroup) return AWQ_ERR_PATH;
         if (depth < 2 || depth > (rows_per_wave == 16 ? 4 : 3)) return AWQ_ERR_PATH;
         p->depth = (int32_t)depth;
@@ -231,40 +210,6 @@ int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_gemv(M, N, K, 2, 512, 16, 8, stream_split(N, K), 3, p);
 }
 
-constexpr int64_t kNarrowMaxM = 16;
-
-int fill_narrow(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t split_k, int64_t depth,
-                int64_t factored, awq_w4a16_plan* p) {
-    if (M > kNarrowMaxM) return AWQ_ERR_PATH;
-    if (!(rows_per_wave == 16 || rows_per_wave == 32)) return AWQ_ERR_PATH;
-    if (depth < 2 || depth > (rows_per_wave == 16 ? 3 : 2)) return AWQ_ERR_PATH;
-    // Only the per-weight mode is served: the group-factored mode gave
-    // non-finite, run-to-run different outputs at M = 1 with split-K.
-    if (factored != 0) return AWQ_ERR_PATH;
-    const int mb = narrow_blocks_for((int)M);
-    const int64_t groups = K / kGroup;
-    if (split_k < 1 || split_k > groups) return AWQ_ERR_PATH;
-    const int64_t per = (groups + split_k - 1) / split_k;
-    if ((groups + per - 1) / per != split_k) return AWQ_ERR_PATH;
-    if (split_k > 1 && gemv_strips((int)N) * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
-    p->path = AWQ_PATH_NARROW;
-    p->variant = 1;
-    p->tile_m = 4 * mb;
-    p->tile_n = 512;
-    p->rows_per_wave = (int32_t)rows_per_wave;
-    p->k_waves = (int32_t)(kGroup / rows_per_wave);
-    p->split_k = (int32_t)split_k;
-    p->block_threads = 64 * p->k_waves;
-    p->factored_scale = (int32_t)factored;
-    p->depth = (int32_t)depth;
-    p->grid = gemv_strips((int)N) * split_k;
-    p->workspace_bytes =
-        split_k > 1 ? skinny_counter_bytes() + (uint64_t)split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
-    p->lds_bytes = 0;
-    if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
-    return AWQ_OK;
-}
-
 // Split count of the K-streaming kernels: as many K splits as keep the grid
 // within one workgroup per CU, at least 2 groups per split.
 int64_t stream_split(int64_t N, int64_t K) {
@@ -275,10 +220,6 @@ int64_t stream_split(int64_t N, int64_t K) {
     if (split < 1) split = 1;
     const int64_t per = (groups + split - 1) / split;
     return (groups + per - 1) / per;
-}
-
-int narrow_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    return fill_narrow(M, N, K, 16, stream_split(N, K), 2, 0, p);
 }
 
 // Stream path (M <= 16): 16x16x32 MFMA, zero/scale folded once per 128-row
@@ -384,27 +325,19 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->factored_scale = 0;
     p->depth = 0;
     p->lds_bytes = 0;
-    if (variant == 3 || variant == 4) {
+    if (!tile_variant_served((int)variant) || split_k < 1) return AWQ_ERR_PATH;
+    if (variant == 4) {
         p->tile_m = 256;
         p->block_threads = 512;
-    }
-    if (variant >= 5 && variant <= kTileVariants) {
+    } else {
         p->tile_m = tile5_rows((int)variant);
         p->tile_n = 256;
         p->block_threads = tile5_threads((int)variant);
     }
     const int64_t tiles = tile_tiles((int)M, (int)N, (int)variant);
-    if (variant == 1) {
-        if (split_k != 1) return AWQ_ERR_PATH;
-        p->split_k = 1;
-        p->grid = tiles;
-        p->workspace_bytes = 0;
-        return AWQ_OK;
-    }
-    if (variant < 2 || variant > kTileVariants || split_k < 1) return AWQ_ERR_PATH;
-    // K range per split: a multiple of the 64-row k-step (variants 5 and up: of
+    // K range per split: a multiple of the 64-row k-step (variants 6 and up: of
     // the 128-row group, two k-steps).
-    const int64_t unit = variant >= 5 ? 128 : 64;
+    const int64_t unit = variant >= 6 ? 128 : 64;
     const int64_t steps = K / unit;
     const int64_t per = (steps + split_k - 1) / split_k;
     const int64_t s = (steps + per - 1) / per;
@@ -549,15 +482,12 @@ int check_plan(int64_t M, int64_t N, int64_t K, const awq_w4a16_plan* p) {
     } else if (p->path == AWQ_PATH_TILE) {
         const int st = fill_tile(M, N, K, p->variant, p->split_k, &q);
         if (st != AWQ_OK) return st;
-    } else if (p->path == AWQ_PATH_NARROW) {
-        const int st = fill_narrow(M, N, K, p->rows_per_wave, p->split_k, p->depth, p->factored_scale, &q);
-        if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_STREAM) {
         const int st = fill_stream(M, N, K, p->rows_per_wave, p->variant, p->k_waves, p->split_k, p->depth, &q);
         if (st != AWQ_OK) return st;
     } else if (p->path == AWQ_PATH_GEMV) {
-        const int st = fill_gemv(M, N, K, p->variant, p->tile_n, p->rows_per_wave, p->k_waves,
-                                 p->variant == 1 ? 0 : p->split_k, p->depth, &q);
+        const int st = fill_gemv(M, N, K, p->variant, p->tile_n, p->rows_per_wave, p->k_waves, p->split_k,
+                                 p->depth, &q);
         if (st != AWQ_OK) return st;
     } else {
         return AWQ_ERR_PATH;
@@ -615,18 +545,6 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
                          : nullptr;
         e = launch_stream(a, p.split_k, p.k_waves, p.depth, p.rows_per_wave, p.variant - 1,
                           static_cast<uint32_t*>(workspace), s);
-    } else if (p.path == AWQ_PATH_NARROW) {
-        NarrowConfig cfg;
-        cfg.rows_per_wave = p.rows_per_wave;
-        cfg.split_k = p.split_k;
-        const int64_t groups = K / kGroup;
-        cfg.chunks_per_split = (int)((groups + p.split_k - 1) / p.split_k);
-        cfg.depth = p.depth;
-        cfg.factored = p.factored_scale != 0;
-        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                              skinny_counter_bytes())
-                                   : nullptr;
-        e = launch_narrow(a, cfg, static_cast<uint32_t*>(workspace), s);
     } else if (p.path == AWQ_PATH_GEMV) {
         GemvConfig cfg;
         cfg.variant = p.variant;
@@ -636,7 +554,6 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         const int64_t groups = K / kGroup;
         cfg.chunks_per_split = (int)((groups + p.split_k - 1) / p.split_k);
         cfg.depth = p.depth;
-        if (p.variant == 3) cfg.rows_per_wave = p.tile_n / 8;  // packed columns per workgroup
         a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                                               skinny_counter_bytes())
                                    : nullptr;
@@ -712,14 +629,6 @@ int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, i
     return fill_stream(M, N, K, rows_per_wave, variant, k_waves, split_k, depth, plan);
 }
 
-int awq_w4a16_plan_narrow(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
-                          int32_t split_k, int32_t depth, int32_t factored_scale, awq_w4a16_plan* plan) {
-    if (!plan) return AWQ_ERR_NULL_POINTER;
-    const int d = check_dims(M, N, K, group_size);
-    if (d != AWQ_OK) return d;
-    return fill_narrow(M, N, K, rows_per_wave, split_k, depth, factored_scale, plan);
-}
-
 int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t path,
                        awq_w4a16_plan* plan) {
     if (!plan) return AWQ_ERR_NULL_POINTER;
@@ -733,7 +642,6 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
             return auto_skinny(M, N) ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);
         case AWQ_PATH_SKINNY: return skinny_plan(M, N, K, plan);
         case AWQ_PATH_GEMV: return gemv_plan(M, N, K, plan);
-        case AWQ_PATH_NARROW: return narrow_plan(M, N, K, plan);
         case AWQ_PATH_STREAM: return stream_plan(M, N, K, plan);
         case AWQ_PATH_TILE: return tile_plan(M, N, K, plan);
         default: return AWQ_ERR_PATH;

@@ -94,35 +94,50 @@ __device__ __forceinline__ uint32_t magic_vgpr() {
                                                  false);
 }
 
-// As kpairs_magic, but without the shifts by 4: nibbles 1 and 3 of each
-// half-word are masked in place (mask 0x00F000F0), which yields the fp16
-// value 1024 + 16*q.  Columns 2, 3, 6, 7 (c with bit 1 set) therefore come
-// out scaled by 16; the matching zero splat is (1024 + 16*z), the difference
-// 16*(q - z) is still exact in fp16, and the caller folds 1/16 into the scale.
-__device__ __forceinline__ void kpairs_magic_x16(uint32_t a, uint32_t b, uint32_t kp[8]) {
+// fp16 pair (64.0, 64.0).  The unit in the last place of 64 is 1/16, so a
+// code c held in mantissa bits 4..7 (the integer 16c in the mantissa field)
+// reads as 64 + c: a nibble can be cut out of a word in place, without a
+// shift, and still give an exact fp16 code.
+constexpr uint32_t kMagic2Hi = 0x54005400u;
+// kMagic2Hi in a VGPR (see magic_vgpr).
+__device__ __forceinline__ uint32_t magic_hi_vgpr() {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)kMagic2Hi, (int)kMagic2Hi, 0x111 /* row_shr:1 */, 0xF, 0xF,
+                                                 false);
+}
+
+// As kpairs_magic, with half the shifts by 4: nibbles 1 and 3 of each
+// half-word are masked in place (mask 0x00F000F0) and read with the 64.0
+// magic, which yields the fp16 value 64 + q.  Columns 2, 3, 6, 7 (c with bit
+// 1 set) therefore carry the offset 64, the others 1024 (magic_base); with
+// the matching zero splat (zero_splat_inplace) the difference q - z is exact
+// for every column, so fp16((q - z) * s) rounds once, as the reference does.
+__device__ __forceinline__ void kpairs_magic_inplace(uint32_t a, uint32_t b, uint32_t kp[8]) {
     const uint32_t magic = magic_vgpr();
+    const uint32_t magic_hi = magic_hi_vgpr();
     const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
     const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
     const uint32_t lo8 = lo >> 8;
     const uint32_t hi8 = hi >> 8;
     kp[0] = and_or(lo, 0x000F000Fu, magic);
-    kp[2] = and_or(lo, 0x00F000F0u, magic);
+    kp[2] = and_or(lo, 0x00F000F0u, magic_hi);
     kp[4] = and_or(lo8, 0x000F000Fu, magic);
-    kp[6] = and_or(lo8, 0x00F000F0u, magic);
+    kp[6] = and_or(lo8, 0x00F000F0u, magic_hi);
     kp[1] = and_or(hi, 0x000F000Fu, magic);
-    kp[3] = and_or(hi, 0x00F000F0u, magic);
+    kp[3] = and_or(hi, 0x00F000F0u, magic_hi);
     kp[5] = and_or(hi8, 0x000F000Fu, magic);
-    kp[7] = and_or(hi8, 0x00F000F0u, magic);
+    kp[7] = and_or(hi8, 0x00F000F0u, magic_hi);
 }
 
-// Whether kpairs_magic_x16 returns logical column c scaled by 16.
-__device__ __forceinline__ constexpr bool x16_column(int c) { return (c >> 1) & 1; }
+// Whether kpairs_magic_inplace reads logical column c with the 64.0 magic.
+__device__ __forceinline__ constexpr bool inplace_column(int c) { return (c >> 1) & 1; }
+// The offset kpairs_magic_inplace adds to the code of logical column c.
+__device__ __forceinline__ constexpr float magic_base(int c) { return inplace_column(c) ? 64.0f : 1024.0f; }
 
-// Zero splat matching kpairs_magic_x16 for logical column c.
-__device__ __forceinline__ uint32_t zero_splat_x16(uint32_t zw, int c) {
+// Zero splat matching kpairs_magic_inplace for logical column c: the fp16
+// pair (base + z, base + z).
+__device__ __forceinline__ uint32_t zero_splat_inplace(uint32_t zw, int c) {
     const uint32_t z = (zw >> col_shift(c)) & 0xFu;
-    const uint32_t zz = x16_column(c) ? (z << 4) : z;
-    return kMagic2 | zz | (zz << 16);
+    return inplace_column(c) ? (kMagic2Hi | (z << 4) | (z << 20)) : (kMagic2 | z | (z << 16));
 }
 
 // a.lo * b.lo + a.hi * b.hi in fp32 from fp16 pairs, starting from zero.

@@ -1,153 +1,25 @@
 // Decode GEMV (M <= 2) of the W4A16 AWQ GEMM for gfx950.
 //
 // At batch 1 the kernel is a pure stream of the int4 weights, and the time
-// is set by how many bytes are in flight against the HBM latency.  So:
-//
-// * lane l of a wave owns one packed column j = 64*strip + l (8 output
-//   columns), and the wave reads whole 256-byte row segments (64 lanes x one
-//   dword of the same row), rows r0 .. r0+R-1 of its K range;
-// * all R loads of a wave are issued at once, before any arithmetic, and a
-//   wave is small (about 70 VGPRs), so many waves per SIMD keep the HBM queue
-//   full;
-// * no MFMA: with one or two rows of x the 16x16 MFMA tile would be mostly
-//   padding.  Each pair of rows (r, r+1) of a packed column is turned into
-//   fp16 k-pairs (v_perm_b32 + magic-number decode, see awq_device.h), the
-//   zero is subtracted exactly in fp16 and v_dot2_f32_f16 accumulates
-//   x[r]*(q[r]-z) + x[r+1]*(q[r+1]-z) in fp32;
-// * x is uniform across the wave: its row pairs are read with scalar loads
-//   into SGPRs, the second dot2 operand;
-// * a wave covers R rows of one 128-row group, so the scale multiplies its
-//   fp32 sum once at the end.
-//
-// Workgroup = KW waves on the same strip and consecutive K ranges; their
-// sums are added through LDS.  Several workgroups along K (split_k > 1)
-// finish in one launch exactly as the skinny kernel does: device-scope
-// partials [split, M, N], an arrival counter per strip, the last workgroup
-// adds the partials in split order and resets the counter.
+// is set by how many bytes are in flight against the HBM latency and by the
+// split-K finish at the end.  Two kernels:
+//  * variant 2 (awq_gemv_stream_kernel): one 128-row group per step, lane =
+//    packed column, v_dot2_f32_f16 sums; serves N % 32 != 0;
+//  * variants 4 and 5 (awq_gemv_quad_kernel): column quads, 16-byte loads,
+//    interleaved 32-row chunks, fixed-point split-K finish; the default.
+// Both handle the zero outside the dot products: the codes are read as
+// fp16 (b + q) by the magic-number unpack (b = 1024, or 64 for the nibbles
+// cut in place, see awq_device.h), the lanes accumulate
+// sum_r x[r] * (b + q[r]) and sum_r x[r], and each group folds
+// s * (that - (b + z) * sum_r x[r]) in fp32 once.
 #include "awq_kernels.h"
 
 namespace awq {
 
-template <int MR, int R>
-__global__ __launch_bounds__(512) void awq_gemv_kernel(GemmArgs a, int kw_count, int split_k,
-                                                       uint32_t* counters) {
-    __shared__ float red[7 * MR * 8 * 64];
-    __shared__ int last_flag;
-    __shared__ floatx4 fin[512];
-    const int lane = threadIdx.x & 63;
-    const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int pn = a.N >> 3;
-    const int n_strips = (pn + 63) / 64;
-    const int strip = blockIdx.x % n_strips;
-    const int split = blockIdx.x / n_strips;
-    const int j = strip * 64 + lane;
-    const bool col_ok = j < pn;
-    const int jc = col_ok ? j : pn - 1;
-    const int r0 = (split * kw_count + kw) * R;
-    const bool active = r0 < a.K;  // wave-uniform
-
-    float acc[MR][8];
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[m][c] = 0.f;
-
-    if (active) {
-        const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
-        const uint32_t row_bytes = (uint32_t)pn * 4u;
-        const uint32_t voff = (uint32_t)jc * 4u;
-        uint32_t w[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) w[i] = buf_load_b32(rw, voff, (uint32_t)(r0 + i) * row_bytes);
-        const int g = r0 / kGroup;
-        const uint32_t zw = a.qzeros[(size_t)g * pn + jc];
-        const half8_t s8 = *reinterpret_cast<const half8_t*>(a.scales + (size_t)g * a.N + 8 * jc);
-        // x row pairs (x[r], x[r+1]) as fp16 pairs; the index is wave-uniform.
-        const uint32_t* x32 = reinterpret_cast<const uint32_t*>(a.x);
-        uint32_t xp[MR][R / 2];
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int p = 0; p < R / 2; ++p)
-                xp[m][p] = __builtin_amdgcn_readfirstlane(x32[((size_t)m * a.K + r0) / 2 + p]);
-        uint32_t zs[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) zs[c] = zero_splat_x16(zw, c);
-#pragma unroll
-        for (int p = 0; p < R / 2; ++p) {
-            uint32_t kp[8];
-            kpairs_magic_x16(w[2 * p], w[2 * p + 1], kp);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const half2_t d = as_h2(kp[c]) - as_h2(zs[c]);
-#pragma unroll
-                for (int m = 0; m < MR; ++m)
-                    acc[m][c] = __builtin_amdgcn_fdot2(d, as_h2(xp[m][p]), acc[m][c], false);
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const float sc = (float)s8[c] * (x16_column(c) ? 0.0625f : 1.0f);
-#pragma unroll
-            for (int m = 0; m < MR; ++m) acc[m][c] *= sc;
-        }
-    }
-
-    // K reduction inside the workgroup through LDS ([wave][m][c][lane]).
-    if (kw_count > 1) {
-        if (kw > 0) {
-#pragma unroll
-            for (int m = 0; m < MR; ++m)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) red[(((kw - 1) * MR + m) * 8 + c) * 64 + lane] = acc[m][c];
-        }
-        __syncthreads();
-        if (kw == 0) {
-            for (int q = 1; q < kw_count; ++q)
-#pragma unroll
-                for (int m = 0; m < MR; ++m)
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) acc[m][c] += red[(((q - 1) * MR + m) * 8 + c) * 64 + lane];
-        }
-    }
-
-    if (split_k == 1) {
-        if (kw != 0 || !col_ok) return;
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            if (m >= a.M) break;
-            store_out<8>(a.out, a.bias, a.residual, a.N, m, 8 * j, acc[m]);
-        }
-        return;
-    }
-
-    const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, part_bytes);
-    if (kw == 0 && col_ok) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            if (m >= a.M) break;
-            const uint32_t off = (uint32_t)((((size_t)split * a.M + m) * a.N + 8 * j) * 4);
-            buf_store_f4_device(floatx4{acc[m][0], acc[m][1], acc[m][2], acc[m][3]}, rp, off);
-            buf_store_f4_device(floatx4{acc[m][4], acc[m][5], acc[m][6], acc[m][7]}, rp, off + 16);
-        }
-    }
-    wait_vm_stores();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        last_flag = __hip_atomic_fetch_add(&counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (uint32_t)(split_k - 1);
-    __syncthreads();
-    if (!last_flag) return;
-    splitk_finish<2>(rp, a.out, a.bias, a.residual, a.M, a.N, 0, a.M, strip * 512, min(512, a.N - strip * 512), split_k, fin);
-    if (threadIdx.x == 0) __hip_atomic_store(&counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // ---------------------------------------------------------------------------
 // Variant 2: K-streaming GEMV.
 //
-// The loads of variant 1 are all issued at once, so the memory system sees
-// requests spread over the whole matrix.  Here a workgroup walks its K range
+// A workgroup walks its K range
 // one 128-row group ("chunk") at a time, top to bottom, with the next chunk's
 // loads in flight while the current one is computed; every workgroup runs
 // the same schedule, so at any moment the machine reads a few bands of
@@ -156,13 +28,12 @@ __global__ __launch_bounds__(512) void awq_gemv_kernel(GemmArgs a, int kw_count,
 // Workgroup = KW = 128 / R waves on one 64-packed-column strip; in chunk c,
 // wave w reads rows 128c + R*w .. +R-1 (all inside the chunk's group), one
 // 256-byte row segment per load instruction.  The zero is handled outside
-// the dot products: the lanes accumulate sum_r x[r] * (1024 + q[r]) (the
-// magic-number code, x16 for columns 2, 3, 6, 7) with v_dot2_f32_f16, and
-// the chunk's result is (that - (1024 + z) * sum_r x[r]) * s, so a weight
-// costs its unpack and one dot2 per row of x.  The products are exact and
-// the fp32 sums carry the 1024 offset (about 10 bits of headroom lost),
-// far inside the tolerance; as in variant 1 the weight is not rounded to
-// fp16 before the product.
+// the dot products: the lanes accumulate sum_r x[r] * (b + q[r]) (the
+// magic-number code) with v_dot2_f32_f16, and the chunk's result is
+// (that - (b + z) * sum_r x[r]) * s, so a weight costs its unpack and one
+// dot2 per row of x.  The products are exact and the fp32 sums carry the
+// offset b (about 10 bits of headroom lost), far inside the tolerance; the
+// weight is not rounded to fp16 before the product.
 template <int MR, int R, int D>
 __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int chunks_per_split, int split_k,
                                                               uint32_t* counters) {
@@ -226,7 +97,7 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 #pragma unroll
         for (int p = 0; p < R / 2; ++p) {
             uint32_t kp[8];
-            kpairs_magic_x16(ck.w[2 * p], ck.w[2 * p + 1], kp);
+            kpairs_magic_inplace(ck.w[2 * p], ck.w[2 * p + 1], kp);
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 sx[m] = __builtin_amdgcn_fdot2(as_h2(ck.xp[m][p]), as_h2(ones), sx[m], false);
@@ -238,8 +109,8 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const uint32_t z = (ck.zw >> col_shift(c)) & 0xFu;
-            const float zz = 1024.f + (float)(x16_column(c) ? 16u * z : z);
-            const float sc = (float)ck.s8[c] * (x16_column(c) ? 0.0625f : 1.0f);
+            const float zz = magic_base(c) + (float)z;
+            const float sc = (float)ck.s8[c];
 #pragma unroll
             for (int m = 0; m < MR; ++m) acc[m][c] += sc * (in[m][c] - zz * sx[m]);
         }
@@ -324,164 +195,6 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 }
 
 // ---------------------------------------------------------------------------
-// Variant 3: one workgroup per narrow column strip over the whole K range.
-//
-// Split-K across workgroups costs a chain of memory round trips at the end of
-// the kernel (partials stored and acknowledged, an arrival atomic, partials
-// reloaded) that is as long as reading a small layer's weights.  Here a
-// workgroup of 16 waves owns P packed columns (8P outputs) for all K, so the
-// whole reduction happens inside it: no workspace, no atomics.
-//
-// Thread t = (p, s) = (t % P, t / P): packed column p, row-octet slot s.  One
-// iteration covers 8 * (1024 / P) rows; the thread reads rows 8s .. 8s+7 of
-// the iteration (always inside one 128-row group, so one zero and one scale
-// per iteration), and a wave's lanes read 64 / P row octets of P adjacent
-// words: 4P bytes per row.  With P < 32 the strips that share a 128-byte
-// line go to one XCD (workgroup b runs on XCD b % 8), so the line is fetched
-// from HBM once and served to the others by that XCD's L2.  D iterations of
-// loads are in flight per thread (ring, unconditional loads).
-//
-// The arithmetic is variant 2's: sum_r x[r] * (1024 + q) by v_dot2_f32_f16,
-// minus (1024 + z) * sum_r x[r], times the scale, once per iteration.  At the
-// end the lanes of a column are added by cross-lane shuffles, the 16 waves
-// through LDS, and 8 consecutive outputs are stored per thread.
-template <int MR, int P, int D>
-__global__ __launch_bounds__(1024) void awq_gemv_col_kernel(GemmArgs a) {
-    constexpr int S = 1024 / P;      // row-octet slots per iteration
-    constexpr int ROWS = 8 * S;      // rows per iteration
-    constexpr int SPL = P >= 32 ? 1 : 32 / P;  // strips per 128-byte line
-    __shared__ float red[16 * MR * P * 8];
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int p = t % P;
-    const int slot = t / P;
-    const int pn = a.N >> 3;
-    const int n_strips = (pn + P - 1) / P;
-    const int xcd = blockIdx.x & 7;
-    const int kx = blockIdx.x >> 3;
-    const int strip = (8 * (kx / SPL) + xcd) * SPL + kx % SPL;
-    if (strip >= n_strips) return;  // whole workgroup
-    const int j = strip * P + p;
-    const bool col_ok = j < pn;
-    const int jc = col_ok ? j : pn - 1;
-    const int n_it = (a.K + ROWS - 1) / ROWS;
-
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
-    const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.qzeros, (uint32_t)((size_t)(a.K / kGroup) * pn * 4));
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, (uint32_t)((size_t)(a.K / kGroup) * a.N * 2));
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
-    const uint32_t row_bytes = (uint32_t)pn * 4u;
-    const uint32_t ones = 0x3C003C00u;
-
-    float acc[MR][8];
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[m][c] = 0.f;
-
-    struct It {
-        uint32_t w[8];
-        u32x4 xq[MR];
-        uint32_t zw;
-        half8_t s8;
-    };
-    // Rows of iteration i for this thread; past K the address is clamped (the
-    // data is then ignored: r0 >= K is uniform over each wave).  The row
-    // differs between the lanes of a wave, so it goes into the VGPR offset
-    // (an SGPR offset would need a waterfall loop per load).
-    auto load = [&](int i, It& it) {
-        const int r0 = min(i * ROWS + 8 * slot, a.K - 8);
-        const uint32_t wo = (uint32_t)r0 * row_bytes + (uint32_t)jc * 4u;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) it.w[q] = buf_load_b32(rw, wo + (uint32_t)q * row_bytes, 0u);
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-            it.xq[m] = __builtin_bit_cast(u32x4, buf_load_h8(rx, (uint32_t)((m * a.K + r0) * 2), 0u));
-        const uint32_t g = (uint32_t)(r0 / kGroup);
-        it.zw = buf_load_b32(rz, g * row_bytes + (uint32_t)jc * 4u, 0u);
-        it.s8 = buf_load_h8(rs, g * (uint32_t)a.N * 2u + (uint32_t)jc * 16u, 0u);
-    };
-    auto compute = [&](int i, const It& it) {
-        if (i * ROWS + 8 * slot >= a.K) return;  // wave-uniform
-        float in[MR][8], sx[MR];
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            sx[m] = 0.f;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) in[m][c] = 0.f;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t kp[8];
-            kpairs_magic_x16(it.w[2 * q], it.w[2 * q + 1], kp);
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const half2_t xv = as_h2(it.xq[m][q]);
-                sx[m] = __builtin_amdgcn_fdot2(xv, as_h2(ones), sx[m], false);
-#pragma unroll
-                for (int c = 0; c < 8; ++c) in[m][c] = __builtin_amdgcn_fdot2(as_h2(kp[c]), xv, in[m][c], false);
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const uint32_t z = (it.zw >> col_shift(c)) & 0xFu;
-            const float zz = 1024.f + (float)(x16_column(c) ? 16u * z : z);
-            const float sc = (float)it.s8[c] * (x16_column(c) ? 0.0625f : 1.0f);
-#pragma unroll
-            for (int m = 0; m < MR; ++m) acc[m][c] += sc * (in[m][c] - zz * sx[m]);
-        }
-    };
-
-    {
-        It ring[D];
-#pragma unroll
-        for (int d = 0; d < D - 1; ++d) load(min(d, n_it - 1), ring[d]);
-        int i = 0;
-        for (; i + D <= n_it; i += D) {
-#pragma unroll
-            for (int d = 0; d < D; ++d) {
-                load(min(i + d + D - 1, n_it - 1), ring[(d + D - 1) % D]);
-                compute(i + d, ring[d]);
-            }
-        }
-        const int rest = n_it - i;
-#pragma unroll
-        for (int d = 0; d < D - 1; ++d)
-            if (d < rest) compute(i + d, ring[d]);
-    }
-
-    // Lanes of the same column inside a wave: lane ^ P, ^ 2P, ...
-#pragma unroll
-    for (int off = P; off < 64; off <<= 1)
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) acc[m][c] += __shfl_xor(acc[m][c], off);
-    if (lane < P) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) red[((wave * MR + m) * P + lane) * 8 + c] = acc[m][c];
-    }
-    __syncthreads();
-    if (t < MR * P) {
-        const int m = t / P;
-        const int pp = t % P;
-        const int jo = strip * P + pp;
-        if (m < a.M && jo < pn) {
-            float o[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) o[c] = 0.f;
-            for (int w = 0; w < 16; ++w)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) o[c] += red[((w * MR + m) * P + pp) * 8 + c];
-            store_out<8>(a.out, a.bias, a.residual, a.N, m, 8 * jo, o);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // Variant 4: quad-column GEMV, interleaved 32-row chunks, fixed-point split-K.
 //
 // Lane l: c4 = l % 16 owns packed columns 4*c4 .. 4*c4+3 of the workgroup's
@@ -498,8 +211,8 @@ __global__ __launch_bounds__(1024) void awq_gemv_col_kernel(GemmArgs a) {
 // A chunk lies inside one 128-row group.
 //
 // Prologue: the workgroup turns the zeros and scales of the groups it
-// touches into fp32 pairs (s', s' * (1024 + z')) per column -- s' and z'
-// carry the x16 of columns 2, 3, 6, 7 -- and stages them and its rows of x
+// touches into fp32 pairs (s, s * (b + z)) per column -- b the offset of the
+// column's magic-number codes -- and stages them and its rows of x
 // in LDS.  The main loop's only vector memory operations are then the weight
 // loads: a ring of D chunk buffers keeps D - 1 chunks' loads in flight while
 // one chunk is computed, every load is issued (chunks past the wave's range get an
@@ -507,9 +220,9 @@ __global__ __launch_bounds__(1024) void awq_gemv_col_kernel(GemmArgs a) {
 // scheduling barriers keep a chunk's arithmetic after the loads issued
 // before it.
 //
-// Arithmetic: sum_r x[r] * (1024 + q) per column by v_dot2_f32_f16 on the
-// magic-number codes (x16 for columns 2, 3, 6, 7) and sum_r x[r]; after each
-// chunk  acc += s' * sum - s'(1024 + z') * sum_x.  At the end the four row
+// Arithmetic: sum_r x[r] * (b + q) per column by v_dot2_f32_f16 on the
+// magic-number codes and sum_r x[r]; after each
+// chunk  acc += s * sum - s(b + z) * sum_x.  At the end the four row
 // slots of a column quad are added with cross-lane shuffles, the waves
 // through LDS, and each output's partial is stored (split_k == 1) or goes
 // through fixed_add_finish.  Needs N % 32 == 0 (whole quads).
@@ -614,8 +327,8 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
                 for (int h = 0; h < 2; ++h) {
                     const int cc = c + h;
                     const uint32_t z = (zv[i] >> col_shift(cc)) & 0xFu;
-                    const float sc = (float)s8[cc] * (x16_column(cc) ? 0.0625f : 1.0f);
-                    const float zz = 1024.f + (float)(x16_column(cc) ? 16u * z : z);
+                    const float sc = (float)s8[cc];
+                    const float zz = magic_base(cc) + (float)z;
                     v[2 * h] = sc;
                     v[2 * h + 1] = sc * zz;
                 }
@@ -653,7 +366,7 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int i = 0; i < 2; ++i) kpairs_magic_x16(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp[2 * h + i]);
+                for (int i = 0; i < 2; ++i) kpairs_magic_inplace(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp[2 * h + i]);
 #pragma unroll
             for (int cc = 0; cc < 8; cc += 2) {
                 const floatx4 v = lc[(gi * 16 + (8 * p + cc) / 2) * 16 + c4];
@@ -696,7 +409,7 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
                     uint32_t kp[8];
-                    kpairs_magic_x16(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp);
+                    kpairs_magic_inplace(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp);
 #pragma unroll
                     for (int cc = 0; cc < 8; ++cc)
 #pragma unroll
@@ -805,26 +518,7 @@ bool gemv_quad_fits(int M, int K, int split_k, int k_waves) {
            mr * per * 4 <= kQuadItemsPerThread * threads;
 }
 
-int64_t gemv_col_blocks(int N, int P) {
-    const int64_t strips = ((N >> 3) + P - 1) / P;
-    const int64_t spl = P >= 32 ? 1 : 32 / P;
-    const int64_t lines = (strips + spl - 1) / spl;
-    return (lines + 7) / 8 * 8 * spl;
-}
-
 int64_t gemv_strips(int N) { return ((N >> 3) + 63) / 64; }
-
-int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count) {
-    const int64_t rows_per_block = (int64_t)rows_per_wave * kw_count;
-    return gemv_strips(N) * ((K + rows_per_block - 1) / rows_per_block);
-}
-
-template <int MR, int R>
-static hipError_t gemv_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream) {
-    const dim3 grid((unsigned)gemv_blocks(a.N, a.K, R, cfg.kw_count)), block(64 * cfg.kw_count);
-    hipLaunchKernelGGL((awq_gemv_kernel<MR, R>), grid, block, 0, stream, a, cfg.kw_count, cfg.split_k, counters);
-    return hipGetLastError();
-}
 
 template <int MR, int R, int D>
 static hipError_t gemv_stream_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
@@ -832,13 +526,6 @@ static hipError_t gemv_stream_launch(const GemmArgs& a, const GemvConfig& cfg, u
     const dim3 grid((unsigned)(gemv_strips(a.N) * cfg.split_k)), block(64 * (kGroup / R));
     hipLaunchKernelGGL((awq_gemv_stream_kernel<MR, R, D>), grid, block, 0, stream, a, cfg.chunks_per_split,
                        cfg.split_k, counters);
-    return hipGetLastError();
-}
-
-template <int MR, int P, int D>
-static hipError_t gemv_col_launch(const GemmArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL((awq_gemv_col_kernel<MR, P, D>), dim3((unsigned)gemv_col_blocks(a.N, P)), dim3(1024), 0,
-                       stream, a);
     return hipGetLastError();
 }
 
@@ -869,28 +556,6 @@ static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, u
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream) {
     if (cfg.variant == 4) return gemv_quad_dispatch<false>(a, cfg, counters, stream);
     if (cfg.variant == 5) return gemv_quad_dispatch<true>(a, cfg, counters, stream);
-    if (cfg.variant == 3) {
-        const int key3 = (a.M <= 1 ? 1 : 2) * 1000 + cfg.rows_per_wave * 10 + cfg.depth;
-        switch (key3) {
-            case 1042: return gemv_col_launch<1, 4, 2>(a, stream);
-            case 1043: return gemv_col_launch<1, 4, 3>(a, stream);
-            case 1082: return gemv_col_launch<1, 8, 2>(a, stream);
-            case 1083: return gemv_col_launch<1, 8, 3>(a, stream);
-            case 1162: return gemv_col_launch<1, 16, 2>(a, stream);
-            case 1163: return gemv_col_launch<1, 16, 3>(a, stream);
-            case 1322: return gemv_col_launch<1, 32, 2>(a, stream);
-            case 1323: return gemv_col_launch<1, 32, 3>(a, stream);
-            case 2042: return gemv_col_launch<2, 4, 2>(a, stream);
-            case 2043: return gemv_col_launch<2, 4, 3>(a, stream);
-            case 2082: return gemv_col_launch<2, 8, 2>(a, stream);
-            case 2083: return gemv_col_launch<2, 8, 3>(a, stream);
-            case 2162: return gemv_col_launch<2, 16, 2>(a, stream);
-            case 2163: return gemv_col_launch<2, 16, 3>(a, stream);
-            case 2322: return gemv_col_launch<2, 32, 2>(a, stream);
-            case 2323: return gemv_col_launch<2, 32, 3>(a, stream);
-            default: return hipErrorInvalidValue;
-        }
-    }
     if (cfg.variant == 2) {
         const int key2 = (a.M <= 1 ? 1 : 2) * 10000 + cfg.rows_per_wave * 10 + cfg.depth;
         switch (key2) {
@@ -907,16 +572,7 @@ hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* count
             default: return hipErrorInvalidValue;
         }
     }
-    const int key = (a.M <= 1 ? 1 : 2) * 1000 + cfg.rows_per_wave;
-    switch (key) {
-        case 1016: return gemv_launch<1, 16>(a, cfg, counters, stream);
-        case 1032: return gemv_launch<1, 32>(a, cfg, counters, stream);
-        case 1064: return gemv_launch<1, 64>(a, cfg, counters, stream);
-        case 2016: return gemv_launch<2, 16>(a, cfg, counters, stream);
-        case 2032: return gemv_launch<2, 32>(a, cfg, counters, stream);
-        case 2064: return gemv_launch<2, 64>(a, cfg, counters, stream);
-        default: return hipErrorInvalidValue;
-    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace awq

@@ -31,37 +31,29 @@ struct SkinnyConfig {
 };
 
 struct GemvConfig {
-    int variant;             // 1: all loads at once; 2: K-streaming, one group per chunk;
-                             // 4: column quads, fixed-point split-K finish
-    int rows_per_wave;       // K rows per wave: 16, 32 or 64 (variant 2: 16 or 32)
-    int kw_count;            // waves per workgroup along K: 1, 2, 4 or 8 (variant 2: 128 / rows_per_wave)
+    int variant;             // 2: K-streaming, one group per chunk; 4, 5: column quads (dot2 /
+                             // MFMA column sums), fixed-point split-K finish
+    int rows_per_wave;       // variant 2: K rows per wave, 16 or 32
+    int kw_count;            // waves per workgroup along K: 1 .. 8 (variant 2: 128 / rows_per_wave)
     int split_k;             // workgroups along K
     int chunks_per_split;    // variant 2: 128-row groups per workgroup
     int depth;               // variant 2: chunk buffers in flight (2, 3 or 4; 4 only for 16 rows per wave)
 };
 
-struct NarrowConfig {
-    int rows_per_wave;       // 16 or 32 (128 / rows_per_wave waves per workgroup)
-    int split_k;             // workgroups along K
-    int chunks_per_split;    // 128-row groups per workgroup
-    int depth;               // chunks in flight: 2 or 3 (3 only for 16 rows per wave)
-    bool factored;           // zero and scale per group sum (M <= 8) or per weight
-};
-
-// Tile variants 5 .. kTileVariants: weights dequantised into MFMA registers,
+// Tile variants 6 .. kTileVariants: weights dequantised into MFMA registers,
 // every load a direct global->LDS load into a ring (x rows per tile, stages).
+// Variant 4: 256 x 128 tiles, weights dequantised once per k-step into LDS.
 constexpr int kTileVariants = 12;
-constexpr int tile5_rows(int variant) {
-    return variant == 5 ? 256 : (variant == 8 || variant == 12) ? 64 : variant == 9 ? 32 : 128;
-}
-constexpr int tile5_threads(int variant) { return (variant == 5 || variant >= 10) ? 512 : 256; }
+constexpr int tile5_rows(int variant) { return (variant == 8 || variant == 12) ? 64 : variant == 9 ? 32 : 128; }
+constexpr int tile5_threads(int variant) { return variant >= 10 ? 512 : 256; }
+// Whether a tile variant number names a kernel.
+constexpr bool tile_variant_served(int variant) { return variant == 4 || (variant >= 6 && variant <= kTileVariants); }
 
 struct TileConfig {
-    int variant;             // 1: 128x128x32; 2: 128x128x64, prefetch, XCD order, split-K; 3: 256x128x64, x ring in LDS;
-                             // 4: 3 with interleaved dequant; 5 .. kTileVariants: register dequant, N tile 256
+    int variant;             // 4: 256x128x64, LDS W^T; 6 .. kTileVariants: register dequant, N tile 256
     int tile_m, tile_n;
-    int split_k;             // variant 2: workgroups along K per tile
-    int k_per_split;         // variant 2: K rows per split (multiple of 64)
+    int split_k;             // workgroups along K per tile
+    int k_per_split;         // K rows per split (multiple of 64; variants 6 and up: of 128)
 };
 
 // out[M, N] = x[M, K] @ w[N, K]^T, fp16 weights (the output projection);
@@ -85,15 +77,13 @@ int64_t skinny_blocks(int N, int K, int rows_per_wave, int kw_count);
 size_t skinny_counter_bytes();
 
 // Same workspace contract as launch_skinny (counters, then partials).
-// Variant 4: the workspace after the counter block holds M * N zeroed 64-bit
-// fixed-point slots (left zero on return) instead of partials.
+// Variants 4 and 5: the workspace after the counter block holds M * N zeroed
+// 64-bit fixed-point slots (left zero on return) instead of partials.
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream);
 int64_t gemv_strips(int N);
 size_t gemv_quad_lds_bytes(int M, int K, int split_k, int k_waves);
 int64_t gemv_quad_max_groups(int K, int split_k);
 bool gemv_quad_fits(int M, int K, int split_k, int k_waves);
-int64_t gemv_col_blocks(int N, int P);
-int64_t gemv_blocks(int N, int K, int rows_per_wave, int kw_count);
 
 // Stream path (M <= 16, N % 32 == 0, split_k <= K / 128).  layout:
 // kStreamRowLayout (M <= 8; 16-row chunks, k_waves waves) or
@@ -115,12 +105,9 @@ size_t stream_lds_bytes(int M, int K, int split_k, int k_waves, int layout);
 bool stream_fits(int M, int K, int split_k, int k_waves, int layout);
 int64_t stream_threads(int layout, int k_waves);
 
-// Same workspace contract as launch_skinny; one arrival counter per 512-column strip.
-hipError_t launch_narrow(const GemmArgs& a, const NarrowConfig& cfg, uint32_t* counters, hipStream_t stream);
-int narrow_blocks_for(int M);
-
-// Variant 2 with split_k > 1 uses the same workspace contract as launch_skinny
-// (counters: one per tile).
+// split_k > 1 uses the same workspace contract as launch_skinny (counters:
+// one per tile; variants 7, 8, 9, 11, 12 add the partials in a second
+// launch of awq_splitk_reduce_kernel on the same stream).
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream);
 int64_t tile_tiles(int M, int N, int variant);
 

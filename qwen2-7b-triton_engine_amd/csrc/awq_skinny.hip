@@ -20,8 +20,9 @@
 //  * per weight: w = (q - z)*s is formed in fp16 as in the reference and the
 //    MFMAs accumulate straight into the totals (28 VALU ops per 16 weights,
 //    fewer registers).
-// Both fold the 16x of kpairs_magic_x16's columns 2, 3, 6, 7 back into the
-// fp32 result (an exact power-of-two scaling).
+// Both read the codes with kpairs_magic_inplace, whose columns 2, 3, 6, 7
+// carry the offset 64 instead of 1024; the matching zero splat makes q - z
+// exact either way.
 //
 // Main loop variants:
 //  1  chunked software pipeline: the loads of the next group (4 k-steps) are
@@ -90,8 +91,8 @@ __global__ __launch_bounds__(512) void awq_skinny_kernel(GemmArgs a, int rows_pe
         auto group_consts = [&](uint32_t zw, half8_t s8, uint32_t (&zs)[8], uint32_t (&ss)[8], float (&sf)[8]) {
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                zs[c] = zero_splat_x16(zw, c);
-                if (FACTORED) sf[c] = (float)s8[c] * (x16_column(c) ? 0.0625f : 1.0f);
+                zs[c] = zero_splat_inplace(zw, c);
+                if (FACTORED) sf[c] = (float)s8[c];
                 else ss[c] = as_u32(half2_t{s8[c], s8[c]});
             }
         };
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(512) void awq_skinny_kernel(GemmArgs a, int rows_pe
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 uint32_t kp[8];
-                kpairs_magic_x16(w[2 * p], w[2 * p + 1], kp);
+                kpairs_magic_inplace(w[2 * p], w[2 * p + 1], kp);
 #pragma unroll
                 for (int c = 0; c < 8; ++c) {
                     const half2_t d = as_h2(kp[c]) - as_h2(zs[c]);
@@ -205,14 +206,6 @@ __global__ __launch_bounds__(512) void awq_skinny_kernel(GemmArgs a, int rows_pe
                 if (chunk + 1 < nchunks) compute_chunk(chunk + 1, wB, xB, zB, sB);
             }
         }
-    }
-
-    if (!FACTORED) {
-#pragma unroll
-        for (int b = 0; b < MB; ++b)
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                if (x16_column(c)) tot[b][c] *= 0.0625f;
     }
 
     // Lane holds rows m = 16b + 4kq + ii of columns 8j .. 8j+7 (contiguous).

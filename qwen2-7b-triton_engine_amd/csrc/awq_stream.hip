@@ -7,15 +7,16 @@
 // loads in flight while one is computed; loads past the end use an
 // out-of-range offset and read zeros, so the compiler's wait counts stay
 // static).  Zeros and scales of the workgroup's groups are staged in LDS once
-// as fp32 pairs (s', s'(1024 + z')) per column (s' = s, or s/16 for the
-// columns the magic-number unpack returns scaled by 16).
+// as fp32 pairs (s, s(b + z)) per column, where b is the offset the
+// magic-number unpack gives that column's codes (1024, or 64 for the columns
+// kpairs_magic_inplace cuts in place).
 //
 // Arithmetic (both layouts): v_mfma_f32_16x16x32_f16 with the magic-number
-// k-pairs (1024 + q') of a lane's 8 rows of one column as its B fragment and
+// k-pairs (b + q) of a lane's 8 rows of one column as its B fragment and
 // rows of x as A.  Over a group one MFMA per column accumulates
-//     C[m][n] = sum_k x[m][k] * (1024 + q'[k][n])
+//     C[m][n] = sum_k x[m][k] * (b + q[k][n])
 // and one MFMA against ones S[m] = sum_k x[m][k]; at the end of the group
-//     acc[m][n] += s'[n] * C[m][n] - s'(1024 + z')[n] * S[m]
+//     acc[m][n] += s[n] * C[m][n] - s(b + z)[n] * S[m]
 // in fp32 (one fold per column and row per group).
 //
 // Row layout (awq_stream_row_kernel, M <= 8): every load instruction covers
@@ -56,7 +57,7 @@ constexpr int kStreamItemsPerThread = 4;  // prologue constant loads per thread
 // Zeros and scales of groups g0 .. g0 + n_g - 1 of a strip: issued first (so
 // that they are in flight with the first chunk loads), stored to LDS after.
 // LDS layout float4 [n_g][2 halves][8][16]: piece i of lane n of a half holds
-// (s', s'(1024 + z')) of the half's columns 16 n + 2 i and + 1 (one
+// (s, s(b + z)) of the half's columns 16 n + 2 i and + 1 (one
 // wave-wide read of a half is 256 consecutive bytes).
 struct StagedConsts {
     u32x4 sv[kStreamItemsPerThread];
@@ -91,8 +92,8 @@ struct StagedConsts {
                     for (int e = 0; e < 2; ++e) {
                         const int cc = c + e;
                         const uint32_t z = (zv[i] >> col_shift(cc)) & 0xFu;
-                        const float sc = (float)s8[cc] * (x16_column(cc) ? 0.0625f : 1.0f);
-                        const float zz = 1024.f + (float)(x16_column(cc) ? 16u * z : z);
+                        const float sc = (float)s8[cc];
+                        const float zz = magic_base(cc) + (float)z;
                         v[2 * e] = sc;
                         v[2 * e + 1] = sc * zz;
                     }
@@ -119,7 +120,7 @@ __device__ __forceinline__ void chunk_mfma(const u32x2 (&w)[8], const half8_t (&
     for (int p = 0; p < 2; ++p) {
         uint32_t kp[4][8];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) kpairs_magic_x16(w[2 * t][p], w[2 * t + 1][p], kp[t]);
+        for (int t = 0; t < 4; ++t) kpairs_magic_inplace(w[2 * t][p], w[2 * t + 1][p], kp[t]);
 #pragma unroll
         for (int cc = 0; cc < 8; ++cc) {
             const half8_t b = __builtin_bit_cast(half8_t, u32x4{kp[0][cc], kp[1][cc], kp[2][cc], kp[3][cc]});
@@ -129,7 +130,7 @@ __device__ __forceinline__ void chunk_mfma(const u32x2 (&w)[8], const half8_t (&
     }
 }
 
-// acc[r][j] += s'[j] * C[j][r] - s'(1024 + z')[j] * S[r] with the constants
+// acc[r][j] += s[j] * C[j][r] - s(b + z)[j] * S[r] with the constants
 // of lane n of half `half` of group gi (relative to the workgroup's first).
 __device__ __forceinline__ void fold_group(const floatx4* lc, int gi, int half, int n, const floatx4& S,
                                            const floatx4 (&Cc)[16], float (&acc)[4][16]) {

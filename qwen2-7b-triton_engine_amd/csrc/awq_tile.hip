@@ -1,367 +1,21 @@
-// Prefill W4A16 AWQ GEMM (large M) for gfx950: LDS-tiled MFMA kernel.
+// Prefill W4A16 AWQ GEMM (large M) for gfx950: LDS-tiled MFMA kernels.
 //
-// Block tile 128 (M) x 128 (N), k-step 32, 256 threads = 4 wavefronts in a
-// 2 x 2 grid, each computing 64 x 64 with v_mfma_f32_16x16x32_f16.
-//
-// The dequantised weight is produced once per block and k-step, next to the
-// load: each thread reads two qweight words (rows r, r+1 of one packed
-// column), forms per-column k-pairs in registers (v_perm_b32 + magic-number
-// decode), subtracts the zero and multiplies by the scale in fp16 -- the
-// reference's exact fp16 weight -- and writes the pairs to LDS in a
-// [n][k] layout, so that every MFMA operand fragment (8 consecutive k of one
-// row) is a single 16-byte LDS read.  x is staged to LDS as [m][k] the same
-// way.  The product is computed transposed, out^T = W^T x^T: the W^T fragment
-// is the MFMA A operand and the x^T fragment the B operand, so each lane ends
-// with 4 consecutive output columns of one row (8-byte stores).
-//
-// Two LDS buffers: the global loads for k-step t+1 are issued before the
-// MFMAs of step t and written to the other buffer after them; one barrier per
-// k-step.
+// Two kernel families:
+//  * awq_tile_kernel_v3 (tile variant 4): 256 x 128 x 64 tiles, weights
+//    dequantised once per k-step into an LDS W^T buffer shared by all 256
+//    rows;
+//  * awq_tile_kernel_v5 (tile variants 6 .. 12): 256 output columns per
+//    tile, weights dequantised straight into MFMA operand registers.
+// Both stream every operand into LDS rings with direct global->LDS loads and
+// form the reference's exact fp16 weight fp16((q - z) * s) next to the load.
 #include <type_traits>
 
 #include "awq_kernels.h"
 
 namespace awq {
-namespace {
-constexpr int BM = 128;
-constexpr int BN = 128;
-constexpr int BK = 32;
-constexpr int PITCH = BK + 8;  // halves per LDS row; 80 B keeps 16-B fragment reads conflict-free
-}  // namespace
-
-__global__ __launch_bounds__(256) void awq_tile_kernel_v1(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) half_t As[2][BM * PITCH];
-    __shared__ __attribute__((aligned(16))) half_t Bs[2][BN * PITCH];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave & 1;
-    const int wn = wave >> 1;
-    const int c16 = lane & 15;
-    const int kq = lane >> 4;
-
-    const int m_tiles = (a.M + BM - 1) / BM;
-    const int tm = blockIdx.x % m_tiles;
-    const int tn = blockIdx.x / m_tiles;
-    const int m0 = tm * BM;
-    const int n0 = tn * BN;
-    const int pn = a.N >> 3;
-
-    // x tile loader: 2 chunks of 8 halves per thread.
-    int a_row[2], a_kc[2];
-    bool a_ok[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int q = tid + 256 * r;
-        a_row[r] = q >> 2;
-        a_kc[r] = q & 3;
-        a_ok[r] = (m0 + a_row[r]) < a.M;
-    }
-    // weight loader: packed column jj (0..15) of the tile, rows 2*rp, 2*rp+1 of the k-step.
-    const int rp = tid & 15;
-    const int jj = tid >> 4;
-    const int jg = (n0 >> 3) + jj;
-    const bool b_ok = jg < pn;
-    const int jgc = b_ok ? jg : pn - 1;
-
-    const int KT = a.K / BK;
-    half8_t xr[2];
-    uint32_t w0, w1;
-    uint32_t zs[8];
-    uint32_t ss[8];  // fp16 scale pairs (s, s)
-
-    auto load_global = [&](int kt) {
-        const int kb = kt * BK;
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            if (a_ok[r])
-                xr[r] = *reinterpret_cast<const half8_t*>(a.x + (size_t)(m0 + a_row[r]) * a.K + kb + 8 * a_kc[r]);
-            else
-                xr[r] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-        const uint32_t* wp = a.qweight + (size_t)(kb + 2 * rp) * pn + jgc;
-        w0 = wp[0];
-        w1 = wp[pn];
-    };
-    auto load_group = [&](int kt) {
-        const int g = (kt * BK) / kGroup;
-        const uint32_t zw = a.qzeros[(size_t)g * pn + jgc];
-        const half8_t s8 = *reinterpret_cast<const half8_t*>(a.scales + (size_t)g * a.N + 8 * jgc);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            zs[c] = zero_splat(zw, c);
-            ss[c] = as_u32(half2_t{s8[c], s8[c]});
-        }
-    };
-    auto store_lds = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-            *reinterpret_cast<half8_t*>(&As[buf][a_row[r] * PITCH + 8 * a_kc[r]]) = xr[r];
-        uint32_t kp[8];
-        kpairs_magic(w0, w1, kp);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const half2_t v = (as_h2(kp[c]) - as_h2(zs[c])) * as_h2(ss[c]);
-            const uint32_t bits = b_ok ? as_u32(v) : 0u;
-            *reinterpret_cast<uint32_t*>(&Bs[buf][(8 * jj + c) * PITCH + 2 * rp]) = bits;
-        }
-    };
-
-    floatx4 acc[4][4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    load_group(0);
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        const bool has_next = kt + 1 < KT;
-        if (has_next) load_global(kt + 1);
-
-        half8_t af[4], bfr[4];
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-            af[x] = *reinterpret_cast<const half8_t*>(&Bs[buf][(64 * wn + 16 * x + c16) * PITCH + 8 * kq]);
-#pragma unroll
-        for (int y = 0; y < 4; ++y)
-            bfr[y] = *reinterpret_cast<const half8_t*>(&As[buf][(64 * wm + 16 * y + c16) * PITCH + 8 * kq]);
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-#pragma unroll
-            for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
-
-        if (has_next) {
-            if (((kt + 1) * BK) % kGroup == 0) load_group(kt + 1);
-            store_lds(buf ^ 1);
-        }
-        __syncthreads();
-    }
-
-    // acc[x][y] lane value v: out^T[n = 16x + 4kq + v][m = 16y + c16] of this wave's 64 x 64.
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-        const int gm = m0 + 64 * wm + 16 * y + c16;
-        if (gm >= a.M) continue;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-            const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
-            if (gn >= a.N) continue;
-            const float v[4] = {acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]};
-            store_out<4>(a.out, a.bias, a.residual, a.N, gm, gn, v);
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
-// Variant 2: 128 x 128 x 64 tiles, register prefetch one k-step ahead,
-// XCD-aware tile order, optional split-K.
-//
-// * LDS rows are k-contiguous with a 144-byte pitch, which keeps the 16-byte
-//   fragment reads of 8 consecutive rows on distinct banks.
-// * Each thread dequantises 4 rows x 1 packed column per k-step (two k-pairs
-//   per logical column) and writes each column's 4 fp16 values as one 8-byte
-//   LDS store; 16 consecutive lanes cover 16 row quads, 128 contiguous bytes.
-// * Work order: workgroup b runs on XCD b % 8 (round-robin dispatch); the
-//   workgroups of one XCD take a contiguous range of the grouped-M tile order
-//   (8 M tiles per group), so concurrent workgroups of an XCD share x rows and
-//   weight columns in that XCD's L2.  Any other dispatch order only costs
-//   locality: the mapping is a bijection either way.
-// * split_k > 1 (small tile grids): each workgroup covers a K range and
-//   finishes like the decode kernels (device-scope partials, arrival counter,
-//   deterministic finish by the last workgroup of the tile).
-namespace {
-constexpr int T2_BM = 128;
-constexpr int T2_BN = 128;
-constexpr int T2_BK = 64;
-constexpr int T2_PITCH = T2_BK + 8;  // halves
-constexpr int T2_GM = 8;             // M tiles per group of the tile order
-}  // namespace
-
-__global__ __launch_bounds__(256, 2) void awq_tile_kernel_v2(GemmArgs a, int split_k, int k_per_split,
-                                                             uint32_t* counters) {
-    __shared__ __attribute__((aligned(16))) half_t As[2][T2_BM * T2_PITCH];
-    __shared__ __attribute__((aligned(16))) half_t Bs[2][T2_BN * T2_PITCH];
-    __shared__ floatx4 fin[256];
-    __shared__ int last_flag;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave & 1;
-    const int wn = wave >> 1;
-    const int c16 = lane & 15;
-    const int kq = lane >> 4;
-
-    // ---- work item of this workgroup ----
-    const int m_tiles = (a.M + T2_BM - 1) / T2_BM;
-    const int n_tiles = (a.N + T2_BN - 1) / T2_BN;
-    const int total = (int)gridDim.x;  // m_tiles * n_tiles * split_k
-    const int xcd = blockIdx.x & 7;
-    const int xi = blockIdx.x >> 3;
-    const int per = (total + 7) >> 3;
-    const int rem = total & 7;
-    const int w = (rem == 0 || xcd < rem) ? xcd * per + xi : rem * per + (xcd - rem) * (per - 1) + xi;
-    const int tile = w / split_k;
-    const int split = w - tile * split_k;
-    const int in_group = T2_GM * n_tiles;
-    const int first_m = (tile / in_group) * T2_GM;
-    const int gm = min(m_tiles - first_m, T2_GM);
-    const int tm = first_m + (tile % in_group) % gm;
-    const int tn = (tile % in_group) / gm;
-    const int m0 = tm * T2_BM;
-    const int n0 = tn * T2_BN;
-    const int pn = a.N >> 3;
-    const int k_begin = split * k_per_split;
-    const int k_end = min(a.K, k_begin + k_per_split);
-    const int KT = (k_end - k_begin) / T2_BK;
-
-    // ---- loaders ----
-    int xrow[4], xkc[4];
-    bool xok[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int q = tid + 256 * r;
-        xrow[r] = q >> 3;
-        xkc[r] = q & 7;
-        xok[r] = m0 + xrow[r] < a.M;
-    }
-    const int rq = tid & 15;       // row quad: rows 4*rq .. 4*rq+3 of the k-step
-    const int jj = tid >> 4;       // packed column of the tile
-    const int jg = (n0 >> 3) + jj;
-    const bool wok = jg < pn;
-    const int jgc = wok ? jg : pn - 1;
-
-    half8_t xr[4];
-    uint32_t wr[4];
-    uint32_t zs[8], ss[8];
-
-    auto load_global = [&](int kt) {
-        const int kb = k_begin + kt * T2_BK;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (xok[r])
-                xr[r] = *reinterpret_cast<const half8_t*>(a.x + (size_t)(m0 + xrow[r]) * a.K + kb + 8 * xkc[r]);
-            else
-                xr[r] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-        const uint32_t* wp = a.qweight + (size_t)(kb + 4 * rq) * pn + jgc;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wr[i] = wp[(size_t)i * pn];
-    };
-    auto load_group = [&](int kt) {
-        const int g = (k_begin + kt * T2_BK) / kGroup;
-        const uint32_t zw = a.qzeros[(size_t)g * pn + jgc];
-        const half8_t s8 = *reinterpret_cast<const half8_t*>(a.scales + (size_t)g * a.N + 8 * jgc);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            zs[c] = zero_splat(zw, c);
-            ss[c] = as_u32(half2_t{s8[c], s8[c]});
-        }
-    };
-    auto store_lds = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<half8_t*>(&As[buf][xrow[r] * T2_PITCH + 8 * xkc[r]]) = xr[r];
-        uint32_t k01[8], k23[8];
-        kpairs_magic(wr[0], wr[1], k01);
-        kpairs_magic(wr[2], wr[3], k23);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const half2_t lo = (as_h2(k01[c]) - as_h2(zs[c])) * as_h2(ss[c]);
-            const half2_t hi = (as_h2(k23[c]) - as_h2(zs[c])) * as_h2(ss[c]);
-            const u32x2 v = wok ? u32x2{as_u32(lo), as_u32(hi)} : u32x2{0u, 0u};
-            *reinterpret_cast<u32x2*>(&Bs[buf][(8 * jj + c) * T2_PITCH + 4 * rq]) = v;
-        }
-    };
-
-    floatx4 acc[4][4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    if (KT > 0) {
-        load_group(0);
-        load_global(0);
-        store_lds(0);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        const bool has_next = kt + 1 < KT;
-        if (has_next) load_global(kt + 1);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            half8_t af[4], bfr[4];
-#pragma unroll
-            for (int x = 0; x < 4; ++x)
-                af[x] = *reinterpret_cast<const half8_t*>(
-                    &Bs[buf][(64 * wn + 16 * x + c16) * T2_PITCH + 32 * s2 + 8 * kq]);
-#pragma unroll
-            for (int y = 0; y < 4; ++y)
-                bfr[y] = *reinterpret_cast<const half8_t*>(
-                    &As[buf][(64 * wm + 16 * y + c16) * T2_PITCH + 32 * s2 + 8 * kq]);
-#pragma unroll
-            for (int x = 0; x < 4; ++x)
-#pragma unroll
-                for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
-        }
-        if (has_next) {
-            if ((k_begin + (kt + 1) * T2_BK) % kGroup == 0) load_group(kt + 1);
-            store_lds(buf ^ 1);
-        }
-        __syncthreads();
-    }
-
-    // acc[x][y] lane value v: out^T[n = 16x + 4kq + v][m = 16y + c16] of this wave's 64 x 64.
-    if (split_k == 1) {
-#pragma unroll
-        for (int y = 0; y < 4; ++y) {
-            const int gm_ = m0 + 64 * wm + 16 * y + c16;
-            if (gm_ >= a.M) continue;
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
-                if (gn >= a.N) continue;
-                const float v[4] = {acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]};
-                store_out<4>(a.out, a.bias, a.residual, a.N, gm_, gn, v);
-            }
-        }
-        return;
-    }
-
-    const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, part_bytes);
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-        const int gm_ = m0 + 64 * wm + 16 * y + c16;
-        if (gm_ >= a.M) continue;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-            const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
-            if (gn >= a.N) continue;
-            buf_store_f4_device(acc[x][y], rp, (uint32_t)((((size_t)split * a.M + gm_) * a.N + gn) * 4));
-        }
-    }
-    wait_vm_stores();
-    __syncthreads();
-    if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (uint32_t)(split_k - 1);
-    __syncthreads();
-    if (!last_flag) return;
-    splitk_finish<16>(rp, a.out, a.bias, a.residual, a.M, a.N, m0, min(T2_BM, a.M - m0), n0, min(T2_BN, a.N - n0), split_k, fin);
-    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---------------------------------------------------------------------------
-// Variant 3: 256 x 128 x 64 tiles, 512 threads (8 waves of 64 x 64), every
+// Variant 4: 256 x 128 x 64 tiles, 512 threads (8 waves of 64 x 64), every
 // operand streamed into LDS rings by direct global->LDS loads.
 //
 // buffer_load_dword[x4] ... lds writes each lane's 4 (16) bytes to
@@ -433,11 +87,10 @@ __device__ __forceinline__ u32x4 raw_rsrc(const void* base, uint32_t num_bytes) 
 }
 }  // namespace
 
-// IL: variant 4 -- the next k-step's dequant (LDS reads issued first, VALU
-// and W^T stores) is interleaved with this k-step's MFMAs by scheduling
-// groups instead of following them, so the 8 waves, which meet at one
-// barrier per k-step, overlap dequant arithmetic with matrix work.
-template <bool IL>
+// The next k-step's dequant (LDS reads issued first, VALU and W^T stores) is
+// interleaved with this k-step's MFMAs by scheduling groups instead of
+// following them, so the 8 waves, which meet at one barrier per k-step,
+// overlap dequant arithmetic with matrix work.
 __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int split_k, int k_per_split,
                                                              uint32_t* counters) {
     __shared__ __attribute__((aligned(16))) half_t Xs[T3_XS][T3_BM * T3_BK];
@@ -455,7 +108,11 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
     const int c16 = lane & 15;
     const int kq = lane >> 4;
 
-    // ---- work item (same XCD-aware grouped order as variant 2) ----
+    // ---- work item: XCD-aware grouped tile order.  Workgroup b runs on XCD
+    // b % 8 (round-robin dispatch); the workgroups of one XCD take a
+    // contiguous range of the grouped-M tile order, so the concurrent
+    // workgroups of an XCD share x rows and weight columns in its L2.  Any
+    // other dispatch order only costs locality: the mapping is a bijection.
     const int m_tiles = (a.M + T3_BM - 1) / T3_BM;
     const int n_tiles = (a.N + T3_BN - 1) / T3_BN;
     const int total = (int)gridDim.x;
@@ -569,75 +226,53 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
             issue_raw(min(kt + 3, last), (kt + 3) % T3_RS);
             const half_t* xs = Xs[kt % T3_XS];
             const half_t* wsb = Ws[kt & 1];
-            if constexpr (!IL) {
+            // Operands of the next k-step's dequant (its stage holds clamped
+            // data on the last step; the W^T buffer it writes is not read
+            // again).
+            const int rs1 = (kt + 1) % T3_RS;
+            const u32x2 wpair =
+                *reinterpret_cast<const u32x2*>(&Wr[rs1][(rp >> 1) * T3_RAW_BLOCK + 4 * jj + 2 * (rp & 1)]);
+            const uint32_t zw = Zs[rs1][jj];
+            const half8_t s8 = *reinterpret_cast<const half8_t*>(&Zs[rs1][64 + 4 * jj]);
+            half8_t af[2][4], bfr[2][4];
 #pragma unroll
-                for (int s2 = 0; s2 < 2; ++s2) {
-                    half8_t af[4], bfr[4];
+            for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
-                    for (int x = 0; x < 4; ++x)
-                        af[x] = *reinterpret_cast<const half8_t*>(
-                            &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
+                for (int x = 0; x < 4; ++x)
+                    af[s2][x] = *reinterpret_cast<const half8_t*>(
+                        &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
 #pragma unroll
-                    for (int y = 0; y < 4; ++y) {
-                        const int r = 64 * wm + 16 * y + c16;
-                        const int phys = (4 * s2 + kq) ^ (r & 7);
-                        bfr[y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
-                    }
-#pragma unroll
-                    for (int x = 0; x < 4; ++x)
-#pragma unroll
-                        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[x], bfr[y], acc[x][y]);
+                for (int y = 0; y < 4; ++y) {
+                    const int r = 64 * wm + 16 * y + c16;
+                    const int phys = (4 * s2 + kq) ^ (r & 7);
+                    bfr[s2][y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
                 }
-                if (kt + 1 < KT) dequant((kt + 1) % T3_RS, (kt + 1) & 1);
-            } else {
-                // Operands of the next k-step's dequant (its stage holds clamped
-                // data on the last step; the W^T buffer it writes is not read
-                // again).
-                const int rs1 = (kt + 1) % T3_RS;
-                const u32x2 wpair =
-                    *reinterpret_cast<const u32x2*>(&Wr[rs1][(rp >> 1) * T3_RAW_BLOCK + 4 * jj + 2 * (rp & 1)]);
-                const uint32_t zw = Zs[rs1][jj];
-                const half8_t s8 = *reinterpret_cast<const half8_t*>(&Zs[rs1][64 + 4 * jj]);
-                half8_t af[2][4], bfr[2][4];
-#pragma unroll
-                for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-                    for (int x = 0; x < 4; ++x)
-                        af[s2][x] = *reinterpret_cast<const half8_t*>(
-                            &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
-#pragma unroll
-                    for (int y = 0; y < 4; ++y) {
-                        const int r = 64 * wm + 16 * y + c16;
-                        const int phys = (4 * s2 + kq) ^ (r & 7);
-                        bfr[s2][y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
-                    }
-                }
-                uint32_t kp[8];
-                kpairs_magic(wpair[0], wpair[1], kp);
-                uint32_t wv[8];
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    wv[c] = as_u32((as_h2(kp[c]) - as_h2(zero_splat(zw, c))) * half2_t{s8[c], s8[c]});
-#pragma unroll
-                for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-                    for (int x = 0; x < 4; ++x)
-#pragma unroll
-                        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[s2][x], bfr[s2][y], acc[x][y]);
-                half_t* wnext = Ws[(kt + 1) & 1];
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    *reinterpret_cast<uint32_t*>(&wnext[(8 * jj + c) * T3_WPITCH + 2 * rp]) = wok ? wv[c] : 0u;
-                // Order: all LDS reads, then MFMAs each followed by two VALU
-                // instructions of the dequant, the W^T stores last.
-                __builtin_amdgcn_sched_group_barrier(0x100, 19, 0);
-#pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-                }
-                __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);
             }
+            uint32_t kp[8];
+            kpairs_magic(wpair[0], wpair[1], kp);
+            uint32_t wv[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                wv[c] = as_u32((as_h2(kp[c]) - as_h2(zero_splat(zw, c))) * half2_t{s8[c], s8[c]});
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+#pragma unroll
+                    for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[s2][x], bfr[s2][y], acc[x][y]);
+            half_t* wnext = Ws[(kt + 1) & 1];
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                *reinterpret_cast<uint32_t*>(&wnext[(8 * jj + c) * T3_WPITCH + 2 * rp]) = wok ? wv[c] : 0u;
+            // Order: all LDS reads, then MFMAs each followed by two VALU
+            // instructions of the dequant, the W^T stores last.
+            __builtin_amdgcn_sched_group_barrier(0x100, 19, 0);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);
             __builtin_amdgcn_s_waitcnt(kWaitVm7);
             __syncthreads();
         }
@@ -687,8 +322,8 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
 }
 
 // ---------------------------------------------------------------------------
-// Variants 5 and 6: 256 output columns per tile, each wave 64 columns x 128
-// x rows, weights dequantised straight into MFMA A registers (never written
+// Variants 6 .. 12: 256 output columns per tile, each wave 64 columns x 32,
+// 64 or 128 x rows, weights dequantised straight into MFMA A registers (never written
 // back to LDS), every global load a direct global->LDS load issued two
 // k-steps ahead into a 3-stage ring.  No VGPR holds data in flight and the
 // compiler sees no global load inside the main loop, so nothing waits on a
@@ -697,23 +332,22 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
 //
 // A stage holds one k-step (64 rows):
 //   * x: BM rows of 128 B, 16-byte chunk p of row r holding k-chunk
-//     p ^ (r & 7) (as variant 5); a wave's dwordx4 load writes 8 rows.
+//     p ^ (r & 7) (as variant 4); a wave's dwordx4 load writes 8 rows.
 //   * packed weights: 64 rows x 32 packed columns, dword
 //     ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h + 8 kb + 4 ub + u
 //     of column j, so the lane that owns column j and rows 8 kb .. + 7 of
 //     half h reads them as two 16-byte words; one dword load covers 4 rows x
 //     16 columns (64-byte row segments).
 //   * the group's zero words (32 dwords) and scales (256 halves).
-// WM: waves along M -- 2: 8 waves, one workgroup per CU; 1: 4 waves.
 // FM: 16-row blocks per wave (8: 128 x rows per wave; 4: 64; 2: 32).
 // KW: 2 -- a second wave per SIMD from the same workgroup: waves w and w + 4
 // take k-half 0 and 1 of every k-step for the same columns and rows (each
 // dequantises only its half) and add their accumulators through LDS at the
 // end; for grids too small to give each CU two workgroups, where a lone
 // wave per SIMD would expose its own latency.
-// Variant 5 = (2, 8): 256 x 256 tiles; 6 = (1, 8): 128 x 256 tiles, two
-// workgroups per CU, last-arriver split-K finish; 7, 8, 9 = (1, 8), (1, 4),
-// (1, 2): 128, 64 and 32 x 256 tiles (two, three, four workgroups per CU)
+// Variant 6 = (8, 1): 128 x 256 tiles, four waves, two workgroups per CU,
+// last-arriver split-K finish; 7, 8, 9 = (8, 1), (4, 1), (2, 1): 128, 64
+// and 32 x 256 tiles (two, three, four workgroups per CU)
 // with the reduce-launch finish -- the smaller tiles for M up to about a
 // thousand, where the larger ones would leave MFMA rows idle or the CUs
 // short of work.
@@ -725,19 +359,19 @@ constexpr int T5_ZS_BYTES = 768;              // 256 B zero words (128 used) + 5
 constexpr int T5_GM = 4;
 constexpr int T5_STAGES = 3;
 
-template <int WM, int FM, int KW>
+template <int FM, int KW>
 struct T5Layout {
     static constexpr int S = T5_STAGES;
     static constexpr int RW = 16 * FM;  // x rows per wave
-    static constexpr int BM = RW * WM;
+    static constexpr int BM = RW;
     static constexpr int X_BYTES = BM * T5_BK * 2;
     static constexpr int STAGE = X_BYTES + T5_W_BYTES + T5_ZS_BYTES;
-    static constexpr int THREADS = 256 * WM * KW;
-    static constexpr int WAVES = 4 * WM * KW;
+    static constexpr int THREADS = 256 * KW;
+    static constexpr int WAVES = 4 * KW;
     static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;   // dwordx4 loads per wave per stage (FM / 2)
     // Workgroups per CU: by registers (accumulators 4 * FM float4 per lane)
     // and by LDS (S stages).
-    static constexpr int PER_CU_REG = (WM == 2 || KW == 2) ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
+    static constexpr int PER_CU_REG = KW == 2 ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
     static constexpr int PER_CU_LDS = (160 * 1024) / (S * (X_BYTES + T5_W_BYTES + T5_ZS_BYTES) + 64);
     static constexpr int PER_CU = PER_CU_REG < PER_CU_LDS ? PER_CU_REG : PER_CU_LDS;
     static constexpr int W_LOADS = T5_W_BYTES / 256 / WAVES;  // dword loads per wave per stage
@@ -767,14 +401,12 @@ __device__ __forceinline__ void wait_batches(int n) {
 // partials; 1 -- partials with plain stores, summed by a second launch of
 // awq_splitk_reduce_kernel over the whole device (for small tiles, whose
 // last arrivers would each read split x tile bytes alone).
-template <int WM, int FM, int KW, int FIN>
-__global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void awq_tile_kernel_v5(
+template <int FM, int KW, int FIN>
+__global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile_kernel_v5(
     GemmArgs a, int split_k, int k_per_split, uint32_t* counters) {
-    using L = T5Layout<WM, FM, KW>;
+    using L = T5Layout<FM, KW>;
     constexpr int BM = L::BM;
-    constexpr int RW = L::RW;
     constexpr int S = L::S;
-    static_assert(KW == 1 || (KW == 2 && WM == 1), "k-half wave pairs only with one wave row");
     static_assert((S - 2) * L::LOADS <= 63, "vmcnt holds 6 bits");
     static_assert(FM % 2 == 0 && L::X_LOADS >= 1, "a wave loads whole 8-row blocks of x");
     static_assert(L::PER_CU >= 1 && L::PER_CU * S * L::STAGE <= 160 * 1024, "LDS per CU");
@@ -785,14 +417,13 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = WM == 2 ? wave >> 2 : 0;
     const int kh = KW == 2 ? wave >> 2 : 0;  // k-half of each step this wave computes (KW = 2)
     const int wn = wave & 3;
     const int n16 = lane & 15;
     const int kb = lane >> 4;
     const int hh = n16 >> 3;
 
-    // ---- work item: XCD-aware grouped tile order (as variants 2 .. 6) ----
+    // ---- work item: XCD-aware grouped tile order (as variant 4) ----
     const int m_tiles = (a.M + BM - 1) / BM;
     const int n_tiles = (a.N + T5_BN - 1) / T5_BN;
     const int total = (int)gridDim.x;
@@ -873,8 +504,9 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
                                base + L::X_BYTES + 256u * (uint32_t)(L::W_LOADS * wave + i));
     };
 
-    // v_perm selectors (byte 0x0C reads as zero), as variant 5.
-    const uint32_t magic = magic_vgpr();  // for one v_and_or_b32 per k-pair
+    // v_perm selectors (byte 0x0C reads as zero).
+    const uint32_t magic = magic_vgpr();        // for one v_and_or_b32 per k-pair
+    const uint32_t magic_hi = magic_hi_vgpr();  // (nibbles cut in place)
     const uint32_t sel_even = hh ? 0x0C050C01u : 0x0C040C00u;
     const uint32_t sel_odd = hh ? 0x0C070C03u : 0x0C060C02u;
     const int jl = 8 * wn + (n16 & 7);  // lane's packed column within the tile
@@ -886,9 +518,10 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
         for (int f = 0; f < FM; ++f) acc[c][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // One k-step from stage memory `st`: per k-half, two 16-byte reads give
-    // the lane's 8 weight words, 4 A fragments are formed (second nibble
-    // masked in place: columns 2, 3 carry 16 (q - z) s, scaled back at the
-    // end), then the 8 B fragments of the wave's x rows, 4 MFMAs each.
+    // the lane's 8 weight words, 4 A fragments are formed (the second nibble
+    // of a byte is masked in place and read with the 64.0 magic, so every
+    // column gives the exact q - z and one fp16 rounding of (q - z) * s), then
+    // the 8 B fragments of the wave's x rows, 4 MFMAs each.
     auto compute = [&](const unsigned char* st) {
         const half_t* xs = reinterpret_cast<const half_t*>(st);
         const uint32_t* ws = reinterpret_cast<const uint32_t*>(st + L::X_BYTES);
@@ -898,7 +531,7 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
         uint32_t zsp[4], ssp[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            zsp[c] = c & 2 ? zero_splat_x16(zw, 4 * hh + c) : zero_splat(zw, 4 * hh + c);
+            zsp[c] = zero_splat_inplace(zw, 4 * hh + c);
             ssp[c] = as_u32(half2_t{s4[c], s4[c]});
         }
 #pragma unroll
@@ -914,13 +547,13 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
                 const uint32_t od = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_odd);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, magic);
+                    const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, c & 2 ? magic_hi : magic);
                     af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
                 }
             }
 #pragma unroll
             for (int f = 0; f < FM; ++f) {
-                const int r = RW * wm + 16 * f + n16;
+                const int r = 16 * f + n16;
                 const half8_t bf = *reinterpret_cast<const half8_t*>(&xs[r * T5_BK + 8 * ((4 * h + kb) ^ (r & 7))]);
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
@@ -975,20 +608,14 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
         }
     }
 
-    // Columns 2, 3 of each half were computed 16 times too large (exact in fp32).
-#pragma unroll
-    for (int c = 2; c < 4; ++c)
-#pragma unroll
-        for (int f = 0; f < FM; ++f) acc[c][f] *= 0.0625f;
-
-    // acc[c][f] lane value r: out[m0 + RW wm + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
+    // acc[c][f] lane value r: out[m0 + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
     const int pc0 = (n0 >> 3) + 8 * wn + 4 * (kb & 1);
     const int coff = 4 * (kb >> 1);
     if (split_k == 1) {
         if (kh != 0) return;  // KW = 2: the sums are in waves 0..3
 #pragma unroll
         for (int f = 0; f < FM; ++f) {
-            const int m = m0 + RW * wm + 16 * f + n16;
+            const int m = m0 + 16 * f + n16;
             if (m >= a.M) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -1004,7 +631,7 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
     const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
-        const int m = m0 + RW * wm + 16 * f + n16;
+        const int m = m0 + 16 * f + n16;
         if (m >= a.M || kh != 0) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -1026,61 +653,39 @@ __global__ __launch_bounds__(256 * WM * KW, (T5Layout<WM, FM, KW>::PER_CU)) void
 }
 
 int64_t tile_tiles(int M, int N, int variant) {
-    if (variant >= 5 && variant <= kTileVariants) {
+    if (variant >= 6 && variant <= kTileVariants) {
         const int bm = tile5_rows(variant);
         return (int64_t)((M + bm - 1) / bm) * ((N + T5_BN - 1) / T5_BN);
     }
-    if (variant >= 3) return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
-    return (int64_t)((M + T2_BM - 1) / T2_BM) * ((N + T2_BN - 1) / T2_BN);
+    return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
 }
 
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream) {
-    if (cfg.variant == 1) {
-        const int64_t m_tiles = (a.M + BM - 1) / BM;
-        const int64_t n_tiles = (a.N + BN - 1) / BN;
-        const int64_t blocks = m_tiles * n_tiles;
+    if (cfg.variant == 4) {
+        const int64_t blocks = tile_tiles(a.M, a.N, 4) * cfg.split_k;
         if (blocks == 0) return hipSuccess;
-        hipLaunchKernelGGL(awq_tile_kernel_v1, dim3((unsigned)blocks), dim3(256), 0, stream, a);
-        return hipGetLastError();
-    }
-    if (cfg.variant == 2) {
-        const int64_t blocks = tile_tiles(a.M, a.N, 2) * cfg.split_k;
-        if (blocks == 0) return hipSuccess;
-        hipLaunchKernelGGL(awq_tile_kernel_v2, dim3((unsigned)blocks), dim3(256), 0, stream, a, cfg.split_k,
+        hipLaunchKernelGGL(awq_tile_kernel_v3, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
                            cfg.k_per_split, counters);
         return hipGetLastError();
     }
-    if (cfg.variant == 3 || cfg.variant == 4) {
-        const int64_t blocks = tile_tiles(a.M, a.N, 3) * cfg.split_k;
-        if (blocks == 0) return hipSuccess;
-        if (cfg.variant == 3)
-            hipLaunchKernelGGL(awq_tile_kernel_v3<false>, dim3((unsigned)blocks), dim3(512), 0, stream, a,
-                               cfg.split_k, cfg.k_per_split, counters);
-        else
-            hipLaunchKernelGGL(awq_tile_kernel_v3<true>, dim3((unsigned)blocks), dim3(512), 0, stream, a,
-                               cfg.split_k, cfg.k_per_split, counters);
-        return hipGetLastError();
-    }
-    if (cfg.variant >= 5 && cfg.variant <= kTileVariants) {
+    if (cfg.variant >= 6 && cfg.variant <= kTileVariants) {
         const int64_t blocks = tile_tiles(a.M, a.N, cfg.variant) * cfg.split_k;
         if (blocks == 0) return hipSuccess;
         const dim3 grid((unsigned)blocks);
         bool reduce = false;
         switch (cfg.variant) {
-            case 5: hipLaunchKernelGGL((awq_tile_kernel_v5<2, 8, 1, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 6: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 1, 0>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 7: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 8: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 4, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 9: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 2, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 10: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 2, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 11: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 8, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 12: hipLaunchKernelGGL((awq_tile_kernel_v5<1, 4, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 6: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 1, 0>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 7: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 8: hipLaunchKernelGGL((awq_tile_kernel_v5<4, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 9: hipLaunchKernelGGL((awq_tile_kernel_v5<2, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 10: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 2, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 11: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 12: hipLaunchKernelGGL((awq_tile_kernel_v5<4, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
             default: return hipErrorInvalidValue;
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess || !reduce || cfg.split_k <= 1) return e;
         return splitk_reduce_launch(a, cfg.split_k, stream);
-        return hipGetLastError();
     }
     return hipErrorInvalidValue;
 }

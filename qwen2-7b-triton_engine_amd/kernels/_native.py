@@ -11,7 +11,7 @@ import os
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libawq_w4a16.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 AWQ_OK = 0
 AWQ_ERR_NULL_POINTER = -1
@@ -27,10 +27,8 @@ PATH_AUTO = 0
 PATH_SKINNY = 1
 PATH_TILE = 2
 PATH_GEMV = 3
-PATH_NARROW = 4
 PATH_STREAM = 5
-PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile", PATH_GEMV: "gemv", PATH_NARROW: "narrow",
-              PATH_STREAM: "stream"}
+PATH_NAMES = {PATH_AUTO: "auto", PATH_SKINNY: "skinny", PATH_TILE: "tile", PATH_GEMV: "gemv", PATH_STREAM: "stream"}
 
 
 class Plan(ctypes.Structure):
@@ -72,8 +70,6 @@ SIGNATURES = {
     "awq_w4a16_plan_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                            ctypes.POINTER(Plan)]),
     "awq_w4a16_plan_tile": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, ctypes.POINTER(Plan)]),
-    "awq_w4a16_plan_narrow": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
-                                             ctypes.POINTER(Plan)]),
     "awq_w4a16_plan_stream": (ctypes.c_int, [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32,
                                               ctypes.POINTER(Plan)]),
     "awq_w4a16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I32]),
@@ -147,24 +143,11 @@ def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, varian
     return p
 
 
-def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant: int = 1, split_k: int = 0,
-              depth: int | None = None, tile_n: int = 512, group_size: int = 128) -> Plan:
-    if depth is None:
-        depth = 0 if variant == 1 else 2
+def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant: int = 5, split_k: int = 1,
+              depth: int = 2, tile_n: int = 512, group_size: int = 128) -> Plan:
     p = Plan()
     check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, variant, tile_n, rows_per_wave, k_waves, split_k, depth,
                                     ctypes.byref(p)), "awq_w4a16_plan_gemv")
-    return p
-
-
-def plan_narrow(M: int, N: int, K: int, rows_per_wave: int, split_k: int, depth: int = 2,
-                factored_scale: int | None = None, group_size: int = 128) -> Plan:
-    """Narrow-M path (M <= 16): GEMV schedule, 4x4x4 MFMA arithmetic."""
-    if factored_scale is None:
-        factored_scale = 0
-    p = Plan()
-    check(lib().awq_w4a16_plan_narrow(M, N, K, group_size, rows_per_wave, split_k, depth, factored_scale,
-                                      ctypes.byref(p)), "awq_w4a16_plan_narrow")
     return p
 
 
@@ -185,12 +168,7 @@ def plan_stream(M: int, N: int, K: int, k_waves: int, split_k: int, variant: int
     return p
 
 
-def plan_gemv_col(M: int, N: int, K: int, tile_n: int, depth: int = 2, group_size: int = 128) -> Plan:
-    """GEMV variant 3: one 16-wave workgroup per ``tile_n``-column strip, whole K."""
-    return plan_gemv(M, N, K, 0, 16, variant=3, split_k=1, depth=depth, tile_n=tile_n, group_size=group_size)
-
-
-def plan_tile(M: int, N: int, K: int, variant: int = 2, split_k: int = 1, group_size: int = 128) -> Plan:
+def plan_tile(M: int, N: int, K: int, variant: int = 6, split_k: int = 1, group_size: int = 128) -> Plan:
     p = Plan()
     check(lib().awq_w4a16_plan_tile(M, N, K, group_size, variant, split_k, ctypes.byref(p)), "awq_w4a16_plan_tile")
     return p

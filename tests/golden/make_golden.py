@@ -18,9 +18,10 @@ Inputs come from ``random.Random`` with fixed seeds.  Two fixtures:
 * ``awq_golden_small.npz``: M=5, K=256, N=64, G=128, random codes and
   scales in [0.002, 0.02);
 * ``awq_golden_edge.npz``: M=3, K=128, N=64, G=128, scales chosen to reach
-  the fp16 corner cases (subnormal results, ties, overflow to infinity,
-  negative scales, signed zeros), codes hitting every nibble value in every
-  slot, and words with the sign bit set.
+  the fp16 corner cases (subnormal results, ties, weights past 4096 and up
+  to the fp16 maximum, overflow to infinity, negative scales, signed zeros),
+  codes hitting every nibble value in every slot, and words with the sign
+  bit set.
 
 Run from the repository root: ``python tests/golden/make_golden.py``.
 """
@@ -147,6 +148,13 @@ def edge():
         0x1000,  # 2^-11
         0x7800,  # 32768: overflow for |q-z| >= 2
         0x3555,  # ~1/3
+        0x6000,  # 512: |w| up to 7680, past 4096
+        0x6A00,  # 3072: |w| up to 46080, finite
+        0x7400,  # 16384: finite for |q-z| <= 3, 65536 rounds to inf
+        0x7A01,  # 49184: finite only for |q-z| <= 1
+        0x0200,  # 2^-15 (subnormal): every product subnormal
+        0x0155,  # subnormal with an odd mantissa
+        0x0401,  # 2^-14 (1 + 2^-10): products at the subnormal/normal boundary
     ]
     rs = random.Random(201)
     s_row = special + [f16_bits(rs.uniform(2.0 ** -14, 2.0)) for _ in range(N - len(special))]

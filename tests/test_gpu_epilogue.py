@@ -25,18 +25,16 @@ def _plans(m, n, k):
     """The AUTO plan, every path's own plan, and forced variants that cover
     each split-K finish (fixed-point slots, last arriver, reduce launch)."""
     makers = [("auto", lambda: _native.plan_for(m, n, k))]
-    for path in (_native.PATH_GEMV, _native.PATH_STREAM, _native.PATH_SKINNY, _native.PATH_NARROW,
-                 _native.PATH_TILE):
+    for path in (_native.PATH_GEMV, _native.PATH_STREAM, _native.PATH_SKINNY, _native.PATH_TILE):
         makers.append((_native.PATH_NAMES[path], lambda path=path: _native.plan_for(m, n, k, path=path)))
     if m <= 2:
         makers += [(f"gemv quad v{v} s{sp}", lambda v=v, sp=sp: _native.plan_gemv(m, n, k, 0, 4, variant=v, split_k=sp))
                    for v in (4, 5) for sp in (1, 3, 16)]
     if m <= 16:
         makers += [(f"stream v{v} s4", lambda v=v: _native.plan_stream(m, n, k, 2, 4, variant=v)) for v in (1, 2, 3)]
-        makers += [(f"narrow s{sp}", lambda sp=sp: _native.plan_narrow(m, n, k, 4, sp)) for sp in (1, 4)]
     if m > 16:
         makers += [(f"tile v{v} s{sp}", lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp))
-                   for v, sp in ((1, 1), (2, 2), (4, 2), (5, 1), (6, 2), (7, 3), (8, 2), (9, 4), (10, 1), (11, 2),
+                   for v, sp in ((4, 1), (4, 2), (6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (10, 1), (11, 2),
                                  (12, 2))]
     out = []
     for label, make in makers:

@@ -120,20 +120,21 @@ def test_auto_plan_invariants(L, m, k, n):
 @pytest.mark.parametrize("k,n", SHAPES)
 def test_tile_plans_cover_k_exactly(L, k, n):
     """Every split-K plan gives each split a whole number of 64-row k-steps
-    (variants 5..9: of 128-row groups) and covers K exactly; the tile count fits
-    the arrival-counter block."""
-    for variant in range(2, 13):
+    (variants 6..12: of 128-row groups) and covers K exactly; the tile count fits
+    the arrival-counter block.  Variant numbers without a kernel are refused."""
+    for variant in range(1, 14):
         for split in (1, 2, 3, 4, 5, 8):
             try:
                 p = _native.plan_tile(512, n, k, variant, split)
             except _native.AwqNativeError as e:
                 assert e.status == _native.AWQ_ERR_PATH
                 continue
+            assert variant == 4 or 6 <= variant <= 12
             per = p.rows_per_wave
-            assert per % (128 if variant >= 5 else 64) == 0
+            assert per % (128 if variant >= 6 else 64) == 0
             assert (split - 1) * per < k <= split * per
-            tm = {3: 256, 4: 256, 5: 256, 6: 128, 7: 128, 8: 64, 9: 32, 12: 64}.get(variant, 128)
-            tn = 256 if variant >= 5 else 128
+            tm = {4: 256, 6: 128, 7: 128, 8: 64, 9: 32, 12: 64}.get(variant, 128)
+            tn = 256 if variant >= 6 else 128
             tiles = -(-512 // tm) * -(-n // tn)
             assert p.grid == tiles * split
             if split > 1:
@@ -142,29 +143,28 @@ def test_tile_plans_cover_k_exactly(L, k, n):
 
 def test_skinny_and_gemv_plan_rejections():
     with pytest.raises(_native.AwqNativeError) as e:
-        _native.plan_gemv(3, 512, 3584, 64, 8)          # GEMV serves M <= 2
+        _native.plan_gemv(3, 512, 3584, 0, 4)           # GEMV serves M <= 2
     assert e.value.status == _native.AWQ_ERR_PATH
     with pytest.raises(_native.AwqNativeError):
-        _native.plan_gemv(1, 512, 3584, 48, 8)          # rows per wave not an instance
-    with pytest.raises(_native.AwqNativeError):
-        _native.plan_gemv(1, 512, 3584, 64, 8, split_k=2)   # variant 1 derives split_k
+        _native.plan_gemv(1, 512, 3584, 16, 8, variant=2, depth=5)   # depth not an instance
+    for variant in (1, 3, 6):                           # no GEMV kernel of that number
+        with pytest.raises(_native.AwqNativeError):
+            _native.plan_gemv(1, 512, 3584, 16, 8, variant=variant)
     with pytest.raises(_native.AwqNativeError):
         _native.plan_gemv(1, 512, 3584, 16, 4, variant=2, split_k=2)   # k_waves must be 128 / rows
     with pytest.raises(_native.AwqNativeError):
         _native.plan_gemv(1, 512, 3584, 16, 8, variant=2, split_k=9)   # 28 groups: no split of 9 whole chunks
     p = _native.plan_gemv(1, 512, 3584, 16, 8, variant=2, split_k=7)
     assert (p.split_k, p.grid, p.block_threads) == (7, 7, 512)
-    with pytest.raises(_native.AwqNativeError):
-        _native.plan_gemv_col(1, 512, 3584, 48)                          # strip width not an instance
-    p = _native.plan_gemv_col(1, 3584, 3584, 128)
-    # 28 strips of 16 packed columns, grouped by 128-byte line onto 8 XCDs: 2 strips per line.
-    assert (p.grid, p.block_threads, p.workspace_bytes) == (32, 1024, 0)
+    p = _native.plan_gemv(1, 3584, 3584, 0, 4, variant=5, split_k=36)
+    # 7 strips of 64 packed columns x 36 splits; one 64-bit fixed-point slot per output
+    assert (p.grid, p.block_threads, p.workspace_bytes) == (252, 256, _native.counter_bytes() + 3584 * 8)
     with pytest.raises(_native.AwqNativeError):
         _native.plan_skinny(65, 512, 3584, 256, 2)      # skinny serves M <= 64
     with pytest.raises(_native.AwqNativeError):
         _native.plan_skinny(8, 512, 3584, 256, 3)       # k_waves must be 1, 2 or 4
     with pytest.raises(_native.AwqNativeError):
-        _native.plan_tile(512, 512, 3584, 1, 2)         # variant 1 has no split-K
+        _native.plan_tile(512, 512, 3584, 5, 1)         # no tile kernel of that number
     with pytest.raises(_native.AwqNativeError):
         _native.plan_tile(512, 512, 3584, 13, 1)
 
@@ -172,7 +172,7 @@ def test_skinny_and_gemv_plan_rejections():
 def test_planned_call_rejects_altered_plan(L):
     """gemm_planned re-derives the plan: a hand-edited field is refused before launch."""
     m, n, k = 512, 3584, 3584
-    p = _native.plan_tile(m, n, k, 3, 1)
+    p = _native.plan_tile(m, n, k, 4, 1)
     p.grid += 1
     buf = np.zeros(1 << 12, dtype=np.uint8)
     ptr = ctypes.c_void_p((buf.ctypes.data + 255) & ~255)

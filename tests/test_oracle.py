@@ -378,3 +378,50 @@ def test_planted_mistakes(mutant):
     dequant = _dequant_with(**kw)
     gemm = _gemm_with(dequant, transpose_x=transpose_x)
     assert _pin_failures(unpack, dequant, gemm), f"planted mistake '{mutant}' passed every check"
+
+
+# ---------------------------------------------------------------------------
+# The timed CPU baseline (oracle/cpu_baseline.py) computes the same thing
+# ---------------------------------------------------------------------------
+
+def _cpu_baseline(x, qw, qz, s):
+    import torch
+
+    from oracle.cpu_baseline import torch_awq_gemm_cpu
+    T = torch.from_numpy
+    return torch_awq_gemm_cpu(T(np.ascontiguousarray(x)), T(np.ascontiguousarray(qw)),
+                              T(np.ascontiguousarray(qz)), T(np.ascontiguousarray(s))).numpy()
+
+
+def test_cpu_baseline_one_hot_reproduces_oracle_weight():
+    """One-hot rows through the timed torch-CPU baseline return the oracle's
+    fp16 weight bit for bit, on random scales and on the edge fixture's
+    finite columns: the baseline's unpack order, zero subtraction, group
+    indexing and single fp16 rounding are the oracle's."""
+    _, qw, qz, s = O.make_inputs(1, 384, 136, seed=81)
+    d = _golden("awq_golden_edge.npz")
+    _, qw_e, qz_e, s_e = _fixture_operands(d)
+    keep = np.isfinite(d["w_f16_bits"].view(np.float16)).all(axis=0)
+    for qw_, qz_, s_, cols in ((qw, qz, s, slice(None)), (qw_e, qz_e, s_e, keep)):
+        k = qw_.shape[0]
+        x = np.eye(k, dtype=np.float16)
+        y = _cpu_baseline(x, qw_, qz_, s_)[:, cols]
+        w = O.dequant_awq(qw_, qz_, s_)[:, cols]
+        assert np.array_equal((y + np.float16(0)).view(np.uint16), (w + np.float16(0)).view(np.uint16))
+
+
+@pytest.mark.parametrize("name", ["awq_golden_small.npz"])
+def test_cpu_baseline_matches_golden_gemm(name):
+    d = _golden(name)
+    x, qw, qz, s = _fixture_operands(d)
+    y = _cpu_baseline(x, qw, qz, s).astype(np.float64)
+    assert O.max_rel_err(y, d["y_f64"]) <= 1e-3
+    assert O.elementwise_violations(y, d["y_f64"], 1e-2) == 0
+
+
+def test_cpu_baseline_matches_oracle_random():
+    for m, k, n in ((1, 1024, 512), (5, 512, 264), (33, 256, 64)):
+        x, qw, qz, s = O.make_inputs(m, k, n, seed=82 + m)
+        y = _cpu_baseline(x, qw, qz, s).astype(np.float64)
+        y_ref = O.awq_gemm_oracle(x, qw, qz, s).astype(np.float64)
+        assert O.max_rel_err(y, y_ref) <= 1e-2 and O.elementwise_violations(y, y_ref, 1e-2) == 0
