@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -38,6 +39,9 @@ VOCAB = 152064
 ENGINE_SHAPES = (("qkv_proj", HIDDEN, 4608), ("o_proj", HIDDEN, HIDDEN),
                  ("gate_up_proj", HIDDEN, 2 * INTER), ("down_proj", INTER, HIDDEN))
 DECODE_M = (1, 4, 16)
+# Weight bytes every per-shape timing cycles through: 2.5x the 256 MB MALL,
+# so that each launch reads its weights from HBM.
+MIN_ROTATE_BYTES = 640e6
 
 
 def log(*a):
@@ -85,14 +89,12 @@ def kernel_family(_native, m, n, k):
 FAMILY_KERNELS = {
     "gemv": ("awq_gemv",),
     "skinny": ("awq_skinny",),
-    "narrow": ("awq_narrow",),
     "stream": ("awq_stream", "awq_splitk_reduce"),
     "tile": ("awq_tile", "awq_splitk_reduce"),
 }
 FAMILY_NAMES = {
     "gemv": "awq_gemv_quad_kernel",
     "skinny": "awq_skinny_kernel",
-    "narrow": "awq_narrow_kernel",
     "stream": "awq_stream_row_kernel / awq_stream_kernel (+ awq_splitk_reduce_kernel)",
     "tile": "awq_tile_kernel (+ awq_splitk_reduce_kernel)",
 }
@@ -104,7 +106,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of timed CPU work")
+    ap.add_argument("--cpu-budget", type=float, default=90.0,
+                    help="seconds of CPU baseline work after which each remaining config gets one timed run")
     ap.add_argument("--no-extras", action="store_true", help="headline only (for profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the end-to-end decode extra (its ~230k kernel launches swamp a kernel trace)")
@@ -209,7 +212,14 @@ def main():
         "cpu_baseline": None,
     }
 
-    # ---- per-GEMM times: each (M, shape) over the 28 layers in one graph ---
+    # ---- per-GEMM times: each (M, shape) over >= 640 MB of weights in one graph
+    def rotation(k, n, base=(), seed=90000):
+        need = max(len(base), 2, math.ceil(MIN_ROTATE_BYTES / (k * n // 2)))
+        ws = list(base)
+        while len(ws) < need:
+            ws.append(make_weights(torch, dev, k, n, seed + len(ws)))
+        return ws
+
     def per_launch(m, k, n, weights):
         x = xs[(m, k)] if (m, k) in xs else torch.randn((m, k), device=dev).half()
         awq_gemm_forward(x, *weights[0])
@@ -222,11 +232,14 @@ def main():
 
     per_gemm = []
     family_time, family_bytes, family_launches = {}, {}, {}
+    rot = {name: rotation(k, n, [layers[li][name] for li in range(LAYERS)], seed=90000 + 1000 * j)
+           for j, (name, k, n) in enumerate(ENGINE_SHAPES)}
     for m in DECODE_M:
         for name, k, n in ENGINE_SHAPES:
-            t = per_launch(m, k, n, [layers[li][name] for li in range(LAYERS)])
+            t = per_launch(m, k, n, rot[name])
             b = algorithmic_bytes(m, n, k)
             fam = kernel_family(_native, m, n, k)
+            log(f"{name} M={m}: {t * 1e6:.2f} us ({fam}, {len(rot[name])} weight copies)")
             per_gemm.append({"shape": name, "M": m, "K": k, "N": n, "us": round(t * 1e6, 2), "kernel": fam,
                              "GBps": round(b / t / 1e9, 1), "hbm_frac": round(b / t / HBM_PEAK_BPS, 3)})
             family_time[fam] = family_time.get(fam, 0.0) + t * LAYERS
@@ -275,10 +288,10 @@ def main():
         for name, k, n in QWEN2_7B_LINEARS:
             if name in ("v_proj", "up_proj", "o_proj"):
                 continue  # same shape as k_proj / gate_proj / q_proj
-            copies = max(2, min(LAYERS, int(640e6 // (k * n // 2)) + 1))
-            ws = [make_weights(torch, dev, k, n, 50000 + c) for c in range(copies)]
+            ws = rotation(k, n, seed=50000)
             for m in DECODE_M:
                 t = per_launch(m, k, n, ws)
+                log(f"unfused {name} M={m}: {t * 1e6:.2f} us ({len(ws)} weight copies)")
                 b = algorithmic_bytes(m, n, k)
                 sweep.append({"shape": name, "M": m, "K": k, "N": n, "us": round(t * 1e6, 2),
                               "kernel": kernel_family(_native, m, n, k),
@@ -286,19 +299,22 @@ def main():
             del ws
         result["per_gemm_unfused_shapes"] = sweep
 
-        # prefill gate||up at M = 2048 and the down_proj M-sweep
-        def mfma_point(m, k, n, copies):
-            ws = [make_weights(torch, dev, k, n, 70000 + c) for c in range(copies)]
-            t = per_launch(m, k, n, ws)
+        # prefill at M = 2048 on the four engine shapes, and the down_proj M-sweep
+        def mfma_point(m, k, n, weights, name=None):
+            t = per_launch(m, k, n, weights)
             f = flops(m, n, k)
             b = algorithmic_bytes(m, n, k)
-            del ws
-            return {"M": m, "K": k, "N": n, "us": round(t * 1e6, 2), "kernel": kernel_family(_native, m, n, k),
-                    "TFLOPs": round(f / t / 1e12, 1), "mfma_frac": round(f / t / MFMA_F16_DENSE_PEAK_FLOPS, 4),
-                    "GBps": round(b / t / 1e9, 1), "hbm_frac": round(b / t / HBM_PEAK_BPS, 3)}
+            log(f"{name or 'down_proj'} M={m}: {t * 1e6:.2f} us, {f / t / 1e12:.1f} TFLOP/s")
+            row = {"shape": name} if name else {}
+            row.update({"M": m, "K": k, "N": n, "us": round(t * 1e6, 2), "kernel": kernel_family(_native, m, n, k),
+                        "TFLOPs": round(f / t / 1e12, 1), "mfma_frac": round(f / t / MFMA_F16_DENSE_PEAK_FLOPS, 4),
+                        "GBps": round(b / t / 1e9, 1), "hbm_frac": round(b / t / HBM_PEAK_BPS, 3)})
+            return row
 
-        result["prefill_gate_up"] = mfma_point(2048, HIDDEN, 2 * INTER, 4)
-        result["down_m_sweep"] = [mfma_point(m, INTER, HIDDEN, 4 if m >= 512 else 16) for m in (1, 8, 64, 512, 2048)]
+        result["prefill_m2048"] = [mfma_point(2048, k, n, rot[name][:4], name) for name, k, n in ENGINE_SHAPES]
+        result["prefill_gate_up"] = next(r for r in result["prefill_m2048"] if r["shape"] == "gate_up_proj")
+        result["down_m_sweep"] = [mfma_point(m, INTER, HIDDEN, rot["down_proj"][:4] if m >= 512 else rot["down_proj"])
+                                  for m in (1, 8, 64, 512, 2048)]
 
         # fp16 lm_head GEMV (vocab x hidden, 1.09 GB per token), next to torch's own F.linear
         from kernels.lm_head import lm_head_forward
@@ -317,6 +333,7 @@ def main():
                 t = min(time_graph(torch, g, 5) for _ in range(3)) / len(lm_ws)
                 row[key] = round(t * 1e6, 2)
                 del g
+            log(f"lm_head M={m}: {row['us']} us (torch F.linear {row['torch_linear_us']} us)")
             row["GBps"] = round(lm_bytes / (row["us"] * 1e-6) / 1e9, 1)
             row["hbm_frac"] = round(lm_bytes / (row["us"] * 1e-6) / HBM_PEAK_BPS, 3)
             lm.append(row)
@@ -331,8 +348,10 @@ def main():
         torch.cuda.empty_cache()
         e2e = Qwen2AwqDecoder(QWEN2_7B, max_seq_len=1024 + 128, seed=0, device=dev)
         prompt = torch.randint(0, QWEN2_7B.vocab_size, (1024,), generator=torch.Generator().manual_seed(1))
+        log("e2e decode: capture + warm-up")
         e2e.generate(prompt, 128)                      # capture + warm-up
         r = e2e.generate(prompt, 128)
+        log(f"e2e decode: {r['decode_tokens_per_s']:.1f} tokens/s")
         result["e2e_decode"] = {
             "layers": QWEN2_7B.num_layers, "prompt_tokens": 1024, "new_tokens": 128,
             "prefill_ms": round(r["prefill_s"] * 1e3, 2),
@@ -345,34 +364,62 @@ def main():
         torch.cuda.empty_cache()
 
     # ---- CPU baseline: the reference's dequant + matmul on the host --------
+    # Configs 0-3 on a bounded sample: torch-CPU fp16 matmul runs at about
+    # 1-2 GFLOP/s on this host (no native fp16 GEMM), so a config whose full
+    # size would take minutes is timed on its first `rows` rows of x (the
+    # matmul, which dominates, is linear in the rows) and its full-size time
+    # is projected from the sample's FLOP rate.  1 warm-up + median of 5 timed
+    # runs (3 for samples of the M >= 512 configs), all host threads.
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import time_cpu_baseline  # reported baseline, not the product
 
         threads = min(16, os.cpu_count() or 1)
-        total_b = total_t = 0.0
-        spent = 0.0
-        done = []
-        for j, (name, k, n) in enumerate(ENGINE_SHAPES):
-            if spent >= args.cpu_budget:
-                break
-            qw, qz, sc = (t.cpu() for t in layers[0][name])
-            x = xs[(1, k)].cpu()
-            r = time_cpu_baseline(x, qw, qz, sc, reps=3, warmup=1, threads=threads,
-                                  budget_s=max(1.0, args.cpu_budget - spent))
-            spent += r["median_s"] * (r["reps"] + 1)
-            total_b += algorithmic_bytes(1, n, k)
-            total_t += r["median_s"]
-            done.append(name)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(11)
+        # (config, shape, full M, sampled rows, K, N, weights)
+        samples = [("0: q_proj GEMV (a 3584 x 3584 weight)", "q_proj", 1, 1, HIDDEN, HIDDEN, layers[0]["o_proj"])]
+        samples += [("1: decode sweep, layer 0", name, m, m, k, n, layers[0][name])
+                    for m in (1, 4) for name, k, n in ENGINE_SHAPES]
+        samples += [("2: prefill gate_up", "gate_up_proj", 2048, 4, HIDDEN, 2 * INTER, layers[0]["gate_up_proj"])]
+        samples += [("3: down_proj M-sweep", "down_proj", m, min(m, 8), INTER, HIDDEN, layers[0]["down_proj"])
+                    for m in (1, 8, 64, 512, 2048)]
+        rows, r, spent, cache = [], None, 0.0, {}
+        for cfg, name, m, ms, k, n, w in samples:
+            if (name, ms, k, n) in cache:            # the same sampled computation as an earlier row
+                r = cache[(name, ms, k, n)]
+            else:
+                qw, qz, sc = (t.cpu() for t in w)
+                x = torch.randn((ms, k), generator=gen, device=dev).half().cpu()
+                t0 = time.perf_counter()
+                r = time_cpu_baseline(x, qw, qz, sc, reps=3 if m >= 512 else 5, warmup=1, threads=threads,
+                                      budget_s=max(1e-3, args.cpu_budget - spent))
+                spent += time.perf_counter() - t0
+                cache[(name, ms, k, n)] = r
+            rate = flops(ms, n, k) / r["median_s"]
+            full_s = r["median_s"] if ms == m else flops(m, n, k) / rate
+            log(f"cpu baseline {cfg} {name} M={m} ({ms} rows timed): median {r['median_s']:.4f} s of {r['reps']}"
+                f", full size {full_s:.3f} s")
+            rows.append({"config": cfg, "shape": name, "M": m, "K": k, "N": n, "rows_timed": ms,
+                         "median_s": round(r["median_s"], 5), "reps": r["reps"],
+                         "full_size_s": round(full_s, 4) if ms == m else round(full_s, 2),
+                         "projected": ms != m,
+                         "GBps": round(algorithmic_bytes(m, n, k) / full_s / 1e9, 4),
+                         "TFLOPs": round(flops(m, n, k) / full_s / 1e12, 6)})
+        sweep = [row for row in rows if row["config"].startswith("1:")]
+        sweep_b = sum(algorithmic_bytes(row["M"], row["N"], row["K"]) for row in sweep)
+        sweep_t = sum(row["median_s"] for row in sweep)
         result["cpu_baseline"] = {
-            "value": round(total_b / total_t / 1e9, 3),
+            "value": round(sweep_b / sweep_t / 1e9, 4),
             "unit": "GB/s",
             "cores": r["threads"],
             "kind": "port",
-            "sample": f"layer 0 GEMMs {'+'.join(done)} at M=1 (torch-CPU restatement of the reference's "
-                      f"dequant+matmul, test/compare_benchmark.py:72-95), 1 warm-up + median of up to 3",
+            "sample": "value: layer 0 of the decode sweep at M = 1 and 4 (qkv, o, gate_up, down; 8 of the 336 "
+                      "GEMMs of a step) through the torch-CPU restatement of the reference's dequant+matmul "
+                      "(test/compare_benchmark.py:72-95), 1 warm-up + median of 5; per_config: configs 0-3, the "
+                      "M = 2048 gate_up and the down M >= 64 rows timed on 4 / 8 rows of x and projected by FLOP rate",
             "cpu_model": r["cpu_model"],
             "os_cpu_count": r["os_cpu_count"],
-            "seconds_per_step_equiv": round(total_t / total_b * step_bytes, 3),
+            "per_config": rows,
         }
 
     print(json.dumps(result), flush=True)

@@ -165,6 +165,56 @@ __device__ __forceinline__ u32x4 buf_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t 
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
+// Direct global->LDS loads: buffer_load_dword[x4] ... lds writes each lane's
+// 4 (16) bytes to M0 + 4*lane (16*lane), so a wave fills one contiguous LDS
+// block per instruction and each lane chooses which global element lands in
+// its slot; no VGPR holds the data, so many can be in flight.  Issued from
+// inline assembly: the compiler cannot tell which LDS bytes such a load
+// writes and would otherwise wait for every outstanding load before each LDS
+// read.  The caller waits itself (s_waitcnt vmcnt, then a barrier).
+__device__ __forceinline__ void buffer_load_lds_x4(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %0, %1, %2 offen lds"
+        :
+        : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_base)
+        : "memory", "m0");
+}
+__device__ __forceinline__ void buffer_load_lds_x1(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %0, %1, %2 offen lds"
+        :
+        : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_base)
+        : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p);
+}
+
+__device__ __forceinline__ u32x4 raw_rsrc(const void* base, uint32_t num_bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, num_bytes, 0x00020000u};
+}
+
+// s_waitcnt vmcnt(n * LOADS) for a wave-uniform n in 0 .. N (immediate
+// operands only, hence the chain).
+template <int LOADS, int N>
+__device__ __forceinline__ void wait_batches(int n) {
+    if constexpr (N > 0) {
+        if (n >= N) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N * LOADS) : "memory");
+            return;
+        }
+        wait_batches<LOADS, N - 1>(n);
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
 // Device-scope (cache policy SC1) 16-byte store and load: coherent across
 // the XCDs of the device without whole-L2 maintenance.
 constexpr int kCpolSC1 = 16;

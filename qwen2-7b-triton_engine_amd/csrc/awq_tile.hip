@@ -58,33 +58,6 @@ constexpr int T3_ZS_WORDS = 128;      // 64 zero-word slots (16 used) + 64 scale
 // s_waitcnt vmcnt(7), expcnt/lgkmcnt at their maxima (gfx9 encoding).
 constexpr int kWaitVm7 = 0x0F77;
 
-__device__ __forceinline__ void buffer_load_lds_x4(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
-    asm volatile(
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %0, %1, %2 offen lds"
-        :
-        : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_base)
-        : "memory", "m0");
-}
-__device__ __forceinline__ void buffer_load_lds_x1(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
-    asm volatile(
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dword %0, %1, %2 offen lds"
-        :
-        : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_base)
-        : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p);
-}
-
-__device__ __forceinline__ u32x4 raw_rsrc(const void* base, uint32_t num_bytes) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    return u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, num_bytes, 0x00020000u};
-}
 }  // namespace
 
 // The next k-step's dequant (LDS reads issued first, VALU and W^T stores) is
@@ -381,21 +354,6 @@ struct T5Layout {
     static constexpr int LOADS = X_LOADS + W_LOADS;
 };
 }  // namespace
-
-// s_waitcnt vmcnt(n * LOADS) for a wave-uniform n in 0 .. N (immediate
-// operands only, hence the chain).
-template <int LOADS, int N>
-__device__ __forceinline__ void wait_batches(int n) {
-    if constexpr (N > 0) {
-        if (n >= N) {
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N * LOADS) : "memory");
-            return;
-        }
-        wait_batches<LOADS, N - 1>(n);
-    } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-}
 
 // FIN (split_k > 1): 0 -- the last workgroup of a tile to arrive adds the
 // partials; 1 -- partials with plain stores, summed by a second launch of

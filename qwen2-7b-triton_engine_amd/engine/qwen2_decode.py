@@ -71,6 +71,23 @@ def _rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).half()
 
 
+def _greedy_token(logits: torch.Tensor) -> torch.Tensor:
+    """Index of the first largest logit, as an int64 [1] tensor, without a
+    reduction that spans workgroups.  A whole-vector ``torch.argmax`` over a
+    vocabulary-sized tensor is a multi-workgroup reduction whose captured
+    graph holds a memset node, and such nodes have given wrong results on
+    graph replays after the first (an out-of-range token follows).  Here each
+    256-logit row is reduced on its own, then the row maxima (a few hundred
+    values, one workgroup) -- the same first-maximum index as torch.argmax."""
+    v = logits.reshape(-1)
+    pad = (-v.numel()) % 256
+    if pad:
+        v = torch.nn.functional.pad(v, (0, pad), value=float("-inf"))
+    vals, idx = v.view(-1, 256).max(dim=1)
+    row = torch.argmax(vals).view(1)
+    return row * 256 + idx.index_select(0, row)
+
+
 def _rotate_half(x: torch.Tensor) -> torch.Tensor:
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
@@ -206,7 +223,7 @@ class Qwen2AwqDecoder:
 
         def step():
             logits = self._forward(self._tok, self._pos, causal=False)
-            nxt = torch.argmax(logits).view(1)
+            nxt = _greedy_token(logits)
             self._out.index_copy_(0, self._pos, nxt)       # out[p] = token generated at position p + 1
             self._tok.copy_(nxt)
             self._pos.add_(1)

@@ -341,3 +341,18 @@ def test_no_valu_inline_asm_in_kernels():
             if re.search(r"\bv_[a-z0-9_]+", body):
                 offenders.append(f"{name}: {body.strip()[:60]}")
     assert offenders == [], offenders
+
+
+def test_greedy_token_is_first_argmax():
+    """The harness's graph-safe greedy pick (row maxima, then the best row)
+    returns torch.argmax's index: the first largest logit, ties included."""
+    sys.path.insert(0, os.path.join(ROOT, "qwen2-7b-triton_engine_amd"))
+    from engine.qwen2_decode import _greedy_token
+
+    g = torch.Generator().manual_seed(0)
+    for n in (256, 257, 1000, 152064):
+        for t in range(12):
+            x = torch.randn(n, generator=g).half()
+            if t % 3 == 0:
+                x[torch.randint(0, n, (3,), generator=g)] = x.max()
+            assert int(_greedy_token(x)) == int(torch.argmax(x)), (n, t)
