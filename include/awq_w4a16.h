@@ -56,7 +56,8 @@ typedef enum awq_w4a16_status {
     AWQ_ERR_WORKSPACE = -5,      /* workspace NULL or smaller than required            */
     AWQ_ERR_LAUNCH = -6,         /* the HIP runtime rejected a kernel launch           */
     AWQ_ERR_PATH = -7,           /* unknown kernel path, or path cannot serve this M   */
-    AWQ_ERR_TOO_LARGE = -8       /* M > 2^30, K > 2^22, N > 2^20 or operand > 2^31-1 B */
+    AWQ_ERR_TOO_LARGE = -8,      /* M > 2^30, K > 2^22, N > 2^20 or operand > 2^31-1 B */
+    AWQ_ERR_SCRATCH = -9         /* awq_w4a16_gemm_noalloc: workspace > the static scratch */
 } awq_w4a16_status;
 
 /* Kernel paths.  AUTO lets the shape dispatcher choose (the reference's own
@@ -218,6 +219,26 @@ int awq_w4a16_gemm_planned(const void* x, const int32_t* qweight, const int32_t*
                            const void* scales, void* out, int64_t M, int64_t N, int64_t K,
                            int32_t group_size, void* workspace, size_t workspace_bytes,
                            const awq_w4a16_plan* plan, void* stream);
+
+/* Bytes of the per-device static scratch of awq_w4a16_gemm_noalloc. */
+#define AWQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* As awq_w4a16_gemm, allocating nothing and taking no workspace argument.
+ * No reference counterpart: it is for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  The split-K workspace is a static device array of
+ * AWQ_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on every GPU it
+ * runs on until the process ends; the first call on a device looks up its
+ * address and clears it (one fill kernel on `stream`).  The plan is the AUTO
+ * plan, except that a tile plan whose workspace would exceed the scratch
+ * takes the largest split-K count that fits (so results can differ from
+ * awq_w4a16_gemm in the last bits there); a decode plan that does not fit
+ * (M * N beyond about a million outputs) returns AWQ_ERR_SCRATCH.  Every
+ * call on a GPU shares that GPU's scratch, which each call leaves zero:
+ * calls that overlap on one GPU (other streams, other threads) race. */
+int awq_w4a16_gemm_noalloc(const void* x, const int32_t* qweight, const int32_t* qzeros,
+                           const void* scales, void* out, int64_t M, int64_t N, int64_t K,
+                           int32_t group_size, void* stream);
 
 /* w[K,N] fp16 = fp16((q - z) * s), the dense dequantised weight, bit-exact.
  * Replaces _dequant_to_fp16 / _dequant_awq_kernel (kernels/awq_gemm.py:14-87);

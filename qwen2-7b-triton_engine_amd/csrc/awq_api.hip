@@ -3,6 +3,8 @@
 #include <limits.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/awq_w4a16.h"
 #include "awq_kernels.h"
 
@@ -573,6 +575,71 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
     return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
 }
 
+// ---- the allocation-free entry point (awq_w4a16_gemm_noalloc) ---------------
+//
+// Its split-K workspace is `scratch`, a file-scope device array of
+// AWQ_NOALLOC_SCRATCH_BYTES: the code object loader gives every GPU the
+// library runs on its own copy, at its own address, held until the process
+// ends.  In host code the array's name is only a stand-in for the symbol:
+// set-up asks the runtime for this device's address (hipGetSymbolAddress,
+// with the device current) and the launches use that pointer.  The scratch
+// follows the workspace contract of the other entry points: zero between
+// calls, left zero by every call; set-up clears it once per device.  Every
+// call on a device shares its scratch, so calls that overlap on one GPU race.
+constexpr size_t kScratchBytes = (size_t)AWQ_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+__global__ void awq_zero_fill_kernel(u32x4* p, size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device, once set up
+
+// This device's scratch address; the first call on a device looks it up and
+// clears the array with a fill kernel on the caller's stream (a kernel, not
+// hipMemsetAsync, so that a call under graph capture records no memset node).
+int device_scratch(hipStream_t stream, void** ptr_out);
+
+// The AUTO plan, with the tile path's split-K count lowered until its
+// workspace fits the scratch (split 1 needs none); AWQ_ERR_SCRATCH if a
+// plan of another path needs more.
+int noalloc_plan(int64_t M, int64_t N, int64_t K, int32_t group_size, awq_w4a16_plan* p) {
+    const int st = awq_w4a16_plan_for(M, N, K, group_size, AWQ_PATH_AUTO, p);
+    if (st != AWQ_OK || p->workspace_bytes <= kScratchBytes) return st;
+    if (p->path != AWQ_PATH_TILE) return AWQ_ERR_SCRATCH;
+    for (int64_t sp = p->split_k - 1; sp >= 1; --sp) {
+        awq_w4a16_plan q;
+        if (fill_tile(M, N, K, p->variant, sp, &q) == AWQ_OK && q.workspace_bytes <= kScratchBytes) {
+            *p = q;
+            return AWQ_OK;
+        }
+    }
+    return AWQ_ERR_SCRATCH;
+}
+
+}  // namespace
+
+// File scope, outside the anonymous namespace: the symbol the loader places.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+int device_scratch(hipStream_t stream, void** ptr_out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return AWQ_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return AWQ_ERR_LAUNCH;
+        hipLaunchKernelGGL(awq_zero_fill_kernel, dim3(1024), dim3(256), 0, stream, static_cast<u32x4*>(ptr),
+                           kScratchBytes / 16);
+        if (hipGetLastError() != hipSuccess) return AWQ_ERR_LAUNCH;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *ptr_out = g_scratch_ptr[dev];
+    return AWQ_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -590,6 +657,9 @@ const char* awq_w4a16_error_string(int status) {
         case AWQ_ERR_LAUNCH: return "HIP kernel launch failed";
         case AWQ_ERR_PATH: return "kernel path or plan cannot serve this shape";
         case AWQ_ERR_TOO_LARGE: return "M exceeds 2^30, K exceeds 2^22, N exceeds 2^20, or an operand exceeds 2^31-1 bytes";
+        case AWQ_ERR_SCRATCH:
+            return "the shape's split-K workspace exceeds the allocation-free entry point's static scratch "
+                   "(AWQ_NOALLOC_SCRATCH_BYTES); call awq_w4a16_gemm with a workspace instead";
         default: return "unknown status";
     }
 }
@@ -748,6 +818,21 @@ int awq_w4a16_gemm_epilogue(const void* x, const int32_t* qweight, const int32_t
         awq_w4a16_plan_for(M, N, K, group_size, AWQ_PATH_AUTO, &p);
     }
     return run_plan(x, qweight, qzeros, scales, out, M, N, K, workspace, p, stream, bias, residual);
+}
+
+int awq_w4a16_gemm_noalloc(const void* x, const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                           void* out, int64_t M, int64_t N, int64_t K, int32_t group_size, void* stream) {
+    awq_w4a16_plan p;
+    int st = noalloc_plan(M, N, K, group_size, &p);
+    if (st != AWQ_OK) return st;
+    st = check_pointers(x, qweight, qzeros, scales, out, M);
+    if (st != AWQ_OK || M == 0) return st;
+    void* ws = nullptr;
+    if (p.workspace_bytes > 0) {
+        st = device_scratch(static_cast<hipStream_t>(stream), &ws);
+        if (st != AWQ_OK) return st;
+    }
+    return run_plan(x, qweight, qzeros, scales, out, M, N, K, ws, p, stream);
 }
 
 int awq_silu_mul(const void* gate_up, void* out, int64_t M, int64_t I, void* stream) {

@@ -22,6 +22,8 @@ AWQ_ERR_WORKSPACE = -5
 AWQ_ERR_LAUNCH = -6
 AWQ_ERR_PATH = -7
 AWQ_ERR_TOO_LARGE = -8
+AWQ_ERR_SCRATCH = -9
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 PATH_AUTO = 0
 PATH_SKINNY = 1
@@ -87,6 +89,7 @@ SIGNATURES = {
     "awq_w4a16_gemm_epilogue": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP,
                                                ctypes.c_size_t, ctypes.POINTER(Plan), _VP]),
     "awq_silu_mul": (ctypes.c_int, [_VP, _VP, _I64, _I64, _VP]),
+    "awq_w4a16_gemm_noalloc": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP]),
 }
 
 _lib = None

@@ -343,6 +343,27 @@ def test_no_valu_inline_asm_in_kernels():
     assert offenders == [], offenders
 
 
+def test_noalloc_refuses_shapes_beyond_its_scratch(L):
+    """awq_w4a16_gemm_noalloc refuses a shape whose decode plan needs more
+    workspace than its static scratch with AWQ_ERR_SCRATCH, before touching a
+    pointer or the GPU; bad dimensions are refused first, and M = 0 is a
+    no-op.  (Its GPU results are checked against awq_w4a16_gemm in the GPU
+    tests.)"""
+    m, n, k = 16, 262144, 8192
+    p = _native.plan_for(m, n, k)
+    assert p.path != _native.PATH_TILE and p.workspace_bytes > _native.NOALLOC_SCRATCH_BYTES
+    buf = np.zeros(1 << 12, dtype=np.uint8)
+    ptr = ctypes.c_void_p((buf.ctypes.data + 255) & ~255)
+    assert L.awq_w4a16_gemm_noalloc(ptr, ptr, ptr, ptr, ptr, m, n, k, 128, None) == _native.AWQ_ERR_SCRATCH
+    assert "scratch" in _native.error_string(_native.AWQ_ERR_SCRATCH)
+    assert L.awq_w4a16_gemm_noalloc(ptr, ptr, ptr, ptr, ptr, 1, 12, 128, 128, None) == _native.AWQ_ERR_BAD_DIMS
+    assert L.awq_w4a16_gemm_noalloc(ptr, ptr, ptr, ptr, ptr, 1, 64, 128, 64, None) == _native.AWQ_ERR_GROUP_SIZE
+    assert L.awq_w4a16_gemm_noalloc(None, ptr, ptr, ptr, None, 0, 64, 128, 128, None) == _native.AWQ_OK
+    # A tile plan past the scratch is lowered, not refused: down_proj at M = 2048 (56 MB of partials).
+    big = _native.plan_for(2048, 3584, 18944)
+    assert big.path == _native.PATH_TILE and big.workspace_bytes > _native.NOALLOC_SCRATCH_BYTES
+
+
 def test_greedy_token_is_first_argmax():
     """The harness's graph-safe greedy pick (row maxima, then the best row)
     returns torch.argmax's index: the first largest logit, ties included."""
