@@ -84,8 +84,8 @@ typedef struct awq_w4a16_plan {
     int32_t factored_scale;      /* skinny: 1 = scale applied per group sum, 0 = per weight */
     int32_t depth;               /* gemv variant 2: 128-row chunks in flight per wave; else 0 */
     int64_t grid;                /* workgroups in the one launch                            */
-    uint64_t workspace_bytes;    /* split_k > 1: counter block + fp32 partials or 64-bit
-                                    fixed-point slots (GEMV variant 4, STREAM); else 0   */
+    uint64_t workspace_bytes;    /* split_k > 1: counter block + 64-bit fixed-point slots
+                                    or counters + slot region + fp32 partials; else 0    */
     uint64_t lds_bytes;          /* dynamic LDS per workgroup                               */
 } awq_w4a16_plan;
 
@@ -169,17 +169,24 @@ int awq_w4a16_plan_gemv(int64_t M, int64_t N, int64_t K, int32_t group_size, int
 int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t rows_per_wave,
                           int32_t variant, int32_t k_waves, int32_t split_k, int32_t depth,
                           awq_w4a16_plan* plan);
+/* Bytes of the fixed-point slot region of a workspace (see below). */
+#define AWQ_W4A16_SLOT_BYTES ((size_t)2 << 20)
+
 /* Host-only: bytes of workspace awq_w4a16_gemm needs for this shape
  * (0 if none).  Replaces the module-global _dequant_buffer of
- * kernels/awq_gemm.py:234,255-262, which holds K*N fp16 values; the
- * workspace here holds, for split-K launches, a block of uint32 arrival
- * counters (first awq_w4a16_counter_bytes() bytes) followed by either the
- * fp32 partial sums [split_k, M, N] or one 64-bit fixed-point slot per
- * output element [M, N] (GEMV variants 4, 5 and stream variant 1).  The whole
- * workspace must be zero-filled before it is first used; every call leaves
- * it zero again, so one zeroed workspace serves any number of calls of any
- * path, as long as calls that share it do not run concurrently.  Returns 0
- * for invalid dimensions as well; awq_w4a16_plan_for reports the reason. */
+ * kernels/awq_gemm.py:234,255-262, which holds K*N fp16 values.  The
+ * workspace of a split-K launch is laid out as
+ *   [uint32 arrival counters: awq_w4a16_counter_bytes()]
+ *   [64-bit fixed-point slots, one per output element [M, N]: at most
+ *    AWQ_W4A16_SLOT_BYTES (GEMV variants 4, 5 and stream variant 1)]
+ *   [fp32 partial sums [split_k, M, N] (every other split-K plan)]
+ * and its size is the end of the last region the plan uses.  The counters
+ * and slots must be zero-filled before the first call and every call leaves
+ * them zero; the partials region is never cleared (each call writes every
+ * partial it reads).  So one workspace zero-filled once serves any number of
+ * calls of any path, as long as calls that share it do not run
+ * concurrently.  Returns 0 for invalid dimensions as well;
+ * awq_w4a16_plan_for reports the reason. */
 size_t awq_w4a16_counter_bytes(void);
 size_t awq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size);
 size_t awq_w4a16_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int32_t group_size,

@@ -40,6 +40,11 @@ int check_dims(int64_t M, int64_t N, int64_t K, int32_t G) {
     return AWQ_OK;
 }
 
+// Workspace bytes of a plan that keeps fp32 partials [split, M, N].
+uint64_t partials_workspace(int64_t split, int64_t M, int64_t N) {
+    return kPartialsOffset + (uint64_t)split * (uint64_t)M * (uint64_t)N * 4u;
+}
+
 bool valid_rows_per_wave(int64_t r, int64_t K) {
     if (r == 32 || r == 64) return true;
     return r > 0 && r % kGroup == 0 && r <= K;
@@ -75,8 +80,7 @@ int fill_skinny(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t 
     p->factored_scale = (int32_t)factored;
     p->depth = 0;
     p->grid = skinny_blocks((int)N, (int)K, (int)rows_per_wave, (int)k_waves);
-    p->workspace_bytes =
-        p->split_k > 1 ? skinny_counter_bytes() + (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    p->workspace_bytes = p->split_k > 1 ? partials_workspace(p->split_k, M, N) : 0u;
     p->lds_bytes = skinny_lds_bytes((int)M, mb, (int)k_waves);
     if (p->lds_bytes > kSkinnyLdsBudget) return AWQ_ERR_PATH;
     if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
@@ -150,6 +154,7 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
         p->split_k = (int32_t)split_k;
         p->depth = (int32_t)depth;
         p->grid = gemv_strips((int)N) * split_k;
+        if (split_k > 1 && (uint64_t)M * (uint64_t)N * 8u > kSlotBytes) return AWQ_ERR_PATH;
         p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
         p->lds_bytes = gemv_quad_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves);
         if (p->lds_bytes > kQuadLdsBudget) return AWQ_ERR_PATH;
@@ -170,8 +175,7 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
     } else {
         return AWQ_ERR_PATH;
     }
-    p->workspace_bytes =
-        p->split_k > 1 ? skinny_counter_bytes() + (uint64_t)p->split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    p->workspace_bytes = p->split_k > 1 ? partials_workspace(p->split_k, M, N) : 0u;
     p->lds_bytes = 0;
     if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
@@ -245,6 +249,7 @@ int fill_stream(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t 
         return AWQ_ERR_PATH;
     if (variant == 2 && split_k > 1 && gemv_strips((int)N) * 4 > (int64_t)kCounterBytes) return AWQ_ERR_PATH;
     if (variant == 1 && split_k > kFixMaxSplit) return AWQ_ERR_PATH;
+    if (variant == 1 && split_k > 1 && (uint64_t)M * (uint64_t)N * 8u > kSlotBytes) return AWQ_ERR_PATH;
     if (k_waves < 1 || split_k < 1) return AWQ_ERR_PATH;
     if (!stream_fits((int)M, (int)K, (int)split_k, (int)k_waves, (int)rows_per_wave)) return AWQ_ERR_PATH;
     p->path = AWQ_PATH_STREAM;
@@ -259,7 +264,8 @@ int fill_stream(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t 
     p->depth = (int32_t)depth;
     p->grid = gemv_strips((int)N) * split_k;
     p->workspace_bytes = split_k <= 1 ? 0u
-                         : kCounterBytes + (uint64_t)M * (uint64_t)N * (variant == 1 ? 8u : 4u * (uint64_t)split_k);
+                         : variant == 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u
+                                        : partials_workspace(split_k, M, N);
     p->lds_bytes = stream_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves, (int)rows_per_wave);
     if (p->lds_bytes > kStreamLdsBudget) return AWQ_ERR_PATH;
     if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
@@ -348,8 +354,7 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->split_k = (int32_t)split_k;
     p->rows_per_wave = (int32_t)(per * unit);  // K rows per split
     p->grid = tiles * split_k;
-    p->workspace_bytes =
-        split_k > 1 ? skinny_counter_bytes() + (uint64_t)split_k * (uint64_t)M * (uint64_t)N * 4u : 0u;
+    p->workspace_bytes = split_k > 1 ? partials_workspace(split_k, M, N) : 0u;
     if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
 }
@@ -537,13 +542,12 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         cfg.variant = p.variant;
         cfg.factored = p.factored_scale != 0;
         uint32_t* counters = static_cast<uint32_t*>(workspace);
-        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                              skinny_counter_bytes())
+        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kPartialsOffset)
                                    : nullptr;
         e = launch_skinny(a, cfg, counters, s);
     } else if (p.path == AWQ_PATH_STREAM) {
         a.partials = p.variant >= 2 && p.split_k > 1
-                         ? reinterpret_cast<float*>(static_cast<char*>(workspace) + skinny_counter_bytes())
+                         ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kPartialsOffset)
                          : nullptr;
         e = launch_stream(a, p.split_k, p.k_waves, p.depth, p.rows_per_wave, p.variant - 1,
                           static_cast<uint32_t*>(workspace), s);
@@ -556,8 +560,7 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         const int64_t groups = K / kGroup;
         cfg.chunks_per_split = (int)((groups + p.split_k - 1) / p.split_k);
         cfg.depth = p.depth;
-        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                              skinny_counter_bytes())
+        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kPartialsOffset)
                                    : nullptr;
         e = launch_gemv(a, cfg, static_cast<uint32_t*>(workspace), s);
     } else {
@@ -567,8 +570,7 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         cfg.tile_n = p.tile_n;
         cfg.split_k = p.split_k;
         cfg.k_per_split = p.rows_per_wave;
-        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                              skinny_counter_bytes())
+        a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kPartialsOffset)
                                    : nullptr;
         e = launch_tile(a, cfg, static_cast<uint32_t*>(workspace), s);
     }
@@ -583,8 +585,10 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
 // ends.  In host code the array's name is only a stand-in for the symbol:
 // set-up asks the runtime for this device's address (hipGetSymbolAddress,
 // with the device current) and the launches use that pointer.  The scratch
-// follows the workspace contract of the other entry points: zero between
-// calls, left zero by every call; set-up clears it once per device.  Every
+// follows the workspace contract of the other entry points (counters and
+// fixed-point slots zero between calls and left zero by every call, the
+// partials region rewritten by each call that reads it); set-up clears it
+// once per device.  Every
 // call on a device shares its scratch, so calls that overlap on one GPU race.
 constexpr size_t kScratchBytes = (size_t)AWQ_NOALLOC_SCRATCH_BYTES;
 constexpr int kMaxDevices = 64;

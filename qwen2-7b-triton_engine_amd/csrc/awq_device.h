@@ -372,9 +372,8 @@ __device__ __forceinline__ void finish_batch(unsigned long long* fix, half_t* ou
 //    parameter so that callers that never have many outputs keep their
 //    register footprint).
 // Either way each element is summed in a fixed order, independent of timing.
-// The partials read are overwritten with zeros, so that the whole workspace
-// is zero again when the kernel ends (the fixed-point finish above relies on
-// zero slots, and both share the workspace).
+// The partials are left as they are: the next split-K call writes every
+// partial it reads, and the fixed-point slots live in a region of their own.
 // `fin` holds blockDim.x float4.  Must be called by the whole workgroup.
 template <int U>
 __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t* __restrict__ out,
@@ -407,8 +406,6 @@ __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t*
             const uint32_t off = item_off(item, m, n);
 #pragma unroll 8
             for (int q = part; q < split_k; q += P) s += buf_load_f4_device(rp, off + (uint32_t)q * stride);
-#pragma unroll 8
-            for (int q = part; q < split_k; q += P) buf_store_f4_device(floatx4{0.f, 0.f, 0.f, 0.f}, rp, off + (uint32_t)q * stride);
         }
         if (P > 1) {
             if (valid) fin[t] = s;
@@ -434,12 +431,6 @@ __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t*
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (base + u * nt + t < items) s[u] += buf_load_f4_device(rp, off[u] + (uint32_t)q * stride);
-        }
-        for (int q = 0; q < split_k; ++q) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (base + u * nt + t < items)
-                    buf_store_f4_device(floatx4{0.f, 0.f, 0.f, 0.f}, rp, off[u] + (uint32_t)q * stride);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/awq_w4a16.h"
 #include "awq_device.h"
 
 namespace awq {
@@ -69,7 +70,8 @@ hipError_t launch_dequant(const uint32_t* qweight, const uint32_t* qzeros, const
                           half_t* w, int N, int K, hipStream_t stream);
 
 // counters: skinny_counter_bytes() of zero-filled uint32 arrival counters
-// (left zero on return); a.partials: split_k * M * N floats (split_k > 1).
+// (left zero on return); a.partials: split_k * M * N floats (split_k > 1),
+// at kPartialsOffset in the workspace.
 hipError_t launch_skinny(const GemmArgs& a, const SkinnyConfig& cfg, uint32_t* counters, hipStream_t stream);
 size_t skinny_lds_bytes(int M, int m_blocks, int kw_count);
 int64_t skinny_pairs(int N);
@@ -92,12 +94,11 @@ bool gemv_quad_fits(int M, int K, int split_k, int k_waves);
 // (k_waves <= 4), 4 or 6 (k_waves <= 2).  finish 0: the workspace after the
 // counter block holds M * N zeroed 64-bit fixed-point slots; 1: fp32
 // partials [split_k, M, N] and one arrival counter per strip; 2: fp32
-// partials added by a second kernel launch.  The workspace is left zero on
-// return.
+// partials added by a second kernel launch.  The counter block and the slots
+// are left zero on return.
 constexpr int kStreamHalfLayout = 32;  // rows per chunk
 constexpr int kStreamRowLayout = 16;
-// awq_splitk_reduce_kernel over a.partials [split_k][M][N] fp32 -> a.out,
-// zeroing the partials it reads.
+// awq_splitk_reduce_kernel over a.partials [split_k][M][N] fp32 -> a.out.
 hipError_t splitk_reduce_launch(const GemmArgs& a, int split_k, hipStream_t stream);
 hipError_t launch_stream(const GemmArgs& a, int split_k, int k_waves, int depth, int layout, int finish,
                          uint32_t* counters, hipStream_t stream);
@@ -117,5 +118,13 @@ constexpr int kSkinnyCols = 128;
 // pair of 128-column tiles, so N up to kCounterBytes / 4 * 256 columns.
 constexpr size_t kCounterBytes = 16384;
 constexpr int64_t kMaxN = (int64_t)(kCounterBytes / 4) * 2 * kSkinnyCols;
+// Workspace of a split-K plan: [arrival counters: kCounterBytes]
+// [64-bit fixed-point slots: up to kSlotBytes] [fp32 partials].  Counters
+// and slots are zero between calls (every call leaves them zero); the
+// partials region keeps whatever the last call wrote -- each call writes
+// every partial it reads, so it is never cleared.  Fixed-point plans need
+// M * N * 8 <= kSlotBytes.
+constexpr size_t kSlotBytes = AWQ_W4A16_SLOT_BYTES;
+constexpr size_t kPartialsOffset = kCounterBytes + kSlotBytes;
 
 }  // namespace awq

@@ -460,8 +460,8 @@ __global__ __launch_bounds__(R == 2 ? 512 : 256) void awq_stream_kernel(GemmArgs
 // m, n]), each element summed in split order (deterministic).  P threads
 // share an output quad (splits part, part + P, ...; at most eight loads each,
 // all in flight together) and combine through LDS in part order.  The
-// partials read are overwritten with zeros, so the workspace is zero again
-// when the kernel ends.
+// partials are read once and left as they are (the workspace's partials
+// region is not kept zero).
 __global__ __launch_bounds__(256) void awq_splitk_reduce_kernel(float* __restrict__ partials, half_t* __restrict__ out,
                                                                const half_t* bias, const half_t* residual, int M,
                                                                int N, int split_k, int P) {
@@ -479,8 +479,6 @@ __global__ __launch_bounds__(256) void awq_splitk_reduce_kernel(float* __restric
         const size_t step = stride / 4;  // one split, in float4
 #pragma unroll 8
         for (int sp = part; sp < split_k; sp += P) s += __builtin_nontemporal_load(p + (size_t)sp * step);
-#pragma unroll 8
-        for (int sp = part; sp < split_k; sp += P) p[(size_t)sp * step] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     fin[t] = s;
     __syncthreads();

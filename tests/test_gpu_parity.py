@@ -352,9 +352,10 @@ def test_stream_and_quad_one_hot_bit_exact(gpu):
 
 
 def test_split_k_workspace_left_zero(gpu):
-    """Every split-K finish leaves the whole shared workspace zero (arrival
-    counters reset, partials and fixed-point slots cleared), so it is ready
-    for the next call of any path and for graph replays."""
+    """Every split-K finish leaves the counter block and the fixed-point
+    slot region of the shared workspace zero (arrival counters reset, slots
+    cleared), so it is ready for the next call of any path and for graph
+    replays; the partials region is rewritten by every call that reads it."""
     from kernels import awq_gemm as G
     k, n = 3584, 4608
     cases = [(m, _native.plan_for(m, n, k, path=path))
@@ -373,7 +374,8 @@ def test_split_k_workspace_left_zero(gpu):
         print(f"workspace check M={m} path={name} split={p.split_k}", flush=True)
         y = _run(gpu, x, qw, qz, s, plan_obj=p)
         ws = G._workspaces[gpu.index][-1]
-        assert int((ws.view(torch.int32) != 0).sum().item()) == 0, name
+        kept_zero = (_native.counter_bytes() + _native.SLOT_BYTES) // 4
+        assert int((ws.view(torch.int32)[:kept_zero] != 0).sum().item()) == 0, name
         y2 = _run(gpu, x, qw, qz, s, plan_obj=p)
         assert np.array_equal(y.view(np.uint16), y2.view(np.uint16)), name
 

@@ -111,7 +111,7 @@ def test_auto_plan_invariants(L, m, k, n):
             assert p.workspace_bytes == _native.counter_bytes() + m * n * 8
             assert p.split_k <= 255
         else:
-            assert p.workspace_bytes == _native.counter_bytes() + p.split_k * m * n * 4
+            assert p.workspace_bytes == _native.counter_bytes() + _native.SLOT_BYTES + p.split_k * m * n * 4
     else:
         assert p.workspace_bytes == 0
     assert _native.workspace_bytes(m, n, k) == p.workspace_bytes
