@@ -211,8 +211,11 @@ int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_gemv(M, N, K, 5, 512, 0, w, split, 2, p);
 }
 
+// Column quads while their fixed-point slots (M x N x 8 bytes) fit the slot
+// region; else (and for N % 32 != 0) the K-streaming variant 2, whose fp32
+// partials have no such limit.
 int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    if (N % 32 == 0) return quad_plan(M, N, K, p);
+    if (N % 32 == 0 && quad_plan(M, N, K, p) == AWQ_OK) return AWQ_OK;
     return fill_gemv(M, N, K, 2, 512, 16, 8, stream_split(N, K), 3, p);
 }
 
@@ -272,33 +275,52 @@ int fill_stream(int64_t M, int64_t N, int64_t K, int64_t rows_per_wave, int64_t 
     return AWQ_OK;
 }
 
-// Stream plan (measured on the Qwen2-7B shapes): split K into whole groups
-// so that the grid fills the device with one workgroup per CU, keeping at
-// least two groups per workgroup.  M <= 8: row layout, eight waves sharing
-// every group, one chunk buffer; M <= 16: half-strip layout, four wave
-// pairs, two buffers.  Finish: fixed-point atomics for M <= 4 (one atomic
-// per output element and split: cheapest while M * N * split stays a few
-// hundred thousand); above, the last-arriving workgroup of a strip while the
+// Stream plan (measured on the Qwen2-7B shapes at M = 2 .. 16, every layout,
+// finish, wave count and split of 3 .. 36): split K into groups so that the
+// grid fills the device with one workgroup per CU, keeping about 1.5 groups
+// per workgroup or more (2 x groups / 3 splits at most: 18 on K = 3584,
+// 3 - 4 % faster than 14 at M = 3 and 4).  Layouts:
+//   M <= 2: half-strip layout with two wave pairs where a split holds at
+//     most two groups (K = 3584: 8.3 us against 9.7 for the column-quad
+//     GEMV), else the row layout with four waves and two chunk buffers
+//     (18944 x 3584: 13.0 us against 15.0);
+//   M <= 8: row layout, eight waves sharing every group, one chunk buffer;
+//     at M >= 5 with more than 8 splits, four waves and two buffers
+//     (18944 x 3584: 16.3 us against 17.4 at M = 5, 16.7 against 17.5 at 8);
+//   M <= 16: half-strip layout, four wave pairs, two buffers.
+// Finish: fixed-point atomics for M <= 4 (one atomic per output element and
+// split: cheapest while M * N * split stays a few hundred thousand) while
+// their slots fit; above, the last-arriving workgroup of a strip while the
 // partials it reads stay small (M * split <= 32), else a second launch that
 // adds the partials over the whole device.
 int stream_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (M > kStreamMaxM || N % 32 != 0) return AWQ_ERR_PATH;
-    const bool row = M <= 8;
-    const int64_t layout = row ? kStreamRowLayout : kStreamHalfLayout;
-    const int64_t kw = row ? 8 : 4;
-    const int64_t depth = row ? 1 : 2;
     const int64_t strips = gemv_strips((int)N);
     const int64_t groups = K / kGroup;
     int64_t split = kCUs / strips;
-    if (split > groups / 2) split = groups / 2;
+    if (split > (2 * groups) / 3) split = (2 * groups) / 3;
     if (split < 1) split = 1;
+    const int64_t per = (groups + split - 1) / split;
+    bool row = M <= 8;
+    int64_t kw = row ? 8 : 4;
+    int64_t depth = row ? 1 : 2;
+    if (M <= 2 && per <= 2) {
+        row = false;
+        kw = 2;
+        depth = 2;
+    } else if (M <= 2 || (M >= 5 && row && split > 8)) {
+        kw = 4;
+        depth = 2;
+    }
+    const int64_t layout = row ? kStreamRowLayout : kStreamHalfLayout;
     while (split < groups && (!stream_fits((int)M, (int)K, (int)split, (int)kw, (int)layout) ||
                               stream_lds_bytes((int)M, (int)K, (int)split, (int)kw, (int)layout) > kStreamLdsBudget))
         ++split;
     int64_t variant = 1;
     if (split > 1 && M > 4) variant = M * split <= 32 ? 2 : 3;
-    if (variant == 1 && split > kFixMaxSplit) variant = 3;
-    if (!row && split > 1) {
+    if (variant == 1 && split > 1 && (split > kFixMaxSplit || (uint64_t)M * (uint64_t)N * 8u > kSlotBytes))
+        variant = M * split <= 32 ? 2 : 3;
+    if (M > 8 && split > 1) {
         // Half layout (9 <= M <= 16), measured on 3584 x 37888 (split 3) and
         // 18944 x 3584 (split 36) at M = 9, 12, 16: fewer wave pairs per
         // workgroup -- two for a few splits, three for many -- and the reduce
@@ -312,7 +334,7 @@ int stream_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_stream(M, N, K, layout, variant, kw, split, depth, p);
 }
 
-// AUTO between the stream path and skinny for 2 < M <= 16 (measured on the
+// AUTO between the stream path and skinny for 2 <= M <= 16 (measured on the
 // Qwen2-7B shapes): the stream path for M <= 4 on every shape; above, where
 // the weight is wide (at least 16 strips of 512 columns) or deep (K >= 8192),
 // whose splits keep the partial sums small against the weight stream.
@@ -710,7 +732,7 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
     if (d != AWQ_OK) return d;
     switch (path) {
         case AWQ_PATH_AUTO:
-            if (M <= kGemvMaxM) return gemv_plan(M, N, K, plan);
+            if (M == 1 || (M <= kGemvMaxM && N % 32 != 0)) return gemv_plan(M, N, K, plan);
             if (auto_stream(M, N, K) && stream_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (small_m_tile_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             return auto_skinny(M, N) ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);

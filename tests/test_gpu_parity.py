@@ -178,6 +178,24 @@ def test_auto_small_m_routes(gpu, m, k, n, path, variant, k_waves):
     _assert_close(_run(gpu, x, qw, qz, s), y_ref, f"auto M={m} K={k} N={n}")
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_auto_vocab_wide(gpu, m):
+    """AUTO on a vocab-wide weight (3584 x 152064, the Qwen2-7B LM head's
+    shape) at decode sizes, where the split plans' fixed-point slots
+    (M x N x 8 bytes) may not fit their region and the planner takes an fp32
+    partials finish instead.  Checked against the oracle on three 512-column
+    slices (first, middle, last: each packed column dequantises on its own)."""
+    k, n = 3584, 152064
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=90 + m)
+    p = _native.plan_for(m, n, k)
+    print(f"vocab-wide M={m} auto={_native.PATH_NAMES[p.path]} v{p.variant} split={p.split_k}", flush=True)
+    y = _run(gpu, x, qw, qz, s)
+    for c0 in (0, n // 2 - 256, n - 512):
+        w = O.dequant_awq_f32eval(qw[:, c0 // 8:(c0 + 512) // 8], qz[:, c0 // 8:(c0 + 512) // 8],
+                                  s[:, c0:c0 + 512]).astype(np.float64)
+        _assert_close(y[:, c0:c0 + 512], x.astype(np.float64) @ w, f"vocab-wide M={m} columns {c0}..")
+
+
 @pytest.mark.parametrize("m", [1, 8, 64, 512, 2048])
 def test_gemm_down_m_sweep(gpu, m):
     k, n = _SHAPES["down_proj"]

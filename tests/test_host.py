@@ -80,7 +80,7 @@ def test_auto_plan_invariants(L, m, k, n):
     p = _native.plan_for(m, n, k)
     strips = -(-(n // 8) // 64)            # 512-column strips of the stream path
     stream = n % 32 == 0 and m <= 16 and (m <= 4 or strips >= 16 or k >= 8192)
-    if m <= 2:
+    if m == 1 or (m == 2 and n % 32 != 0):
         assert p.path == _native.PATH_GEMV
     elif stream:
         assert p.path == _native.PATH_STREAM
@@ -115,6 +115,36 @@ def test_auto_plan_invariants(L, m, k, n):
     else:
         assert p.workspace_bytes == 0
     assert _native.workspace_bytes(m, n, k) == p.workspace_bytes
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 262144, 4096), (2, 152064, 3584), (2, 262144, 4096), (3, 262144, 3584),
+                                   (4, 152064, 3584), (4, 65536, 18944)])
+def test_auto_plan_falls_back_when_slots_do_not_fit(L, m, n, k):
+    """Where the fixed-point slots of a split plan (M x N x 8 bytes) exceed the
+    slot region, AUTO still serves the shape, with an fp32-partials finish or
+    without a split, and never asks for more slots than the region holds."""
+    p = _native.plan_for(m, n, k)
+    fixed_point = (p.path == _native.PATH_GEMV and p.variant in (4, 5)) or \
+                  (p.path == _native.PATH_STREAM and p.variant == 1)
+    if p.split_k > 1 and fixed_point:
+        assert m * n * 8 <= _native.SLOT_BYTES
+    if m * n * 8 > _native.SLOT_BYTES and p.split_k > 1:
+        assert not fixed_point
+        assert p.workspace_bytes == _native.counter_bytes() + _native.SLOT_BYTES + p.split_k * m * n * 4
+
+
+def test_auto_stream_split_keeps_a_group_and_a_half_per_split(L):
+    """K = 3584 (28 groups) at M = 2 .. 4: 18 splits, the cap of 2 x groups / 3;
+    M = 2 takes the half-strip layout with two wave pairs there, the row layout
+    with four waves on deep weights (148 groups, 36 splits)."""
+    for m in (2, 3, 4):
+        for n in (4608, 3584):
+            p = _native.plan_for(m, n, 3584)
+            assert p.path == _native.PATH_STREAM and p.split_k == 18
+    p = _native.plan_for(2, 4608, 3584)
+    assert (p.rows_per_wave, p.k_waves, p.depth, p.variant) == (32, 2, 2, 1)
+    p = _native.plan_for(2, 3584, 18944)
+    assert (p.rows_per_wave, p.k_waves, p.depth, p.split_k) == (16, 4, 2, 36)
 
 
 @pytest.mark.parametrize("k,n", SHAPES)
