@@ -187,7 +187,7 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
 // CUs with twice the work), at least 2 chunks per split.
 int64_t stream_split(int64_t N, int64_t K);
 
-// Column-quad GEMV (variant 4) shape: as many K splits as keep the grid
+// Column-quad GEMV (variant 5) shape: as many K splits as keep the grid
 // within one workgroup per CU (a CU holding two workgroups finishes last),
 // four waves per workgroup (measured: interleaved chunks of four waves
 // stream faster than eight), fewer when a workgroup has fewer chunks; more
@@ -199,7 +199,9 @@ int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (split > C) split = C;
     if (split > kFixMaxSplit) split = kFixMaxSplit;
     if (split < 1) split = 1;
-    int64_t w = C / split;
+    // Waves: one per chunk of the split, rounded up, four at most (3584 x 3584
+    // at 36 splits of 3 - 4 chunks: 6.9 us with four waves, 7.1 with three).
+    int64_t w = (C + split - 1) / split;
     if (w > 4) w = 4;
     if (w < 1) w = 1;
     while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w) ||
@@ -448,6 +450,34 @@ int small_m_tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return AWQ_OK;
 }
 
+// The same model priced for the CU that holds the most workgroups: the grid
+// runs in rounds of per_cu x kCUs workgroup slots, every full round puts
+// per_cu workgroups on each CU, the last one ceil(rest / kCUs) on the
+// busiest, and a round costs steps x t1 x (1 + eta (c - 1)) for that CU.
+// tile_cost averages c over the CUs, which fits M <= 1024; above, the
+// busiest CU sets the time: the Qwen2-7B qkv GEMM (3584 x 4608) at M = 2048 /
+// 4096 ran 95.9 / 157 us with the 64-row tile (variant 8: 576 / 1152
+// workgroups, three per CU) against 102 / 175 for variant 6, as this
+// predicts and the average does not, while variant 6 stays the choice for
+// the other three GEMMs (measured best at M = 2048 and 4096).
+double tile_cost_busiest(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
+    const int64_t wg = tile_tiles((int)M, (int)N, t.variant) * split;
+    const int64_t slots = (int64_t)t.per_cu * kCUs;
+    const int64_t steps = 2 * ((K / kGroup + split - 1) / split);
+    const int64_t full = wg / slots, rest = wg % slots;
+    const int64_t c_last = (rest + kCUs - 1) / kCUs;
+    double time = 7.54 + (double)full * (double)steps * t.t1 * (1.0 + t.eta * (double)(t.per_cu - 1));
+    if (rest > 0) time += (double)steps * t.t1 * (1.0 + t.eta * (double)(c_last - 1));
+    if (split > 1) time += 0.14 + (double)split * (double)M * (double)N * 8.0 / 2.07e6;
+    return time;
+}
+
+const TileModel* tile_model(int variant) {
+    for (const TileModel& t : kTileModels)
+        if (t.variant == variant) return &t;
+    return nullptr;
+}
+
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t tiles6 = tile_tiles((int)M, (int)N, 6);
     if (M <= 1024 && tiles6 < 2 * kCUs) {
@@ -484,6 +514,24 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
         const int64_t units = K / kGroup;
         const int64_t per = (units + split6 - 1) / split6;
         split6 = (units + per - 1) / per;
+    }
+    if (M > 1024) {
+        // Variant 6 (split as above), the 64-row tile or the 128-row k-half
+        // pair tile, unsplit: the least busiest-CU time.
+        const int64_t cand[3][2] = {{6, split6}, {8, 1}, {10, 1}};
+        double best = 0.0;
+        int best_i = -1;
+        for (int i = 0; i < 3; ++i) {
+            awq_w4a16_plan q;
+            const TileModel* t = tile_model((int)cand[i][0]);
+            if (t == nullptr || fill_tile(M, N, K, cand[i][0], cand[i][1], &q) != AWQ_OK) continue;
+            const double time = tile_cost_busiest(*t, M, N, K, cand[i][1]);
+            if (best_i < 0 || time < best) {
+                best = time;
+                best_i = i;
+            }
+        }
+        if (best_i >= 0 && fill_tile(M, N, K, cand[best_i][0], cand[best_i][1], p) == AWQ_OK) return AWQ_OK;
     }
     if (tiles6 * split6 >= kCUs && fill_tile(M, N, K, 6, split6, p) == AWQ_OK) return AWQ_OK;
     if (tiles6 <= kCUs && fill_tile(M, N, K, 10, 1, p) == AWQ_OK) return AWQ_OK;
