@@ -313,6 +313,28 @@ def main():
 
         result["prefill_m2048"] = [mfma_point(2048, k, n, rot[name][:4], name) for name, k, n in ENGINE_SHAPES]
         result["prefill_gate_up"] = next(r for r in result["prefill_m2048"] if r["shape"] == "gate_up_proj")
+
+        # The same shapes on torch's dense fp16 GEMM (hipBLASLt; F.linear with an [N, K] fp16
+        # weight, no dequantisation at all), timed the same way over >= 640 MB of weights: the
+        # library's own MFMA efficiency on this chip, next to the fused int4 kernels'.
+        import torch.nn.functional as F
+
+        for row in result["prefill_m2048"]:
+            k, n = row["K"], row["N"]
+            copies = max(2, math.ceil(MIN_ROTATE_BYTES / (k * n * 2)))
+            dense = [(torch.randn((n, k), device=dev) * 0.02).half() for _ in range(copies)]
+            xp = torch.randn((2048, k), device=dev).half()
+            F.linear(xp, dense[0])
+            torch.cuda.synchronize()
+            gg = graph_of(torch, lambda: [F.linear(xp, w) for w in dense])
+            gg.replay()
+            t = min(time_graph(torch, gg, 3) for _ in range(3)) / copies
+            del gg, dense
+            torch.cuda.empty_cache()
+            f = flops(2048, n, k)
+            row["library_fp16_us"] = round(t * 1e6, 2)
+            row["library_fp16_mfma_frac"] = round(f / t / MFMA_F16_DENSE_PEAK_FLOPS, 4)
+            log(f"{row['shape']} M=2048 dense fp16 F.linear: {t * 1e6:.2f} us, {f / t / 1e12:.1f} TFLOP/s")
         result["down_m_sweep"] = [mfma_point(m, INTER, HIDDEN, rot["down_proj"][:4] if m >= 512 else rot["down_proj"])
                                   for m in (1, 8, 64, 512, 2048)]
 
