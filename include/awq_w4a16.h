@@ -98,7 +98,10 @@ int awq_w4a16_abi_version(void);
 const char* awq_w4a16_error_string(int status);
 
 /* Host-only: fill *plan with what awq_w4a16_gemm_ex would launch for this
- * shape and path, after validating the dimensions.  Touches no GPU.
+ * shape and path, after validating the dimensions.  Launches nothing; grids
+ * and split counts are sized for the compute units of the current device
+ * (read once per device; 256, an MI355X, where no device is visible), so a
+ * plan made for one device should be launched on a device of the same kind.
  * Replaces the M-based dispatch of kernels/awq_gemm.py:251 (M <= 4 ->
  * dequant + cuBLAS, else the autotuned Triton GEMM of :152-164). */
 int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size,

@@ -3,6 +3,7 @@
 #include <limits.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "../../include/awq_w4a16.h"
@@ -17,8 +18,24 @@ constexpr int64_t kSkinnyMaxM = 64;
 // LDS the skinny dispatcher allows one workgroup for its K reduction.
 constexpr uint64_t kSkinnyLdsBudget = 64 * 1024;
 
-// Compute units of an MI355X.
-constexpr int64_t kCUs = 256;
+// Compute units of an MI355X: the planner's count where no device answers
+// (a host without a GPU that plans ahead).
+constexpr int64_t kDefaultCUs = 256;
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];  // per device, 0 until looked up
+// Compute units of the current device, looked up once per device: every grid
+// and split count below is sized by it, so a partitioned or smaller device
+// gets grids for its own CU count.
+int64_t cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return kDefaultCUs;
+    int n = g_cus[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = (int)kDefaultCUs;
+    g_cus[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
 // Largest M awq_fp16_linear serves (decode: the last position's logits).
 constexpr int64_t kFp16LinearMaxM = 8;
 
@@ -195,7 +212,7 @@ int64_t stream_split(int64_t N, int64_t K);
 int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t strips = gemv_strips((int)N);
     const int64_t C = K / 32;
-    int64_t split = kCUs / strips;
+    int64_t split = cus() / strips;
     if (split > C) split = C;
     if (split > kFixMaxSplit) split = kFixMaxSplit;
     if (split < 1) split = 1;
@@ -226,7 +243,7 @@ int gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
 int64_t stream_split(int64_t N, int64_t K) {
     const int64_t groups = K / kGroup;
     const int64_t strips = gemv_strips((int)N);
-    int64_t split = kCUs / strips;
+    int64_t split = cus() / strips;
     if (split > groups / 2) split = groups / 2;
     if (split < 1) split = 1;
     const int64_t per = (groups + split - 1) / split;
@@ -299,7 +316,7 @@ int stream_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (M > kStreamMaxM || N % 32 != 0) return AWQ_ERR_PATH;
     const int64_t strips = gemv_strips((int)N);
     const int64_t groups = K / kGroup;
-    int64_t split = kCUs / strips;
+    int64_t split = cus() / strips;
     if (split > (2 * groups) / 3) split = (2 * groups) / 3;
     if (split < 1) split = 1;
     const int64_t per = (groups + split - 1) / split;
@@ -402,7 +419,7 @@ constexpr TileModel kTileModels[] = {
 // Predicted time (microseconds) of a tile plan: a workgroup alone on its CU
 // takes t1 per k-step (its waves expose their own latency: LDS, dependent
 // VALU, barrier); each further workgroup on the CU slows every step by eta;
-// the grid runs in rounds of per_cu x kCUs slots; a fixed launch, prologue
+// the grid runs in rounds of per_cu x CUs slots; a fixed launch, prologue
 // and epilogue cost; the reduce launch moves split x M x N x 8 bytes
 // (partials written, read, cleared).  The constants were fitted so that the
 // model's choice is fast, not its absolute times: on the four Qwen2-7B GEMMs
@@ -411,10 +428,10 @@ constexpr TileModel kTileModels[] = {
 // 9 %) slower than the best measured configuration.
 double tile_cost(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
     const int64_t wg = tile_tiles((int)M, (int)N, t.variant) * split;
-    const int64_t slots = (int64_t)t.per_cu * kCUs;
+    const int64_t slots = (int64_t)t.per_cu * cus();
     const int64_t steps = 2 * ((K / kGroup + split - 1) / split);
     const int64_t rounds = (wg + slots - 1) / slots;
-    const double c = (double)(wg < slots ? wg : slots) / (double)kCUs;
+    const double c = (double)(wg < slots ? wg : slots) / (double)cus();
     const double share = 1.0 + t.eta * (c - 1.0);
     double time = 7.54 + (double)rounds * (double)steps * t.t1 * (share > 1.0 ? share : 1.0);
     if (split > 1) time += 0.14 + (double)split * (double)M * (double)N * 8.0 / 2.07e6;
@@ -423,7 +440,7 @@ double tile_cost(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t sp
 
 // Where variant 6's grid covers two workgroups per CU (gate||up at M >= 512):
 // variant 6.  Above M = 1024 otherwise: variant 6 when, with split-K up to
-// one pass over its 2 * kCUs slots and at least 4096 rows of K per split, it
+// one pass over its 2 * CUs slots and at least 4096 rows of K per split, it
 // has at least one workgroup per CU; else the k-half pair tile (variant 10)
 // when its tiles fit one pass over the CUs; else variant 4 (256 x 128 tiles)
 // with split-K filling one pass over the CUs, >= 16 k-steps per split.
@@ -445,14 +462,14 @@ int small_m_tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t per = (units + split - 1) / split;
     split = (units + per - 1) / per;
     awq_w4a16_plan q;
-    if (fill_tile(M, N, K, 9, split, &q) != AWQ_OK || q.grid * 2 < kCUs) return AWQ_ERR_PATH;
+    if (fill_tile(M, N, K, 9, split, &q) != AWQ_OK || q.grid * 2 < cus()) return AWQ_ERR_PATH;
     *p = q;
     return AWQ_OK;
 }
 
 // The same model priced for the CU that holds the most workgroups: the grid
-// runs in rounds of per_cu x kCUs workgroup slots, every full round puts
-// per_cu workgroups on each CU, the last one ceil(rest / kCUs) on the
+// runs in rounds of per_cu x CUs workgroup slots, every full round puts
+// per_cu workgroups on each CU, the last one ceil(rest / CUs) on the
 // busiest, and a round costs steps x t1 x (1 + eta (c - 1)) for that CU.
 // tile_cost averages c over the CUs, which fits M <= 1024; above, the
 // busiest CU sets the time: the Qwen2-7B qkv GEMM (3584 x 4608) at M = 2048 /
@@ -462,10 +479,10 @@ int small_m_tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
 // the other three GEMMs (measured best at M = 2048 and 4096).
 double tile_cost_busiest(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
     const int64_t wg = tile_tiles((int)M, (int)N, t.variant) * split;
-    const int64_t slots = (int64_t)t.per_cu * kCUs;
+    const int64_t slots = (int64_t)t.per_cu * cus();
     const int64_t steps = 2 * ((K / kGroup + split - 1) / split);
     const int64_t full = wg / slots, rest = wg % slots;
-    const int64_t c_last = (rest + kCUs - 1) / kCUs;
+    const int64_t c_last = (rest + cus() - 1) / cus();
     double time = 7.54 + (double)full * (double)steps * t.t1 * (1.0 + t.eta * (double)(t.per_cu - 1));
     if (rest > 0) time += (double)steps * t.t1 * (1.0 + t.eta * (double)(c_last - 1));
     if (split > 1) time += 0.14 + (double)split * (double)M * (double)N * 8.0 / 2.07e6;
@@ -480,7 +497,7 @@ const TileModel* tile_model(int variant) {
 
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t tiles6 = tile_tiles((int)M, (int)N, 6);
-    if (M <= 1024 && tiles6 < 2 * kCUs) {
+    if (M <= 1024 && tiles6 < 2 * cus()) {
         const int64_t groups = K / kGroup;
         double best = 0.0;
         int64_t best_v = 0, best_s = 0;
@@ -494,7 +511,7 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
                 awq_w4a16_plan q;
                 if (fill_tile(M, N, K, t.variant, sp, &q) != AWQ_OK) continue;
                 // Splitting beyond 7/4 workgroups per CU never measured faster.
-                if (sp > 1 && q.grid * 4 > 7 * kCUs) continue;
+                if (sp > 1 && q.grid * 4 > 7 * cus()) continue;
                 const double time = tile_cost(t, M, N, K, sp);
                 if (best_v == 0 || time < best) {
                     best = time;
@@ -506,8 +523,8 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
         if (best_v != 0 && fill_tile(M, N, K, best_v, best_s, p) == AWQ_OK) return AWQ_OK;
     }
     int64_t split6 = 1;
-    if (tiles6 > 0 && tiles6 < 2 * kCUs && tiles6 * 4 <= (int64_t)kCounterBytes) {
-        split6 = (2 * kCUs) / tiles6;
+    if (tiles6 > 0 && tiles6 < 2 * cus() && tiles6 * 4 <= (int64_t)kCounterBytes) {
+        split6 = (2 * cus()) / tiles6;
         const int64_t max_split = K / 4096;
         if (split6 > max_split) split6 = max_split;
         if (split6 < 1) split6 = 1;
@@ -533,12 +550,12 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
         }
         if (best_i >= 0 && fill_tile(M, N, K, cand[best_i][0], cand[best_i][1], p) == AWQ_OK) return AWQ_OK;
     }
-    if (tiles6 * split6 >= kCUs && fill_tile(M, N, K, 6, split6, p) == AWQ_OK) return AWQ_OK;
-    if (tiles6 <= kCUs && fill_tile(M, N, K, 10, 1, p) == AWQ_OK) return AWQ_OK;
+    if (tiles6 * split6 >= cus() && fill_tile(M, N, K, 6, split6, p) == AWQ_OK) return AWQ_OK;
+    if (tiles6 <= cus() && fill_tile(M, N, K, 10, 1, p) == AWQ_OK) return AWQ_OK;
     const int64_t tiles = tile_tiles((int)M, (int)N, 4);
     int64_t split = 1;
-    if (tiles < kCUs && tiles * 4 <= (int64_t)kCounterBytes) {
-        split = kCUs / tiles;
+    if (tiles < cus() && tiles * 4 <= (int64_t)kCounterBytes) {
+        split = cus() / tiles;
         const int64_t max_split = (K / 64) / 16;
         if (split > max_split) split = max_split;
         if (split < 1) split = 1;
@@ -661,7 +678,6 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
 // once per device.  Every
 // call on a device shares its scratch, so calls that overlap on one GPU race.
 constexpr size_t kScratchBytes = (size_t)AWQ_NOALLOC_SCRATCH_BYTES;
-constexpr int kMaxDevices = 64;
 
 __global__ void awq_zero_fill_kernel(u32x4* p, size_t n16) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;

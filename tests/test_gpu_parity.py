@@ -196,6 +196,17 @@ def test_auto_vocab_wide(gpu, m):
         _assert_close(y[:, c0:c0 + 512], x.astype(np.float64) @ w, f"vocab-wide M={m} columns {c0}..")
 
 
+def test_decode_plans_sized_by_the_device(gpu):
+    """The planner sizes its grids by the current device's compute units (read
+    once per device): the decode plans of the Qwen2-7B shapes put at most one
+    workgroup on each CU and keep more than half of them busy."""
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    print(f"device compute units: {cus}", flush=True)
+    for m, k, n in [(1, 3584, 4608), (1, 3584, 37888), (4, 3584, 4608), (4, 18944, 3584), (16, 18944, 3584)]:
+        p = _native.plan_for(m, n, k)
+        assert cus // 2 < p.grid <= cus, (m, k, n, p.grid, cus)
+
+
 @pytest.mark.parametrize("m", [1, 8, 64, 512, 2048])
 def test_gemm_down_m_sweep(gpu, m):
     k, n = _SHAPES["down_proj"]
