@@ -15,10 +15,12 @@
  *                              accumulated in fp32, rounded once to fp16
  *
  * All pointers are device pointers.  `stream` is a hipStream_t (NULL = the
- * legacy default stream).  No entry point allocates device memory,
- * synchronises the host or keeps mutable global state, so every call is
- * reentrant and can be captured into a HIP graph.  Every entry point returns
- * AWQ_OK (0) or a negative awq_w4a16_status.
+ * legacy default stream).  No entry point allocates device memory or
+ * synchronises the host, and the only global state is looked up once per
+ * device and then read (the device's compute-unit count; the address of the
+ * allocation-free entry point's static scratch), so every call is reentrant
+ * and can be captured into a HIP graph.  Every entry point returns AWQ_OK (0)
+ * or a negative awq_w4a16_status.
  *
  * A GEMM call is one kernel launch, or two on the same stream when its plan
  * adds split-K partials in a second launch of a reduce kernel: tile
@@ -128,10 +130,15 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
  * summed by a second, whole-device launch; variants 10, 11, 12: 128-, 128-
  * and 64-row tiles with two wavefronts per SIMD from one workgroup, each
  * taking one k-half of every k-step (10: last-arriver split-K finish, 11 and
- * 12: the second launch).  Every variant takes split_k >= 1 workgroups
- * along K (variants 6 and up in whole 128-row groups); the plan's
- * rows_per_wave holds the K rows per split.  Other variant numbers:
- * AWQ_ERR_PATH. */
+ * 12: the second launch); variants 13, 14: hybrids of variants 6 and 8 for
+ * grids that do not divide the CUs -- `full` whole tiles on every CU (fewer
+ * than a CU holds: one for 13, one or two for 14) and the L leftover tiles
+ * split split_k >= 2 ways along K, at most one piece per CU (grid = full x
+ * CUs + L x split_k), the pieces' partials compact ([split_k, L, rows, 256]
+ * fp32) and added by each leftover tile's last-arriving piece; other shapes
+ * get AWQ_ERR_PATH.  Every variant takes split_k >= 1 workgroups along K
+ * (variants 6 and up in whole 128-row groups); the plan's rows_per_wave
+ * holds the K rows per split.  Other variant numbers: AWQ_ERR_PATH. */
 int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 

@@ -396,6 +396,18 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->rows_per_wave = (int32_t)(per * unit);  // K rows per split
     p->grid = tiles * split_k;
     p->workspace_bytes = split_k > 1 ? partials_workspace(split_k, M, N) : 0u;
+    if (tile_hybrid((int)variant)) {
+        // Whole tiles: `full` per CU on every CU (fewer than the workgroups a
+        // CU holds: 2 for 128 rows, 3 for 64); the L leftover tiles split
+        // split_k ways, at most one piece per CU; compact partials.
+        const int64_t C = cus();
+        const int64_t per_cu = variant == 13 ? 2 : 3;
+        const int64_t full = tiles / C;
+        const int64_t L = tiles - full * C;
+        if (split_k < 2 || full < 1 || full > per_cu - 1 || L < 1 || L * split_k > C) return AWQ_ERR_PATH;
+        p->grid = full * C + L * split_k;
+        p->workspace_bytes = kPartialsOffset + (uint64_t)split_k * (uint64_t)L * (uint64_t)p->tile_m * 256u * 4u;
+    }
     if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
     return AWQ_OK;
 }
@@ -489,6 +501,25 @@ double tile_cost_busiest(const TileModel& t, int64_t M, int64_t N, int64_t K, in
     return time;
 }
 
+// Busiest-CU time of a hybrid plan (variants 13, 14 with the constants of
+// variants 6, 8): `full` whole tiles on every CU, and on L x split CUs one
+// piece of a leftover tile (ceil(groups / split) groups) beside them, whose
+// partials (split x L x rows x 256 x 4 bytes) are added by the pieces' last
+// arrivers while the whole tiles still run -- priced at 2.6 TB/s, which puts
+// the best split of the Qwen2-7B qkv GEMM at M = 2048 where it measured
+// (three: 86.0 us, against 89.5 and 88.3 for two and four).
+double tile_cost_hybrid(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
+    const int64_t tiles = tile_tiles((int)M, (int)N, t.variant);
+    const int64_t full = tiles / cus();
+    const int64_t left = tiles - full * cus();
+    const int64_t groups = K / kGroup;
+    const int64_t steps = 2 * groups;
+    const int64_t sk_steps = 2 * ((groups + split - 1) / split);
+    return 7.54 + (double)sk_steps * t.t1 * (1.0 + t.eta * (double)full) +
+           (double)(steps - sk_steps) * t.t1 * (1.0 + t.eta * (double)(full - 1)) +
+           (double)split * (double)left * (double)t.rows * 256.0 * 4.0 / 2.6e6;
+}
+
 const TileModel* tile_model(int variant) {
     for (const TileModel& t : kTileModels)
         if (t.variant == variant) return &t;
@@ -547,6 +578,32 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
                 best = time;
                 best_i = i;
             }
+        }
+        // An unsplit choice leaves CUs idle or some CUs a whole tile more
+        // than others; where a hybrid plan exists, the hybrid of least
+        // predicted time instead.  Measured against the unsplit plans on the
+        // Qwen2-7B GEMMs at M = 1025 - 3072: 3 - 16 % faster on every shape
+        // where it applies (qkv M = 2048: 88.5 against 98.3 us; o M = 2560:
+        // 87.1 against 97.1; down M = 2560: 396 against 471).  Against
+        // variant 6 split along a deep K (down at M = 1280, 1536) it lost
+        // 22 - 24 %, hence unsplit choices only.
+        if (best_i >= 0 && cand[best_i][1] == 1) {
+            double hbest = 0.0;
+            int64_t hv = 0, hs = 0;
+            for (int64_t v = 13; v <= 14; ++v) {
+                const TileModel* t = tile_model(v == 13 ? 6 : 8);
+                for (int64_t sp = 2; sp <= 8; ++sp) {
+                    awq_w4a16_plan q;
+                    if (t == nullptr || fill_tile(M, N, K, v, sp, &q) != AWQ_OK) continue;
+                    const double time = tile_cost_hybrid(*t, M, N, K, sp);
+                    if (hv == 0 || time < hbest) {
+                        hbest = time;
+                        hv = v;
+                        hs = sp;
+                    }
+                }
+            }
+            if (hv != 0 && fill_tile(M, N, K, hv, hs, p) == AWQ_OK) return AWQ_OK;
         }
         if (best_i >= 0 && fill_tile(M, N, K, cand[best_i][0], cand[best_i][1], p) == AWQ_OK) return AWQ_OK;
     }
@@ -657,6 +714,7 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         cfg.tile_n = p.tile_n;
         cfg.split_k = p.split_k;
         cfg.k_per_split = p.rows_per_wave;
+        cfg.grid = p.grid;
         a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kPartialsOffset)
                                    : nullptr;
         e = launch_tile(a, cfg, static_cast<uint32_t*>(workspace), s);
@@ -705,6 +763,12 @@ int noalloc_plan(int64_t M, int64_t N, int64_t K, int32_t group_size, awq_w4a16_
             *p = q;
             return AWQ_OK;
         }
+    }
+    // A hybrid needs two splits at least; its unsplit tile needs no workspace.
+    awq_w4a16_plan q;
+    if (tile_hybrid(p->variant) && fill_tile(M, N, K, p->variant == 13 ? 6 : 8, 1, &q) == AWQ_OK) {
+        *p = q;
+        return AWQ_OK;
     }
     return AWQ_ERR_SCRATCH;
 }

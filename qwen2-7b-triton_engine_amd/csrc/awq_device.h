@@ -375,21 +375,32 @@ __device__ __forceinline__ void finish_batch(unsigned long long* fix, half_t* ou
 // The partials are left as they are: the next split-K call writes every
 // partial it reads, and the fixed-point slots live in a region of their own.
 // `fin` holds blockDim.x float4.  Must be called by the whole workgroup.
+// Where the partial of split q for output (row0 + r, col0 + c) lives: byte
+// base + r * row_stride + 4 c + q * split_stride of the partials buffer.
+struct PartLayout {
+    uint32_t base, row_stride, split_stride;
+};
+// The [split, M, N] layout.
+__device__ __forceinline__ PartLayout full_parts(int M, int N, int row0, int col0) {
+    return PartLayout{(uint32_t)(((size_t)row0 * N + col0) * 4), (uint32_t)N * 4u, (uint32_t)((size_t)M * N * 4)};
+}
+
 template <int U>
 __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t* __restrict__ out,
                                               const half_t* bias, const half_t* residual, int M, int N,
                                               int row0, int nrows, int col0, int ncols, int split_k,
-                                              floatx4* fin) {
+                                              floatx4* fin, PartLayout pl) {
     const int quads = ncols / 4;
     const int items = nrows * quads;
     const int nt = blockDim.x;
     const int t = threadIdx.x;
-    const uint32_t stride = (uint32_t)((size_t)M * N * 4);
+    const uint32_t stride = pl.split_stride;
     auto item_off = [&](int item, int& m, int& n) {
         const int r = item / quads;
+        const int c = 4 * (item - r * quads);
         m = row0 + r;
-        n = col0 + 4 * (item - r * quads);
-        return (uint32_t)(((size_t)m * N + n) * 4);
+        n = col0 + c;
+        return pl.base + (uint32_t)r * pl.row_stride + (uint32_t)c * 4u;
     };
     auto store = [&](int m, int n, floatx4 s) {
         const float y[4] = {s[0], s[1], s[2], s[3]};
@@ -436,6 +447,16 @@ __device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t*
         for (int u = 0; u < U; ++u)
             if (base + u * nt + t < items) store(mm[u], nn[u], s[u]);
     }
+}
+
+// splitk_finish over the [split, M, N] partials layout.
+template <int U>
+__device__ __forceinline__ void splitk_finish(__amdgpu_buffer_rsrc_t rp, half_t* __restrict__ out,
+                                              const half_t* bias, const half_t* residual, int M, int N,
+                                              int row0, int nrows, int col0, int ncols, int split_k,
+                                              floatx4* fin) {
+    splitk_finish<U>(rp, out, bias, residual, M, N, row0, nrows, col0, ncols, split_k, fin,
+                     full_parts(M, N, row0, col0));
 }
 
 }  // namespace awq

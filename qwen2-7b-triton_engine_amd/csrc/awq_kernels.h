@@ -44,17 +44,23 @@ struct GemvConfig {
 // Tile variants 6 .. kTileVariants: weights dequantised into MFMA registers,
 // every load a direct global->LDS load into a ring (x rows per tile, stages).
 // Variant 4: 256 x 128 tiles, weights dequantised once per k-step into LDS.
-constexpr int kTileVariants = 12;
-constexpr int tile5_rows(int variant) { return (variant == 8 || variant == 12) ? 64 : variant == 9 ? 32 : 128; }
-constexpr int tile5_threads(int variant) { return variant >= 10 ? 512 : 256; }
+// Variants 13, 14: the hybrid of variants 6 (128 rows) and 8 (64 rows) --
+// whole tiles on every CU, the leftover tiles split along K.
+constexpr int kTileVariants = 14;
+constexpr int tile5_rows(int variant) {
+    return (variant == 8 || variant == 12 || variant == 14) ? 64 : variant == 9 ? 32 : 128;
+}
+constexpr int tile5_threads(int variant) { return (variant >= 10 && variant <= 12) ? 512 : 256; }
+constexpr bool tile_hybrid(int variant) { return variant == 13 || variant == 14; }
 // Whether a tile variant number names a kernel.
 constexpr bool tile_variant_served(int variant) { return variant == 4 || (variant >= 6 && variant <= kTileVariants); }
 
 struct TileConfig {
     int variant;             // 4: 256x128x64, LDS W^T; 6 .. kTileVariants: register dequant, N tile 256
     int tile_m, tile_n;
-    int split_k;             // workgroups along K per tile
+    int split_k;             // workgroups along K per tile (hybrid: per leftover tile)
     int k_per_split;         // K rows per split (multiple of 64; variants 6 and up: of 128)
+    int64_t grid;            // workgroups (the hybrid's: whole tiles + leftover tiles x split_k)
 };
 
 // out[M, N] = x[M, K] @ w[N, K]^T, fp16 weights (the output projection);

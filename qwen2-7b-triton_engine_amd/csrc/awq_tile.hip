@@ -359,7 +359,16 @@ struct T5Layout {
 // partials; 1 -- partials with plain stores, summed by a second launch of
 // awq_splitk_reduce_kernel over the whole device (for small tiles, whose
 // last arrivers would each read split x tile bytes alone).
-template <int FM, int KW, int FIN>
+// HY (hybrid, FIN 0): workgroups 0 .. D-1 each take one whole tile, the last
+// L tiles of the order are split split_k ways along K, one piece per
+// remaining workgroup (grid = D + L split_k, so L = (grid - tiles) /
+// (split_k - 1)).  With D a whole number of workgroups per CU and L split_k at
+// most one more per CU, every CU holds its whole tiles plus at most one short
+// piece, instead of some CUs holding a whole tile more than the others; the
+// pieces finish early, so their last arrivers add the partials while the
+// whole tiles still run.  The pieces' partials are compact: [split_k][L][BM
+// rows][256 columns] fp32.
+template <int FM, int KW, int FIN, bool HY = false>
 __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile_kernel_v5(
     GemmArgs a, int split_k, int k_per_split, uint32_t* counters) {
     using L = T5Layout<FM, KW>;
@@ -384,14 +393,32 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
     // ---- work item: XCD-aware grouped tile order (as variant 4) ----
     const int m_tiles = (a.M + BM - 1) / BM;
     const int n_tiles = (a.N + T5_BN - 1) / T5_BN;
-    const int total = (int)gridDim.x;
-    const int xcd = blockIdx.x & 7;
-    const int xi = blockIdx.x >> 3;
-    const int per = (total + 7) >> 3;
-    const int rem = total & 7;
-    const int w = (rem == 0 || xcd < rem) ? xcd * per + xi : rem * per + (xcd - rem) * (per - 1) + xi;
-    const int tile = w / split_k;
-    const int split = w - tile * split_k;
+    // Position of workgroup b among `total` consecutive ones in XCD order:
+    // the workgroups one XCD runs (b % 8 == x) get consecutive positions.
+    auto xcd_order = [](int b, int total) {
+        const int xcd = b & 7, xi = b >> 3, per = (total + 7) >> 3, rem = total & 7;
+        return (rem == 0 || xcd < rem) ? xcd * per + xi : rem * per + (xcd - rem) * (per - 1) + xi;
+    };
+    int tile, split, ks = split_k, sk_tile = 0, n_sk = 0;  // ks: splits of this workgroup's tile
+    if constexpr (HY) {
+        const int T = m_tiles * n_tiles;
+        n_sk = ((int)gridDim.x - T) / (split_k - 1);
+        const int D = T - n_sk;
+        if ((int)blockIdx.x < D) {
+            tile = xcd_order((int)blockIdx.x, D);
+            split = 0;
+            ks = 1;
+        } else {
+            const int w = xcd_order((int)blockIdx.x - D, (int)gridDim.x - D);
+            sk_tile = w / split_k;
+            tile = D + sk_tile;
+            split = w - sk_tile * split_k;
+        }
+    } else {
+        const int w = xcd_order((int)blockIdx.x, (int)gridDim.x);
+        tile = w / split_k;
+        split = w - tile * split_k;
+    }
     const int in_group = T5_GM * n_tiles;
     const int first_m = (tile / in_group) * T5_GM;
     const int gm = min(m_tiles - first_m, T5_GM);
@@ -400,8 +427,8 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
     const int m0 = tm * BM;
     const int n0 = tn * T5_BN;
     const int pn = a.N >> 3;
-    const int k_begin = split * k_per_split;
-    const int k_end = min(a.K, k_begin + k_per_split);
+    const int k_begin = ks == 1 ? 0 : split * k_per_split;
+    const int k_end = ks == 1 ? a.K : min(a.K, k_begin + k_per_split);
     const int KT = (k_end - k_begin) / T5_BK;  // even: whole groups
 
     const u32x4 rx = raw_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
@@ -569,7 +596,7 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
     // acc[c][f] lane value r: out[m0 + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
     const int pc0 = (n0 >> 3) + 8 * wn + 4 * (kb & 1);
     const int coff = 4 * (kb >> 1);
-    if (split_k == 1) {
+    if (ks == 1) {
         if (kh != 0) return;  // KW = 2: the sums are in waves 0..3
 #pragma unroll
         for (int f = 0; f < FM; ++f) {
@@ -585,7 +612,13 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         return;
     }
 
-    const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
+    // Partials of this workgroup's split: [split_k, M, N], or for the hybrid's
+    // pieces [split_k][n_sk][BM][256] (PartLayout: byte base + r row_stride +
+    // 4 c + split split_stride for output (m0 + r, n0 + c)).
+    const PartLayout pl = HY ? PartLayout{(uint32_t)sk_tile * (uint32_t)(BM * T5_BN * 4), (uint32_t)(T5_BN * 4),
+                                          (uint32_t)n_sk * (uint32_t)(BM * T5_BN * 4)}
+                             : full_parts(a.M, a.N, m0, n0);
+    const uint32_t part_bytes = HY ? (uint32_t)split_k * pl.split_stride : (uint32_t)((size_t)split_k * a.M * a.N * 4);
     const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
@@ -594,7 +627,8 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if (pc0 + r >= pn) continue;
-            const uint32_t off = (uint32_t)((((size_t)split * a.M + m) * a.N + 8 * (pc0 + r) + coff) * 4);
+            const uint32_t off = pl.base + (uint32_t)(16 * f + n16) * pl.row_stride +
+                                 (uint32_t)(8 * (pc0 + r) + coff - n0) * 4u + (uint32_t)split * pl.split_stride;
             buf_store_f4_device(floatx4{acc[0][f][r], acc[1][f][r], acc[2][f][r], acc[3][f][r]}, rp_, off);
         }
     }
@@ -606,7 +640,8 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<16>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin);
+    splitk_finish<16>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin,
+                      pl);
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -627,7 +662,7 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
         return hipGetLastError();
     }
     if (cfg.variant >= 6 && cfg.variant <= kTileVariants) {
-        const int64_t blocks = tile_tiles(a.M, a.N, cfg.variant) * cfg.split_k;
+        const int64_t blocks = tile_hybrid(cfg.variant) ? cfg.grid : tile_tiles(a.M, a.N, cfg.variant) * cfg.split_k;
         if (blocks == 0) return hipSuccess;
         const dim3 grid((unsigned)blocks);
         bool reduce = false;
@@ -639,6 +674,8 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
             case 10: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 2, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
             case 11: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
             case 12: hipLaunchKernelGGL((awq_tile_kernel_v5<4, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 13: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 1, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 14: hipLaunchKernelGGL((awq_tile_kernel_v5<4, 1, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
             default: return hipErrorInvalidValue;
         }
         const hipError_t e = hipGetLastError();

@@ -119,7 +119,7 @@ def _outlier_x(m, k, seed):
 
 _ROUTES = ([(name, m) for name in ("qkv_proj", "o_proj", "gate_up_proj", "down_proj") for m in (1, 2, 3, 4, 8, 16)] +
            [("down_proj", 64), ("qkv_proj", 64), ("o_proj", 512), ("down_proj", 512), ("gate_up_proj", 2048),
-            ("qkv_proj", 2048), ("o_proj", 1025)])
+            ("qkv_proj", 2048), ("o_proj", 1025), ("o_proj", 2560), ("down_proj", 3072)])
 
 
 @pytest.mark.parametrize("name,m", _ROUTES)

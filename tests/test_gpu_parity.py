@@ -296,6 +296,35 @@ def test_tile_plans_agree(gpu, m, k, n):
         _assert_close(y, y_ref, f"tile M={m} v={variant} split={sk}")
 
 
+@pytest.mark.parametrize("m,k,n", [(2048, 3584, 4608), (2100, 1024, 4104), (2600, 1280, 3584)])
+def test_tile_hybrid_plans(gpu, m, k, n):
+    """The hybrid tiles (variants 13, 14: a whole tile per CU slot, the leftover
+    tiles split along K with compact partials and a last-arriver finish), on
+    every output against the oracle, with ragged M and N, and bit-exact with
+    one-hot rows of x (each output is one weight: every tile and K piece must
+    land in its own place)."""
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=16)
+    w = O.dequant_awq(qw, qz, s)
+    y_ref = x.astype(np.float32) @ w.astype(np.float32)
+    rows = np.random.default_rng(17).integers(0, k, size=m)
+    x1 = np.zeros((m, k), dtype=np.float16)
+    x1[np.arange(m), rows] = 1.0
+    want = (w[rows] + np.float16(0)).view(np.uint16)
+    tried = 0
+    for variant in (13, 14):
+        for sk in (2, 3, 4, 5, 7):
+            try:
+                p = _native.plan_tile(m, n, k, variant, sk)
+            except _native.AwqNativeError:
+                continue
+            print(f"hybrid tile M={m} K={k} N={n} variant={variant} split_k={sk} grid={p.grid}", flush=True)
+            _assert_close(_run(gpu, x, qw, qz, s, plan_obj=p), y_ref, f"hybrid M={m} v={variant} split={sk}")
+            y1 = _run(gpu, x1, qw, qz, s, plan_obj=p)
+            assert np.array_equal((y1 + np.float16(0)).view(np.uint16), want), f"one-hot hybrid v={variant} split={sk}"
+            tried += 1
+    assert tried >= 4
+
+
 @pytest.mark.parametrize("m", [1, 2])
 def test_gemv_quad_plans_agree(gpu, m):
     """Column-quad GEMV (balanced K split, fixed-point split-K finish): split

@@ -110,6 +110,14 @@ def test_auto_plan_invariants(L, m, k, n):
             # one 64-bit fixed-point slot per output element
             assert p.workspace_bytes == _native.counter_bytes() + m * n * 8
             assert p.split_k <= 255
+        elif p.path == _native.PATH_TILE and p.variant in (13, 14):
+            # hybrid: compact partials of the leftover tiles only
+            tm = 128 if p.variant == 13 else 64
+            tiles = -(-m // tm) * -(-n // 256)
+            left = tiles % 256
+            assert p.grid == tiles - left + left * p.split_k
+            assert p.workspace_bytes == (_native.counter_bytes() + _native.SLOT_BYTES +
+                                         p.split_k * left * tm * 256 * 4)
         else:
             assert p.workspace_bytes == _native.counter_bytes() + _native.SLOT_BYTES + p.split_k * m * n * 4
     else:
@@ -150,25 +158,37 @@ def test_auto_stream_split_keeps_a_group_and_a_half_per_split(L):
 @pytest.mark.parametrize("k,n", SHAPES)
 def test_tile_plans_cover_k_exactly(L, k, n):
     """Every split-K plan gives each split a whole number of 64-row k-steps
-    (variants 6..12: of 128-row groups) and covers K exactly; the tile count fits
-    the arrival-counter block.  Variant numbers without a kernel are refused."""
-    for variant in range(1, 14):
-        for split in (1, 2, 3, 4, 5, 8):
-            try:
-                p = _native.plan_tile(512, n, k, variant, split)
-            except _native.AwqNativeError as e:
-                assert e.status == _native.AWQ_ERR_PATH
-                continue
-            assert variant == 4 or 6 <= variant <= 12
-            per = p.rows_per_wave
-            assert per % (128 if variant >= 6 else 64) == 0
-            assert (split - 1) * per < k <= split * per
-            tm = {4: 256, 6: 128, 7: 128, 8: 64, 9: 32, 12: 64}.get(variant, 128)
-            tn = 256 if variant >= 6 else 128
-            tiles = -(-512 // tm) * -(-n // tn)
-            assert p.grid == tiles * split
-            if split > 1:
-                assert tiles * 4 <= _native.counter_bytes()
+    (variants 6..14: of 128-row groups) and covers K exactly; the tile count fits
+    the arrival-counter block.  The hybrids (13, 14) put `full` whole tiles on
+    each of the 256 CUs (fewer than a CU holds) and split the leftover tiles,
+    at most one piece per CU, with compact partials.  Variant numbers without a
+    kernel are refused."""
+    for m in (512, 2048):
+        for variant in range(1, 16):
+            for split in (1, 2, 3, 4, 5, 8):
+                try:
+                    p = _native.plan_tile(m, n, k, variant, split)
+                except _native.AwqNativeError as e:
+                    # no such kernel or split, or partials beyond 2^31 bytes (M = 2048, 8 splits)
+                    assert e.status in (_native.AWQ_ERR_PATH, _native.AWQ_ERR_TOO_LARGE)
+                    continue
+                assert variant == 4 or 6 <= variant <= 14
+                per = p.rows_per_wave
+                assert per % (128 if variant >= 6 else 64) == 0
+                assert (split - 1) * per < k <= split * per
+                tm = {4: 256, 6: 128, 7: 128, 8: 64, 9: 32, 12: 64, 14: 64}.get(variant, 128)
+                tn = 256 if variant >= 6 else 128
+                tiles = -(-m // tm) * -(-n // tn)
+                if variant in (13, 14):
+                    full, left = tiles // 256, tiles % 256
+                    assert split >= 2 and 1 <= full <= (1 if variant == 13 else 2) and 1 <= left and left * split <= 256
+                    assert p.grid == full * 256 + left * split
+                    assert p.workspace_bytes == (_native.counter_bytes() + _native.SLOT_BYTES +
+                                                 split * left * tm * 256 * 4)
+                else:
+                    assert p.grid == tiles * split
+                if split > 1:
+                    assert tiles * 4 <= _native.counter_bytes()
 
 
 def test_skinny_and_gemv_plan_rejections():
