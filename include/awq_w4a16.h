@@ -35,7 +35,9 @@
  * The fixed-point split-K finish (GEMV variants 4 and 5, stream variant 1)
  * clamps each workgroup's partial sum to +-2^22 and turns a NaN partial
  * into +2^22, so a NaN or an infinity in x gives +-inf (never NaN) on those
- * paths; partials are added in 2^-24 steps.
+ * paths -- except that a +inf and a -inf partial of different splits cancel,
+ * so such an output can come out finite where the reference gives NaN;
+ * partials are added in 2^-24 steps.
  */
 #ifndef AWQ_W4A16_H
 #define AWQ_W4A16_H

@@ -35,7 +35,7 @@ def _plans(m, n, k):
     if m > 16:
         makers += [(f"tile v{v} s{sp}", lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp))
                    for v, sp in ((4, 1), (4, 2), (6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (10, 1), (11, 2),
-                                 (12, 2))]
+                                 (12, 2), (13, 2), (14, 3))]
     out = []
     for label, make in makers:
         try:
@@ -46,7 +46,7 @@ def _plans(m, n, k):
     return out
 
 
-@pytest.mark.parametrize("m", [1, 2, 4, 16, 100, 300])
+@pytest.mark.parametrize("m", [1, 2, 4, 16, 100, 300, 2048])
 def test_bias_residual_epilogue_bit_exact(gpu, m):
     k, n = 3584, 4608
     x, qw, qz, s = O.make_inputs(m, k, n, seed=40 + m)
