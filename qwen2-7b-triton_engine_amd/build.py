@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import glob
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -27,17 +28,39 @@ COMMON_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall",
                 "-Wno-unused-command-line-argument", "-munsafe-fp-atomics"]
 
 
+# Per-kernel resource remarks (registers, LDS, scratch), read below: no kernel
+# may spill registers to scratch memory.
+RESOURCE_FLAGS = ["-Rpass-analysis=kernel-resource-usage"]
+
+
+def _spills(remarks: str) -> list:
+    """(kernel, bytes per lane) of every kernel whose remarks report scratch."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            out.append((name, int(m.group(1))))
+    return out
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, *RESOURCE_FLAGS, "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the device feature above and says so; drop that line.
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    lines = [l for l in r.stderr.splitlines() if noise not in l]
+    err = "\n".join(l for l in lines if "remark:" not in l)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{err}")
+    spills = _spills("\n".join(lines))
+    if spills:
+        raise RuntimeError(f"{src}: kernels spill registers to scratch: {spills}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
     return obj

@@ -548,7 +548,11 @@ static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, u
         case 14: return gemv_quad_launch<1, MM, 4>(a, cfg, counters, stream);
         case 22: return gemv_quad_launch<2, MM, 2>(a, cfg, counters, stream);
         case 23: return gemv_quad_launch<2, MM, 3>(a, cfg, counters, stream);
-        case 24: return gemv_quad_launch<2, MM, 4>(a, cfg, counters, stream);
+        case 24:
+            // The dot2 form with two x rows and four chunk buffers would spill
+            // registers; plans refuse it, so it is not built.
+            if constexpr (MM) return gemv_quad_launch<2, MM, 4>(a, cfg, counters, stream);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }

@@ -640,8 +640,11 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
                     (uint32_t)(split_k - 1);
     __syncthreads();
     if (!last_flag) return;
-    splitk_finish<16>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(BM, a.M - m0), n0, min(T5_BN, a.N - n0), split_k, fin,
-                      pl);
+    // Quads per thread in flight while summing: 16 fit the 128-row tile's
+    // registers; the 64-row tile (three workgroups per CU, 168 VGPRs) takes
+    // 8 so that nothing spills.
+    splitk_finish<(FM >= 8 ? 16 : 8)>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(BM, a.M - m0), n0,
+                                      min(T5_BN, a.N - n0), split_k, fin, pl);
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -191,6 +191,23 @@ def test_tile_plans_cover_k_exactly(L, k, n):
                     assert tiles * 4 <= _native.counter_bytes()
 
 
+def test_build_rejects_register_spills():
+    """build.py reads hipcc's per-kernel resource remarks and refuses kernels
+    that spill registers to scratch memory."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_awq_build_check",
+                                                  os.path.join(ROOT, "qwen2-7b-triton_engine_amd", "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    remarks = ("a.hip:1:1: remark: Function Name: _Z4goodv [-Rpass-analysis=kernel-resource-usage]\n"
+               "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]\n"
+               "a.hip:9:1: remark: Function Name: _Z5spillv [-Rpass-analysis=kernel-resource-usage]\n"
+               "a.hip:9:1: remark:     ScratchSize [bytes/lane]: 88 [-Rpass-analysis=kernel-resource-usage]\n")
+    assert mod._spills(remarks) == [("_Z5spillv", 88)]
+    assert "-Rpass-analysis=kernel-resource-usage" in mod.RESOURCE_FLAGS
+
+
 def test_skinny_and_gemv_plan_rejections():
     with pytest.raises(_native.AwqNativeError) as e:
         _native.plan_gemv(3, 512, 3584, 0, 4)           # GEMV serves M <= 2
