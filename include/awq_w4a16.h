@@ -290,7 +290,8 @@ int awq_w4a16_gemm_epilogue(const void* x, const int32_t* qweight, const int32_t
  * I % 8 == 0. */
 int awq_silu_mul(const void* gate_up, void* out, int64_t M, int64_t I, void* stream);
 
-/* out[M,N] = x[M,K] @ weight[N,K]^T in fp16 with fp32 accumulation: the
+/* out[M,N] = x[M,K] @ weight[N,K]^T in fp16 with fp32 accumulation (one
+ * v_mfma_f32_16x16x32_f16 per 16 weight rows x 32 k): the
  * fp16 output projection (lm_head) of model/qwen2.py:253,280
  * (nn.Linear(hidden_size, vocab_size, bias=False), applied at :280), at
  * decode sizes.  weight is nn.Linear's row-major [out_features, in_features]

@@ -1010,7 +1010,7 @@ int awq_fp16_linear(const void* x, const void* weight, void* out, int64_t M, int
     if (!x || !weight || !out) return AWQ_ERR_NULL_POINTER;
     if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, 2)) return AWQ_ERR_MISALIGNED;
     const hipError_t e = launch_fp16_gemv(static_cast<const half_t*>(x), static_cast<const half_t*>(weight),
-                                          static_cast<half_t*>(out), (int)M, (int)N, (int)K,
+                                          static_cast<half_t*>(out), (int)M, (int)N, (int)K, (int)cus(),
                                           static_cast<hipStream_t>(stream));
     return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
 }

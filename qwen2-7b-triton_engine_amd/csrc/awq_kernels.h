@@ -63,11 +63,13 @@ struct TileConfig {
     int64_t grid;            // workgroups (the hybrid's: whole tiles + leftover tiles x split_k)
 };
 
-// out[M, N] = x[M, K] @ w[N, K]^T, fp16 weights (the output projection);
-// M <= 8, K % 8 == 0, K <= fp16_gemv_max_k(), M * K * 2 <= 64 KiB.
-hipError_t launch_fp16_gemv(const half_t* x, const half_t* w, half_t* out, int M, int N, int K, hipStream_t stream);
+// out[M, N] = x[M, K] @ w[N, K]^T, fp16 weights (the output projection), one
+// MFMA per 16 weight rows x 32 k; M <= 8, K % 8 == 0, K <= fp16_gemv_max_k()
+// (x staged in LDS: at most 8 x 4104 x 2 bytes); grids sized for `cus`
+// compute units.
+hipError_t launch_fp16_gemv(const half_t* x, const half_t* w, half_t* out, int M, int N, int K, int cus,
+                            hipStream_t stream);
 int fp16_gemv_max_k();
-int fp16_gemv_blocks(int N);
 
 // out[m, i] = fp16(silu(gate_up[m, i]) * gate_up[m, I + i]); I % 8 == 0.
 hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int M, int I, hipStream_t stream);
