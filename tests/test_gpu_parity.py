@@ -487,8 +487,12 @@ def test_errors_raise(gpu):
 
 
 def test_graph_capture_replay(gpu):
-    """Captured into a graph (split-K workspace included), every replay matches eager."""
-    shapes = [(1, 3584, 512), (4, 3584, 3584), (200, 1024, 1024)]
+    """Captured into a graph (split-K workspace included), every replay matches
+    eager bit for bit: the GEMV, the stream kernels (M = 2, 4), the 32-row
+    tile with its reduce launch (M = 16), a small-M tile and the hybrid tile
+    (M = 2048)."""
+    shapes = [(1, 3584, 512), (2, 3584, 4608), (4, 3584, 3584), (16, 3584, 4608), (200, 1024, 1024),
+              (2048, 3584, 4608)]
     inputs = []
     for m, k, n in shapes:
         x, qw, qz, s = O.make_inputs(m, k, n, seed=m)
