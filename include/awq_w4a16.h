@@ -32,7 +32,7 @@
  * scale); the GEMV, stream and factored skinny paths multiply the fp32 sum
  * of x * (q - z) over a 128-row group by the scale instead (no per-weight
  * rounding: they stay finite where a reference weight would overflow).
- * The fixed-point split-K finish (GEMV variants 4 and 5, stream variant 1)
+ * The fixed-point split-K finish (GEMV variant 5, stream variant 1)
  * clamps each workgroup's partial sum to +-2^22 and turns a NaN partial
  * into +2^22, so a NaN or an infinity in x gives +-inf (never NaN) on those
  * paths -- except that a +inf and a -inf partial of different splits cancel,
@@ -120,10 +120,7 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
                           int32_t rows_per_wave, int32_t k_waves, int32_t variant,
                           int32_t factored_scale, awq_w4a16_plan* plan);
 
-/* Host-only: a tile-path plan.  Variant 4: 256x128x64 tiles, x streamed
- * into a 3-stage LDS ring by direct loads, weights dequantised once per
- * k-step into an LDS W^T buffer, the next k-step's dequant interleaved with
- * this k-step's MFMAs.  Variant 6: 128x256x64 tiles (four wavefronts, two
+/* Host-only: a tile-path plan.  Variant 6: 128x256x64 tiles (four wavefronts, two
  * workgroups per CU), each wavefront 128 x rows x 64 columns, weights
  * dequantised straight into MFMA operand registers, x, raw weights and
  * zeros/scales brought by direct global->LDS loads two k-steps ahead into a
@@ -138,15 +135,15 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
  * split split_k >= 2 ways along K, at most one piece per CU (grid = full x
  * CUs + L x split_k), the pieces' partials compact ([split_k, L, rows, 256]
  * fp32) and added by each leftover tile's last-arriving piece; other shapes
- * get AWQ_ERR_PATH.  Every variant takes split_k >= 1 workgroups along K
- * (variants 6 and up in whole 128-row groups); the plan's rows_per_wave
- * holds the K rows per split.  Other variant numbers: AWQ_ERR_PATH. */
+ * get AWQ_ERR_PATH.  Every variant takes split_k >= 1 workgroups along K in
+ * whole 128-row groups; the plan's rows_per_wave holds the K rows per split.
+ * Other variant numbers (1 .. 5 included): AWQ_ERR_PATH. */
 int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 
 /* Host-only: a GEMV-path plan (M <= 2) with explicit tuning values.
- * variant 4 (column quads, N % 32 == 0; variant 5: the same with the column
- * sums on v_mfma_f32_16x16x32_f16): tile_n 512; rows_per_wave 0; depth 2
+ * variant 5 (column quads, N % 32 == 0, column sums on
+ * v_mfma_f32_16x16x32_f16): tile_n 512; rows_per_wave 0; depth 2
  * .. 4 chunk buffers per wavefront (depth - 1 chunks of loads in flight
  * while one is computed); k_waves 1 .. 8 wavefronts, which take every k_waves-th 32-row
  * chunk of the workgroup's share of K; split_k 1 .. min(K/32, 255) workgroups
@@ -190,7 +187,7 @@ int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, i
  * workspace of a split-K launch is laid out as
  *   [uint32 arrival counters: awq_w4a16_counter_bytes()]
  *   [64-bit fixed-point slots, one per output element [M, N]: at most
- *    AWQ_W4A16_SLOT_BYTES (GEMV variants 4, 5 and stream variant 1)]
+ *    AWQ_W4A16_SLOT_BYTES (GEMV variant 5 and stream variant 1)]
  *   [fp32 partial sums (every other split-K plan): [split_k, M, N], or for
  *    the hybrid tile variants 13 and 14 only the leftover tiles',
  *    [split_k, leftover tiles, tile rows, 256]]

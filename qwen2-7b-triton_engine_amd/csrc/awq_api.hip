@@ -41,7 +41,8 @@ constexpr int64_t kFp16LinearMaxM = 8;
 
 constexpr int64_t kIndexLimit = (int64_t)1 << 30;
 // K bound that keeps every 32-bit buffer offset in range, including the rows
-// past M that a 256-row tile reads as zeros: (M + 256) * K * 2 < 2^32.
+// past M that a tile reads as zeros: (M + 256) * K * 2 < 2^32 (tiles hold at
+// most 128 rows; the bound keeps a margin).
 constexpr int64_t kMaxK = (int64_t)1 << 22;
 // Byte-size limit of any one operand (buffer descriptors carry 32-bit sizes).
 constexpr int64_t kBytesLimit = ((int64_t)1 << 31) - 1;
@@ -141,8 +142,8 @@ constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 
 // 512-column strips (tile_n = 512).  Variant 2: k_waves = 128 /
 // rows_per_wave, split_k in 1 .. K/128 with each split a whole number of
-// groups, depth 2 .. 4 chunk buffers (3 at most for 32 rows).  Variants 4
-// and 5: see below.
+// groups, depth 2 .. 4 chunk buffers (3 at most for 32 rows).  Variant 5:
+// see below.
 int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, int64_t rows_per_wave,
               int64_t k_waves, int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
     if (M > kGemvMaxM) return AWQ_ERR_PATH;
@@ -156,15 +157,14 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
     p->factored_scale = 1;
     p->depth = 0;
     if (tile_n != 512) return AWQ_ERR_PATH;
-    if (variant == 4 || variant == 5) {
-        // Column quads (5: MFMA column sums): N % 32 == 0; rows_per_wave 0;
+    if (variant == 5) {
+        // Column quads with MFMA column sums: N % 32 == 0; rows_per_wave 0;
         // depth 2 .. 4 chunk buffers per wave (each
         // strip's K/32 chunks are divided evenly over split_k workgroups of
         // k_waves waves); split_k <= min(K/32, kFixMaxSplit); the groups and
         // x rows a workgroup stages must fit its prologue loads, and the
         // staged data its LDS.
         if (N % 32 != 0 || rows_per_wave != 0 || depth < 2 || depth > 4) return AWQ_ERR_PATH;
-        if (variant == 4 && M > 1 && depth > 3) return AWQ_ERR_PATH;  // that instance would spill registers
         if (k_waves < 1 || k_waves > 8 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
             return AWQ_ERR_PATH;
         if (!gemv_quad_fits((int)M, (int)K, (int)split_k, (int)k_waves)) return AWQ_ERR_PATH;
@@ -375,18 +375,12 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->depth = 0;
     p->lds_bytes = 0;
     if (!tile_variant_served((int)variant) || split_k < 1) return AWQ_ERR_PATH;
-    if (variant == 4) {
-        p->tile_m = 256;
-        p->block_threads = 512;
-    } else {
-        p->tile_m = tile5_rows((int)variant);
-        p->tile_n = 256;
-        p->block_threads = tile5_threads((int)variant);
-    }
+    p->tile_m = tile5_rows((int)variant);
+    p->tile_n = 256;
+    p->block_threads = tile5_threads((int)variant);
     const int64_t tiles = tile_tiles((int)M, (int)N, (int)variant);
-    // K range per split: a multiple of the 64-row k-step (variants 6 and up: of
-    // the 128-row group, two k-steps).
-    const int64_t unit = variant >= 6 ? 128 : 64;
+    // K range per split: whole 128-row groups (two 64-row k-steps).
+    const int64_t unit = kGroup;
     const int64_t steps = K / unit;
     const int64_t per = (steps + split_k - 1) / split_k;
     const int64_t s = (steps + per - 1) / per;
@@ -450,14 +444,13 @@ double tile_cost(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t sp
     return time;
 }
 
-// Where variant 6's grid covers two workgroups per CU (gate||up at M >= 512):
-// variant 6.  Above M = 1024 otherwise: variant 6 when, with split-K up to
-// one pass over its 2 * CUs slots and at least 4096 rows of K per split, it
-// has at least one workgroup per CU; else the k-half pair tile (variant 10)
-// when its tiles fit one pass over the CUs; else variant 4 (256 x 128 tiles)
-// with split-K filling one pass over the CUs, >= 16 k-steps per split.
-// M <= 1024: the variant and split count of least tile_cost (last-arriver
-// variants unsplit only; split no further than 7/4 workgroups per CU).
+// M <= 1024 with variant 6's grid under two workgroups per CU: the variant
+// and split count of least tile_cost (last-arriver variants unsplit only;
+// split no further than 7/4 workgroups per CU).  Above M = 1024: the least
+// busiest-CU time among variant 6 (split-K up to one pass over its 2 * CUs
+// slots, at least 4096 rows of K per split), the 64-row tile and the k-half
+// pair tile (variant 10), or a hybrid (below).  Else (gate||up at M >= 512:
+// variant 6's grid covers two workgroups per CU) variant 6.
 // Measured on the Qwen2-7B prefill GEMMs (qkv, o, gate||up, down) at
 // M = 32 .. 2048.
 // 5 <= M <= 16 on weights the stream path does not take (narrow and
@@ -609,18 +602,7 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     }
     if (tiles6 * split6 >= cus() && fill_tile(M, N, K, 6, split6, p) == AWQ_OK) return AWQ_OK;
     if (tiles6 <= cus() && fill_tile(M, N, K, 10, 1, p) == AWQ_OK) return AWQ_OK;
-    const int64_t tiles = tile_tiles((int)M, (int)N, 4);
-    int64_t split = 1;
-    if (tiles < cus() && tiles * 4 <= (int64_t)kCounterBytes) {
-        split = cus() / tiles;
-        const int64_t max_split = (K / 64) / 16;
-        if (split > max_split) split = max_split;
-        if (split < 1) split = 1;
-        const int64_t steps = K / 64;
-        const int64_t per = (steps + split - 1) / split;
-        split = (steps + per - 1) / per;
-    }
-    return fill_tile(M, N, K, 4, split, p);
+    return fill_tile(M, N, K, 6, 1, p);
 }
 
 // Checks a caller-supplied plan against the shape: it must be exactly what

@@ -140,10 +140,6 @@ __device__ __forceinline__ uint32_t zero_splat_inplace(uint32_t zw, int c) {
     return inplace_column(c) ? (kMagic2Hi | (z << 4) | (z << 20)) : (kMagic2 | z | (z << 16));
 }
 
-// a.lo * b.lo + a.hi * b.hi in fp32 from fp16 pairs, starting from zero.
-__device__ __forceinline__ float dot2_from_zero(uint32_t a, uint32_t b) {
-    return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), 0.0f, false);
-}
 
 __device__ __forceinline__ floatx4 mfma16x16x32(half8_t a, half8_t b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

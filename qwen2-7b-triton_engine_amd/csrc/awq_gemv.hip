@@ -5,8 +5,9 @@
 // split-K finish at the end.  Two kernels:
 //  * variant 2 (awq_gemv_stream_kernel): one 128-row group per step, lane =
 //    packed column, v_dot2_f32_f16 sums; serves N % 32 != 0;
-//  * variants 4 and 5 (awq_gemv_quad_kernel): column quads, 16-byte loads,
-//    interleaved 32-row chunks, fixed-point split-K finish; the default.
+//  * variant 5 (awq_gemv_quad_kernel): column quads, 16-byte loads,
+//    interleaved 32-row chunks, MFMA column sums, fixed-point split-K
+//    finish; the default.
 // Both handle the zero outside the dot products: the codes are read as
 // fp16 (b + q) by the magic-number unpack (b = 1024, or 64 for the nibbles
 // cut in place, see awq_device.h), the lanes accumulate
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 }
 
 // ---------------------------------------------------------------------------
-// Variant 4: quad-column GEMV, interleaved 32-row chunks, fixed-point split-K.
+// Variant 5: column-quad GEMV, interleaved 32-row chunks, fixed-point split-K.
 //
 // Lane l: c4 = l % 16 owns packed columns 4*c4 .. 4*c4+3 of the workgroup's
 // 64-column strip (32 outputs) and reads them with one 16-byte load per row,
@@ -220,23 +221,19 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 // scheduling barriers keep a chunk's arithmetic after the loads issued
 // before it.
 //
-// Arithmetic: sum_r x[r] * (b + q) per column by v_dot2_f32_f16 on the
-// magic-number codes and sum_r x[r]; after each
-// chunk  acc += s * sum - s(b + z) * sum_x.  At the end the four row
-// slots of a column quad are added with cross-lane shuffles, the waves
-// through LDS, and each output's partial is stored (split_k == 1) or goes
-// through fixed_add_finish.  Needs N % 32 == 0 (whole quads).
+// Arithmetic: per chunk, sum_r x[r] * (b + q) per column on
+// v_mfma_f32_16x16x32_f16: the magic-number k-pairs of a lane's 8 rows of
+// one column are its B fragment as they are (lane n = c4, k-block = rq: the
+// MFMA operand layout), x rows m = c4 < M supply A in the same k order, and
+// an MFMA against ones gives sum_r x[r]; the MFMA sums the 32 rows inside the
+// chunk, so lane (c4, rq = 0) holds row m of its 32 columns in register m
+// and no cross-lane reduction is needed.  After each chunk acc += s * sum -
+// s(b + z) * sum_x for the M live rows.  At the end the waves are added
+// through LDS and each output's partial is stored (split_k == 1) or goes
+// through the fixed-point finish.  Needs N % 32 == 0 (whole quads).
 constexpr int kQuadItemsPerThread = 4;  // prologue loads per thread (consts and x each)
 
-// MM (variant 5): the column sums of a chunk come from v_mfma_f32_16x16x32_f16
-// instead of v_dot2: the magic-number k-pairs of a lane's 8 rows of one column
-// are its B fragment as they are (lane n = c4, k-block = rq: the MFMA
-// operand layout), x rows m = c4 < M supply A in the same k order, and an
-// MFMA against ones gives sum_r x[r]; the MFMA sums the 32 rows inside the
-// chunk, so lane (c4, rq = 0) holds row m of its 32 columns in register m
-// and no cross-lane reduction is needed.  The fold per chunk touches the M
-// live rows only.
-template <int MR, bool MM, int D>
+template <int MR, int D>
 __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int split_k, unsigned long long* fix) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int lane = threadIdx.x & 63;
@@ -340,15 +337,15 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     }
     __syncthreads();
 
-    float acc[MR][32], in[MR][32], sx[MR];
+    float acc[MR][32];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
         for (int i = 0; i < 32; ++i) acc[m][i] = 0.f;
     const uint32_t ones = 0x3C003C00u;  // fp16 (1, 1)
 
-    // MFMA form: A = x rows (zero for lanes c4 >= M), S = row sums of x.
-    auto compute_mfma = [&](const Chunk& ck, int c) {
+    // A = x rows (zero for lanes c4 >= M), S = row sums of x.
+    auto compute = [&](const Chunk& ck, int c) {
         const int cl = c - c0;
         u32x4 av = {0u, 0u, 0u, 0u};
         if (c4 < MR) {
@@ -384,55 +381,6 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         }
     };
 
-    // The first row pair of a chunk starts each sum from zero without a
-    // register clear (dot2_from_zero), and the fold is two fused
-    // multiply-adds per column.
-    auto compute = [&](const Chunk& ck, int c) {
-        if constexpr (MM) {
-            compute_mfma(ck, c);
-            return;
-        }
-        const int cl = c - c0;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            u32x2 xq[MR];
-#pragma unroll
-            for (int m = 0; m < MR; ++m)
-                xq[m] = *reinterpret_cast<const u32x2*>(lx + (size_t)m * nc * 32 + cl * 32 + 16 * h + 4 * rq);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const bool first = h == 0 && i == 0;
-#pragma unroll
-                for (int m = 0; m < MR; ++m)
-                    sx[m] = first ? dot2_from_zero(xq[m][i], ones)
-                                  : __builtin_amdgcn_fdot2(as_h2(xq[m][i]), as_h2(ones), sx[m], false);
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    uint32_t kp[8];
-                    kpairs_magic_inplace(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp);
-#pragma unroll
-                    for (int cc = 0; cc < 8; ++cc)
-#pragma unroll
-                        for (int m = 0; m < MR; ++m)
-                            in[m][8 * p + cc] = first ? dot2_from_zero(kp[cc], xq[m][i])
-                                                      : __builtin_amdgcn_fdot2(as_h2(kp[cc]), as_h2(xq[m][i]),
-                                                                               in[m][8 * p + cc], false);
-                }
-            }
-        }
-        const int gi = c / 4 - g_lo;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const floatx4 v = lc[(gi * 16 + i) * 16 + c4];
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                acc[m][2 * i] = __builtin_fmaf(-v[1], sx[m], __builtin_fmaf(v[0], in[m][2 * i], acc[m][2 * i]));
-                acc[m][2 * i + 1] =
-                    __builtin_fmaf(-v[3], sx[m], __builtin_fmaf(v[2], in[m][2 * i + 1], acc[m][2 * i + 1]));
-            }
-        }
-    };
-
     for (int c = c0 + wave; c < c1; c += D * nw) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
@@ -444,19 +392,6 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         fence();
     }
 
-    // Row slots rq = 0..3 of a column quad sit in lanes l, l^16, l^32, l^48
-    // (the MFMA form has already summed them).
-    if constexpr (!MM) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                float v = acc[m][i];
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
-                acc[m][i] = v;
-            }
-    }
     __syncthreads();  // every wave is done with the staged consts: the LDS becomes the reduction buffer
     float* red = reinterpret_cast<float*>(lds);
     if (rq == 0) {
@@ -529,37 +464,31 @@ static hipError_t gemv_stream_launch(const GemmArgs& a, const GemvConfig& cfg, u
     return hipGetLastError();
 }
 
-template <int MR, bool MM, int D>
+template <int MR, int D>
 static hipError_t gemv_quad_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
                                    hipStream_t stream) {
     unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
     const size_t lds = gemv_quad_lds_bytes(a.M, a.K, cfg.split_k, cfg.kw_count);
-    hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, MM, D>), dim3((unsigned)(gemv_strips(a.N) * cfg.split_k)),
+    hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D>), dim3((unsigned)(gemv_strips(a.N) * cfg.split_k)),
                        dim3(64 * cfg.kw_count), lds, stream, a, cfg.split_k, fix);
     return hipGetLastError();
 }
 
-template <bool MM>
 static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
                                      hipStream_t stream) {
     switch ((a.M <= 1 ? 10 : 20) + cfg.depth) {
-        case 12: return gemv_quad_launch<1, MM, 2>(a, cfg, counters, stream);
-        case 13: return gemv_quad_launch<1, MM, 3>(a, cfg, counters, stream);
-        case 14: return gemv_quad_launch<1, MM, 4>(a, cfg, counters, stream);
-        case 22: return gemv_quad_launch<2, MM, 2>(a, cfg, counters, stream);
-        case 23: return gemv_quad_launch<2, MM, 3>(a, cfg, counters, stream);
-        case 24:
-            // The dot2 form with two x rows and four chunk buffers would spill
-            // registers; plans refuse it, so it is not built.
-            if constexpr (MM) return gemv_quad_launch<2, MM, 4>(a, cfg, counters, stream);
-            return hipErrorInvalidValue;
+        case 12: return gemv_quad_launch<1, 2>(a, cfg, counters, stream);
+        case 13: return gemv_quad_launch<1, 3>(a, cfg, counters, stream);
+        case 14: return gemv_quad_launch<1, 4>(a, cfg, counters, stream);
+        case 22: return gemv_quad_launch<2, 2>(a, cfg, counters, stream);
+        case 23: return gemv_quad_launch<2, 3>(a, cfg, counters, stream);
+        case 24: return gemv_quad_launch<2, 4>(a, cfg, counters, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream) {
-    if (cfg.variant == 4) return gemv_quad_dispatch<false>(a, cfg, counters, stream);
-    if (cfg.variant == 5) return gemv_quad_dispatch<true>(a, cfg, counters, stream);
+    if (cfg.variant == 5) return gemv_quad_dispatch(a, cfg, counters, stream);
     if (cfg.variant == 2) {
         const int key2 = (a.M <= 1 ? 1 : 2) * 10000 + cfg.rows_per_wave * 10 + cfg.depth;
         switch (key2) {

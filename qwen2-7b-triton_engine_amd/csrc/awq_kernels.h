@@ -32,8 +32,8 @@ struct SkinnyConfig {
 };
 
 struct GemvConfig {
-    int variant;             // 2: K-streaming, one group per chunk; 4, 5: column quads (dot2 /
-                             // MFMA column sums), fixed-point split-K finish
+    int variant;             // 2: K-streaming, one group per chunk; 5: column quads with MFMA
+                             // column sums, fixed-point split-K finish
     int rows_per_wave;       // variant 2: K rows per wave, 16 or 32
     int kw_count;            // waves per workgroup along K: 1 .. 8 (variant 2: 128 / rows_per_wave)
     int split_k;             // workgroups along K
@@ -43,7 +43,6 @@ struct GemvConfig {
 
 // Tile variants 6 .. kTileVariants: weights dequantised into MFMA registers,
 // every load a direct global->LDS load into a ring (x rows per tile, stages).
-// Variant 4: 256 x 128 tiles, weights dequantised once per k-step into LDS.
 // Variants 13, 14: the hybrid of variants 6 (128 rows) and 8 (64 rows) --
 // whole tiles on every CU, the leftover tiles split along K.
 constexpr int kTileVariants = 14;
@@ -53,13 +52,13 @@ constexpr int tile5_rows(int variant) {
 constexpr int tile5_threads(int variant) { return (variant >= 10 && variant <= 12) ? 512 : 256; }
 constexpr bool tile_hybrid(int variant) { return variant == 13 || variant == 14; }
 // Whether a tile variant number names a kernel.
-constexpr bool tile_variant_served(int variant) { return variant == 4 || (variant >= 6 && variant <= kTileVariants); }
+constexpr bool tile_variant_served(int variant) { return variant >= 6 && variant <= kTileVariants; }
 
 struct TileConfig {
-    int variant;             // 4: 256x128x64, LDS W^T; 6 .. kTileVariants: register dequant, N tile 256
+    int variant;             // 6 .. kTileVariants: register dequant, N tile 256
     int tile_m, tile_n;
     int split_k;             // workgroups along K per tile (hybrid: per leftover tile)
-    int k_per_split;         // K rows per split (multiple of 64; variants 6 and up: of 128)
+    int k_per_split;         // K rows per split (a multiple of the 128-row group)
     int64_t grid;            // workgroups (the hybrid's: whole tiles + leftover tiles x split_k)
 };
 

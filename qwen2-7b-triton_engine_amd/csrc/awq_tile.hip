@@ -1,301 +1,14 @@
-// Prefill W4A16 AWQ GEMM (large M) for gfx950: LDS-tiled MFMA kernels.
-//
-// Two kernel families:
-//  * awq_tile_kernel_v3 (tile variant 4): 256 x 128 x 64 tiles, weights
-//    dequantised once per k-step into an LDS W^T buffer shared by all 256
-//    rows;
-//  * awq_tile_kernel_v5 (tile variants 6 .. 12): 256 output columns per
-//    tile, weights dequantised straight into MFMA operand registers.
-// Both stream every operand into LDS rings with direct global->LDS loads and
-// form the reference's exact fp16 weight fp16((q - z) * s) next to the load.
-#include <type_traits>
-
+// Prefill W4A16 AWQ GEMM (large M) for gfx950: LDS-tiled MFMA kernels
+// (awq_tile_kernel_v5, tile variants 6 .. 14): 256 output columns per tile,
+// weights dequantised straight into MFMA operand registers, every operand
+// streamed into LDS rings by direct global->LDS loads, the reference's exact
+// fp16 weight fp16((q - z) * s) formed next to the load.
 #include "awq_kernels.h"
 
 namespace awq {
 
 // ---------------------------------------------------------------------------
-// Variant 4: 256 x 128 x 64 tiles, 512 threads (8 waves of 64 x 64), every
-// operand streamed into LDS rings by direct global->LDS loads.
-//
-// buffer_load_dword[x4] ... lds writes each lane's 4 (16) bytes to
-// M0 + 4*lane (16*lane): a wave writes one contiguous LDS block per
-// instruction, and each lane chooses which global element lands in its slot.
-//   * x: 3-stage ring, rows of 128 B XOR-swizzled (16-byte chunk p of row r
-//     holds k-chunk p ^ (r & 7)), so the MFMA fragment reads of 8 consecutive
-//     rows hit 8 distinct chunk positions (all banks once).  Rows beyond M
-//     read as zeros (buffer out-of-range).
-//   * raw int4 words: 4-stage ring.  Block b (68 words, 4 of them padding)
-//     holds rows 4b .. 4b+3 of the 16 packed columns, word 4*jj + (r & 3):
-//     each load instruction reads 4 row segments of 64 bytes, and the thread
-//     that dequantises rows (2p, 2p+1) of packed column jj reads one 8-byte
-//     word pair; the padding spreads a wave's reads over all banks.
-//   * zero words and scales of the k-step's group: 4-stage ring; wave 0
-//     loads the zero words, every other wave the same 64 scale words (one
-//     load per wave keeps the per-wave load count uniform).
-// The dequantised weight (the reference's exact fp16 (q - z) * s) is written
-// to one of two W^T buffers one k-step ahead of its MFMAs.
-//
-// The loads are issued from inline assembly, 7 per wave per k-step (loads
-// past the last k-step re-read it, into free slots).  The compiler, which
-// cannot tell which LDS bytes a direct load writes, would otherwise wait for
-// every outstanding load before each LDS read; the kernel waits itself: the
-// barrier that ends k-step t is preceded by s_waitcnt vmcnt(7), so every load
-// issued up to k-step t-1 has landed.  Distances: x for step t+2 and raw
-// weights for step t+3 are issued in step t; step t+1's raw weights, issued
-// in step t-2, are dequantised in step t; step t+2's x is read in step t+2.
-namespace {
-constexpr int T3_BM = 256;
-constexpr int T3_BN = 128;
-constexpr int T3_BK = 64;
-constexpr int T3_XS = 3;              // x stages
-constexpr int T3_RS = 4;              // raw weight / zero+scale stages
-constexpr int T3_WPITCH = T3_BK + 8;  // halves per W^T row (144 B)
-constexpr int T3_GM = 4;              // M tiles per group of the tile order
-constexpr int T3_RAW_BLOCK = 68;                  // words per 4-row block (64 + padding)
-constexpr int T3_RAW_WORDS = 16 * T3_RAW_BLOCK;   // 64 rows x 16 packed columns
-constexpr int T3_ZS_WORDS = 128;      // 64 zero-word slots (16 used) + 64 scale words
-// s_waitcnt vmcnt(7), expcnt/lgkmcnt at their maxima (gfx9 encoding).
-constexpr int kWaitVm7 = 0x0F77;
-
-}  // namespace
-
-// The next k-step's dequant (LDS reads issued first, VALU and W^T stores) is
-// interleaved with this k-step's MFMAs by scheduling groups instead of
-// following them, so the 8 waves, which meet at one barrier per k-step,
-// overlap dequant arithmetic with matrix work.
-__global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int split_k, int k_per_split,
-                                                             uint32_t* counters) {
-    __shared__ __attribute__((aligned(16))) half_t Xs[T3_XS][T3_BM * T3_BK];
-    __shared__ __attribute__((aligned(16))) half_t Ws[2][T3_BN * T3_WPITCH];
-    __shared__ __attribute__((aligned(16))) uint32_t Wr[T3_RS][T3_RAW_WORDS];
-    __shared__ __attribute__((aligned(16))) uint32_t Zs[T3_RS][T3_ZS_WORDS];
-    __shared__ int last_flag;
-    floatx4* fin = reinterpret_cast<floatx4*>(&Xs[0][0]);  // split-K finish, after the main loop
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 3;
-    const int wn = wave >> 2;
-    const int c16 = lane & 15;
-    const int kq = lane >> 4;
-
-    // ---- work item: XCD-aware grouped tile order.  Workgroup b runs on XCD
-    // b % 8 (round-robin dispatch); the workgroups of one XCD take a
-    // contiguous range of the grouped-M tile order, so the concurrent
-    // workgroups of an XCD share x rows and weight columns in its L2.  Any
-    // other dispatch order only costs locality: the mapping is a bijection.
-    const int m_tiles = (a.M + T3_BM - 1) / T3_BM;
-    const int n_tiles = (a.N + T3_BN - 1) / T3_BN;
-    const int total = (int)gridDim.x;
-    const int xcd = blockIdx.x & 7;
-    const int xi = blockIdx.x >> 3;
-    const int per = (total + 7) >> 3;
-    const int rem = total & 7;
-    const int w = (rem == 0 || xcd < rem) ? xcd * per + xi : rem * per + (xcd - rem) * (per - 1) + xi;
-    const int tile = w / split_k;
-    const int split = w - tile * split_k;
-    const int in_group = T3_GM * n_tiles;
-    const int first_m = (tile / in_group) * T3_GM;
-    const int gm = min(m_tiles - first_m, T3_GM);
-    const int tm = first_m + (tile % in_group) % gm;
-    const int tn = (tile % in_group) / gm;
-    const int m0 = tm * T3_BM;
-    const int n0 = tn * T3_BN;
-    const int pn = a.N >> 3;
-    const int j0 = n0 >> 3;
-    const int k_begin = split * k_per_split;
-    const int k_end = min(a.K, k_begin + k_per_split);
-    const int KT = (k_end - k_begin) / T3_BK;
-
-    // ---- per-lane source offsets of the direct loads ----
-    const u32x4 rx = raw_rsrc(a.x, (uint32_t)((size_t)a.M * a.K * 2));
-    const u32x4 rw = raw_rsrc(a.qweight, (uint32_t)((size_t)a.K * pn * 4));
-    const u32x4 rz = raw_rsrc(a.qzeros, (uint32_t)((size_t)(a.K / kGroup) * pn * 4));
-    const u32x4 rs = raw_rsrc(a.scales, (uint32_t)((size_t)(a.K / kGroup) * a.N * 2));
-    // x: instruction i of wave w fills rows 8*(8i+w) .. +7 of the stage.
-    const int xr_in_blk = lane >> 3;
-    const int xkc = (lane & 7) ^ xr_in_blk;
-    uint32_t x_voff[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 8 * (i * 8 + wave) + xr_in_blk;
-        x_voff[i] = (uint32_t)(((size_t)(m0 + r) * a.K + 8 * xkc) * 2);
-    }
-    // raw weights: instruction i of wave w fills block b = 2w + i; lane l reads
-    // qweight[kb + 4b + (l & 3)][j0 + (l >> 2)] (columns past the last clamp to it).
-    const uint32_t w_voff = (uint32_t)(((lane & 3) * pn + min(j0 + (lane >> 2), pn - 1)) * 4);
-    // zero words (wave 0, lane l: packed column j0 + l, clamped) and scales
-    // (other waves, lane l: columns n0 + 2l, n0 + 2l + 1; past N they read the
-    // next group's bytes or zeros, and are never used).
-    const bool zs_is_zero = wave == 0;  // wave-uniform
-    const uint32_t zs_voff =
-        zs_is_zero ? (uint32_t)(min(j0 + lane, pn - 1) * 4) : (uint32_t)((n0 + 2 * lane) * 2);
-
-    auto issue_x = [&](int kt, int xstage) {
-        const int kb = k_begin + kt * T3_BK;
-        const uint32_t xs_off = __builtin_amdgcn_readfirstlane((uint32_t)kb * 2u);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            buffer_load_lds_x4(rx, x_voff[i], xs_off, lds_addr(&Xs[xstage][(i * 8 + wave) * 512]));
-    };
-    auto issue_raw = [&](int kt, int rstage) {
-        const int kb = k_begin + kt * T3_BK;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int b = 2 * wave + i;
-            buffer_load_lds_x1(rw, w_voff, __builtin_amdgcn_readfirstlane((uint32_t)(kb + 4 * b) * (uint32_t)pn * 4u),
-                               lds_addr(&Wr[rstage][b * T3_RAW_BLOCK]));
-        }
-        const int g = kb / kGroup;
-        if (zs_is_zero)
-            buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
-                               lds_addr(&Zs[rstage][0]));
-        else  // identical bytes from every wave
-            buffer_load_lds_x1(rs, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
-                               lds_addr(&Zs[rstage][64]));
-    };
-
-    // ---- dequant: thread = (packed column jj, row pair rp) ----
-    const int jj = tid >> 5;
-    const int rp = tid & 31;
-    const bool wok = j0 + jj < pn;
-    auto dequant = [&](int rstage, int wbuf) {
-        const u32x2 wpair =
-            *reinterpret_cast<const u32x2*>(&Wr[rstage][(rp >> 1) * T3_RAW_BLOCK + 4 * jj + 2 * (rp & 1)]);
-        const uint32_t zw = Zs[rstage][jj];
-        const half8_t s8 = *reinterpret_cast<const half8_t*>(&Zs[rstage][64 + 4 * jj]);
-        uint32_t kp[8];
-        kpairs_magic(wpair[0], wpair[1], kp);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const half2_t v = (as_h2(kp[c]) - as_h2(zero_splat(zw, c))) * half2_t{s8[c], s8[c]};
-            *reinterpret_cast<uint32_t*>(&Ws[wbuf][(8 * jj + c) * T3_WPITCH + 2 * rp]) = wok ? as_u32(v) : 0u;
-        }
-    };
-
-    floatx4 acc[4][4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    if (KT > 0) {
-        const int last = KT - 1;
-        // Prologue: x for steps 0, 1; raw weights for steps 0, 1, 2.
-        issue_x(0, 0);
-        issue_x(min(1, last), 1);
-        issue_raw(0, 0);
-        issue_raw(min(1, last), 1);
-        issue_raw(min(2, last), 2);
-        wait_vm_stores();
-        __syncthreads();
-        dequant(0, 0);
-        __syncthreads();
-        for (int kt = 0; kt < KT; ++kt) {
-            // Both rings' target stages were last read before the previous barrier.
-            issue_x(min(kt + 2, last), (kt + 2) % T3_XS);
-            issue_raw(min(kt + 3, last), (kt + 3) % T3_RS);
-            const half_t* xs = Xs[kt % T3_XS];
-            const half_t* wsb = Ws[kt & 1];
-            // Operands of the next k-step's dequant (its stage holds clamped
-            // data on the last step; the W^T buffer it writes is not read
-            // again).
-            const int rs1 = (kt + 1) % T3_RS;
-            const u32x2 wpair =
-                *reinterpret_cast<const u32x2*>(&Wr[rs1][(rp >> 1) * T3_RAW_BLOCK + 4 * jj + 2 * (rp & 1)]);
-            const uint32_t zw = Zs[rs1][jj];
-            const half8_t s8 = *reinterpret_cast<const half8_t*>(&Zs[rs1][64 + 4 * jj]);
-            half8_t af[2][4], bfr[2][4];
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    af[s2][x] = *reinterpret_cast<const half8_t*>(
-                        &wsb[(64 * wn + 16 * x + c16) * T3_WPITCH + 32 * s2 + 8 * kq]);
-#pragma unroll
-                for (int y = 0; y < 4; ++y) {
-                    const int r = 64 * wm + 16 * y + c16;
-                    const int phys = (4 * s2 + kq) ^ (r & 7);
-                    bfr[s2][y] = *reinterpret_cast<const half8_t*>(&xs[r * T3_BK + 8 * phys]);
-                }
-            }
-            uint32_t kp[8];
-            kpairs_magic(wpair[0], wpair[1], kp);
-            uint32_t wv[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                wv[c] = as_u32((as_h2(kp[c]) - as_h2(zero_splat(zw, c))) * half2_t{s8[c], s8[c]});
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-                for (int x = 0; x < 4; ++x)
-#pragma unroll
-                    for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(af[s2][x], bfr[s2][y], acc[x][y]);
-            half_t* wnext = Ws[(kt + 1) & 1];
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                *reinterpret_cast<uint32_t*>(&wnext[(8 * jj + c) * T3_WPITCH + 2 * rp]) = wok ? wv[c] : 0u;
-            // Order: all LDS reads, then MFMAs each followed by two VALU
-            // instructions of the dequant, the W^T stores last.
-            __builtin_amdgcn_sched_group_barrier(0x100, 19, 0);
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);
-            __builtin_amdgcn_s_waitcnt(kWaitVm7);
-            __syncthreads();
-        }
-        wait_vm_stores();  // drain the re-read tail loads before the LDS is reused
-        __syncthreads();
-    }
-
-    // acc[x][y] lane value v: out^T[n = 16x + 4kq + v][m = 16y + c16] of this wave's 64 x 64.
-    if (split_k == 1) {
-#pragma unroll
-        for (int y = 0; y < 4; ++y) {
-            const int gm_ = m0 + 64 * wm + 16 * y + c16;
-            if (gm_ >= a.M) continue;
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
-                if (gn >= a.N) continue;
-                const float v[4] = {acc[x][y][0], acc[x][y][1], acc[x][y][2], acc[x][y][3]};
-                store_out<4>(a.out, a.bias, a.residual, a.N, gm_, gn, v);
-            }
-        }
-        return;
-    }
-
-    const uint32_t part_bytes = (uint32_t)((size_t)split_k * a.M * a.N * 4);
-    const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-        const int gm_ = m0 + 64 * wm + 16 * y + c16;
-        if (gm_ >= a.M) continue;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-            const int gn = n0 + 64 * wn + 16 * x + 4 * kq;
-            if (gn >= a.N) continue;
-            buf_store_f4_device(acc[x][y], rp_, (uint32_t)((((size_t)split * a.M + gm_) * a.N + gn) * 4));
-        }
-    }
-    wait_vm_stores();
-    __syncthreads();
-    if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (uint32_t)(split_k - 1);
-    __syncthreads();
-    if (!last_flag) return;
-    splitk_finish<16>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(T3_BM, a.M - m0), n0, min(T3_BN, a.N - n0), split_k, fin);
-    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---------------------------------------------------------------------------
-// Variants 6 .. 12: 256 output columns per tile, each wave 64 columns x 32,
+// Variants 6 .. 14: 256 output columns per tile, each wave 64 columns x 32,
 // 64 or 128 x rows, weights dequantised straight into MFMA A registers (never written
 // back to LDS), every global load a direct global->LDS load issued two
 // k-steps ahead into a 3-stage ring.  No VGPR holds data in flight and the
@@ -304,8 +17,10 @@ __global__ __launch_bounds__(512, 1) void awq_tile_kernel_v3(GemmArgs a, int spl
 // k-step, right before the barrier (vmcnt = the loads issued since).
 //
 // A stage holds one k-step (64 rows):
-//   * x: BM rows of 128 B, 16-byte chunk p of row r holding k-chunk
-//     p ^ (r & 7) (as variant 4); a wave's dwordx4 load writes 8 rows.
+//   * x: BM rows of 128 B, XOR-swizzled: 16-byte chunk p of row r holds
+//     k-chunk p ^ (r & 7), so the MFMA fragment reads of 8 consecutive rows
+//     hit 8 distinct chunk positions (all banks once); rows beyond M read as
+//     zeros (buffer range check); a wave's dwordx4 load writes 8 rows.
 //   * packed weights: 64 rows x 32 packed columns, dword
 //     ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h + 8 kb + 4 ub + u
 //     of column j, so the lane that owns column j and rows 8 kb .. + 7 of
@@ -390,7 +105,7 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
     const int kb = lane >> 4;
     const int hh = n16 >> 3;
 
-    // ---- work item: XCD-aware grouped tile order (as variant 4) ----
+    // ---- work item: XCD-aware grouped tile order (groups of T5_GM row tiles) ----
     const int m_tiles = (a.M + BM - 1) / BM;
     const int n_tiles = (a.N + T5_BN - 1) / T5_BN;
     // Position of workgroup b among `total` consecutive ones in XCD order:
@@ -649,21 +364,11 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
 }
 
 int64_t tile_tiles(int M, int N, int variant) {
-    if (variant >= 6 && variant <= kTileVariants) {
-        const int bm = tile5_rows(variant);
-        return (int64_t)((M + bm - 1) / bm) * ((N + T5_BN - 1) / T5_BN);
-    }
-    return (int64_t)((M + T3_BM - 1) / T3_BM) * ((N + T3_BN - 1) / T3_BN);
+    const int bm = tile5_rows(variant);
+    return (int64_t)((M + bm - 1) / bm) * ((N + T5_BN - 1) / T5_BN);
 }
 
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream) {
-    if (cfg.variant == 4) {
-        const int64_t blocks = tile_tiles(a.M, a.N, 4) * cfg.split_k;
-        if (blocks == 0) return hipSuccess;
-        hipLaunchKernelGGL(awq_tile_kernel_v3, dim3((unsigned)blocks), dim3(512), 0, stream, a, cfg.split_k,
-                           cfg.k_per_split, counters);
-        return hipGetLastError();
-    }
     if (cfg.variant >= 6 && cfg.variant <= kTileVariants) {
         const int64_t blocks = tile_hybrid(cfg.variant) ? cfg.grid : tile_tiles(a.M, a.N, cfg.variant) * cfg.split_k;
         if (blocks == 0) return hipSuccess;

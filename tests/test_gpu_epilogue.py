@@ -29,12 +29,12 @@ def _plans(m, n, k):
         makers.append((_native.PATH_NAMES[path], lambda path=path: _native.plan_for(m, n, k, path=path)))
     if m <= 2:
         makers += [(f"gemv quad v{v} s{sp}", lambda v=v, sp=sp: _native.plan_gemv(m, n, k, 0, 4, variant=v, split_k=sp))
-                   for v in (4, 5) for sp in (1, 3, 16)]
+                   for v in (5,) for sp in (1, 3, 16)]
     if m <= 16:
         makers += [(f"stream v{v} s4", lambda v=v: _native.plan_stream(m, n, k, 2, 4, variant=v)) for v in (1, 2, 3)]
     if m > 16:
         makers += [(f"tile v{v} s{sp}", lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp))
-                   for v, sp in ((4, 1), (4, 2), (6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (10, 1), (11, 2),
+                   for v, sp in ((6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (10, 1), (11, 2),
                                  (12, 2), (13, 2), (14, 3))]
     out = []
     for label, make in makers:

@@ -172,12 +172,12 @@ def test_tile_plans_cover_k_exactly(L, k, n):
                     # no such kernel or split, or partials beyond 2^31 bytes (M = 2048, 8 splits)
                     assert e.status in (_native.AWQ_ERR_PATH, _native.AWQ_ERR_TOO_LARGE)
                     continue
-                assert variant == 4 or 6 <= variant <= 14
+                assert 6 <= variant <= 14
                 per = p.rows_per_wave
-                assert per % (128 if variant >= 6 else 64) == 0
+                assert per % 128 == 0
                 assert (split - 1) * per < k <= split * per
-                tm = {4: 256, 6: 128, 7: 128, 8: 64, 9: 32, 12: 64, 14: 64}.get(variant, 128)
-                tn = 256 if variant >= 6 else 128
+                tm = {6: 128, 7: 128, 8: 64, 9: 32, 12: 64, 14: 64}.get(variant, 128)
+                tn = 256
                 tiles = -(-m // tm) * -(-n // tn)
                 if variant in (13, 14):
                     full, left = tiles // 256, tiles % 256
@@ -214,7 +214,7 @@ def test_skinny_and_gemv_plan_rejections():
     assert e.value.status == _native.AWQ_ERR_PATH
     with pytest.raises(_native.AwqNativeError):
         _native.plan_gemv(1, 512, 3584, 16, 8, variant=2, depth=5)   # depth not an instance
-    for variant in (1, 3, 6):                           # no GEMV kernel of that number
+    for variant in (1, 3, 4, 6):                        # no GEMV kernel of that number
         with pytest.raises(_native.AwqNativeError):
             _native.plan_gemv(1, 512, 3584, 16, 8, variant=variant)
     with pytest.raises(_native.AwqNativeError):
@@ -230,8 +230,9 @@ def test_skinny_and_gemv_plan_rejections():
         _native.plan_skinny(65, 512, 3584, 256, 2)      # skinny serves M <= 64
     with pytest.raises(_native.AwqNativeError):
         _native.plan_skinny(8, 512, 3584, 256, 3)       # k_waves must be 1, 2 or 4
-    with pytest.raises(_native.AwqNativeError):
-        _native.plan_tile(512, 512, 3584, 5, 1)         # no tile kernel of that number
+    for variant in (4, 5):                              # no tile kernel of that number
+        with pytest.raises(_native.AwqNativeError):
+            _native.plan_tile(512, 512, 3584, variant, 1)
     with pytest.raises(_native.AwqNativeError):
         _native.plan_tile(512, 512, 3584, 13, 1)
 
@@ -239,7 +240,7 @@ def test_skinny_and_gemv_plan_rejections():
 def test_planned_call_rejects_altered_plan(L):
     """gemm_planned re-derives the plan: a hand-edited field is refused before launch."""
     m, n, k = 512, 3584, 3584
-    p = _native.plan_tile(m, n, k, 4, 1)
+    p = _native.plan_tile(m, n, k, 6, 1)
     p.grid += 1
     buf = np.zeros(1 << 12, dtype=np.uint8)
     ptr = ctypes.c_void_p((buf.ctypes.data + 255) & ~255)
