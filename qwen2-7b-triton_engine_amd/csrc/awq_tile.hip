@@ -9,24 +9,30 @@ namespace awq {
 
 // ---------------------------------------------------------------------------
 // Variants 6 .. 14: 256 output columns per tile, each wave 64 columns x 32,
-// 64 or 128 x rows, weights dequantised straight into MFMA A registers (never written
-// back to LDS), every global load a direct global->LDS load issued two
+// 64 or 128 x rows, weights dequantised straight into MFMA A registers (never
+// written back to LDS), every global load a direct global->LDS load issued two
 // k-steps ahead into a 3-stage ring.  No VGPR holds data in flight and the
 // compiler sees no global load inside the main loop, so nothing waits on a
 // load before the step that consumes it: the kernel waits itself, once per
-// k-step, right before the barrier (vmcnt = the loads issued since).
+// k-step (vmcnt = the loads issued since).
 //
 // A stage holds one k-step (64 rows):
 //   * x: BM rows of 128 B, XOR-swizzled: 16-byte chunk p of row r holds
 //     k-chunk p ^ (r & 7), so the MFMA fragment reads of 8 consecutive rows
 //     hit 8 distinct chunk positions (all banks once); rows beyond M read as
 //     zeros (buffer range check); a wave's dwordx4 load writes 8 rows.
-//   * packed weights: 64 rows x 32 packed columns, dword
-//     ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h + 8 kb + 4 ub + u
-//     of column j, so the lane that owns column j and rows 8 kb .. + 7 of
-//     half h reads them as two 16-byte words; one dword load covers 4 rows x
-//     16 columns (64-byte row segments).
-//   * the group's zero words (32 dwords) and scales (256 halves).
+//   * packed weights, 64 rows x 32 packed columns.  KW = 1: 64-dword block
+//     8 w + 4 h + kb holds wave w's columns 8 w .. + 7, rows 32 h + 8 kb ..
+//     + 7 as dword 32 ub + 4 c + u = row 32 h + 8 kb + 4 ub + u of column
+//     8 w + c (each wave loads its own block with 8 dword loads).  KW = 2:
+//     dword ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h + 8 kb +
+//     4 ub + u of column j, one dword load covering 4 rows x 16 columns.
+//     Either way the lane that owns column j and rows 8 kb .. + 7 of half h
+//     reads them as two 16-byte words.
+//   * the group's zero words and scales: KW = 1, per wave its 8 zero words
+//     and 64 scales (160 B); KW = 2, 32 zero words and 256 scales.
+// KW = 1 runs each k-step in two phases and overlaps the dequantisation of
+// the next k-half with the MFMAs of the current one (see the main loop).
 // FM: 16-row blocks per wave (8: 128 x rows per wave; 4: 64; 2: 32).
 // KW: 2 -- a second wave per SIMD from the same workgroup: waves w and w + 4
 // take k-half 0 and 1 of every k-step for the same columns and rows (each
@@ -44,6 +50,7 @@ constexpr int T5_BK = 64;
 constexpr int T5_BN = 256;
 constexpr int T5_W_BYTES = 64 * 32 * 4;       // packed weights of one k-step
 constexpr int T5_ZS_BYTES = 768;              // 256 B zero words (128 used) + 512 B scales
+constexpr int T5_ZS_WAVE = 160;               // one wave's 8 zero words + 64 scales
 constexpr int T5_GM = 4;
 constexpr int T5_STAGES = 3;
 
@@ -53,20 +60,24 @@ struct T5Layout {
     static constexpr int RW = 16 * FM;  // x rows per wave
     static constexpr int BM = RW;
     static constexpr int X_BYTES = BM * T5_BK * 2;
-    static constexpr int STAGE = X_BYTES + T5_W_BYTES + T5_ZS_BYTES;
+    // KW = 1: each wave loads the zero words of its own 8 packed columns and
+    // the scales of its 64 columns (32 + 128 B); KW = 2: waves 0..2 load them
+    // for the whole tile.
+    static constexpr int ZS_BYTES = KW == 1 ? 4 * T5_ZS_WAVE : T5_ZS_BYTES;
+    static constexpr int STAGE = X_BYTES + T5_W_BYTES + ZS_BYTES;
     static constexpr int THREADS = 256 * KW;
     static constexpr int WAVES = 4 * KW;
     static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;   // dwordx4 loads per wave per stage (FM / 2)
     // Workgroups per CU: by registers (accumulators 4 * FM float4 per lane)
     // and by LDS (S stages).
     static constexpr int PER_CU_REG = KW == 2 ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
-    static constexpr int PER_CU_LDS = (160 * 1024) / (S * (X_BYTES + T5_W_BYTES + T5_ZS_BYTES) + 64);
+    static constexpr int PER_CU_LDS = (160 * 1024) / (S * STAGE + 64);
     static constexpr int PER_CU = PER_CU_REG < PER_CU_LDS ? PER_CU_REG : PER_CU_LDS;
     static constexpr int W_LOADS = T5_W_BYTES / 256 / WAVES;  // dword loads per wave per stage
-    // Loads a wave issues per stage, not counting the zero/scale load that
-    // waves 0..2 add (issued first, so a wait that leaves this many
-    // outstanding also covers it).
-    static constexpr int LOADS = X_LOADS + W_LOADS;
+    // Loads a wave issues per stage.  KW = 2 does not count the zero/scale
+    // load that waves 0..2 add (issued first, so a wait that leaves this many
+    // outstanding also covers it); KW = 1 counts its two.
+    static constexpr int LOADS = X_LOADS + W_LOADS + (KW == 1 ? 2 : 0);
 };
 }  // namespace
 
@@ -161,22 +172,40 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         const int q = (lane & 7) ^ (lane >> 3);
         x_voff[i] = m0 + r < a.M ? (uint32_t)(((size_t)(m0 + r) * a.K + 8 * q) * 2) : 0x80000000u;
     }
-    // Packed weights: load i of wave w fills 64-dword block B = W_LOADS w + i
-    // = ((h * 4 + kb) * 2 + ub) * 2 + jh: lane l brings row 32 h + 8 kb + 4 ub
-    // + l % 4 of packed column 16 jh + l / 4.
+    // Packed weights.  KW = 2: load i of wave w fills 64-dword block B =
+    // W_LOADS w + i = ((h * 4 + kb) * 2 + ub) * 2 + jh: lane l brings row
+    // 32 h + 8 kb + 4 ub + l % 4 of packed column 16 jh + l / 4.  KW = 1:
+    // wave w loads only its own packed columns 8 w .. 8 w + 7: load i = 4 h +
+    // kb fills block 8 w + i, lane l = 32 ub + 4 c + u bringing row 8 i + 4 ub
+    // + u of packed column 8 w + c (rows 32 h + 8 kb .. + 7 of a column are 8
+    // consecutive dwords).
     uint32_t w_voff[L::W_LOADS];
 #pragma unroll
     for (int i = 0; i < L::W_LOADS; ++i) {
-        const int B = L::W_LOADS * wave + i;
-        const int jh = B & 1, ub = (B >> 1) & 1, bk = (B >> 2) & 3, bh = B >> 4;
-        const int r = 32 * bh + 8 * bk + 4 * ub + (lane & 3);
-        const int jc = (n0 >> 3) + 16 * jh + (lane >> 2);
+        int r, jc;
+        if constexpr (KW == 1) {
+            r = 8 * i + 4 * (lane >> 5) + (lane & 3);
+            jc = (n0 >> 3) + 8 * wave + ((lane >> 2) & 7);
+        } else {
+            const int B = L::W_LOADS * wave + i;
+            const int jh = B & 1, ub = (B >> 1) & 1, bk = (B >> 2) & 3, bh = B >> 4;
+            r = 32 * bh + 8 * bk + 4 * ub + (lane & 3);
+            jc = (n0 >> 3) + 16 * jh + (lane >> 2);
+        }
         w_voff[i] = jc < pn ? (uint32_t)((r * pn + jc) * 4) : 0x80000000u;
     }
-    // Zero words (wave 0: lanes 0..31 useful, the rest repeat them into the
-    // padding) and scales (waves 1, 2: 128 columns each).
-    uint32_t zs_voff = 0x80000000u;
-    if (wave == 0) {
+    // Zero words and scales.  KW = 2: wave 0 loads the zero words (lanes
+    // 0..31 useful, the rest repeat them into the padding), waves 1, 2 the
+    // scales of 128 columns each.  KW = 1: every wave loads the zero words of
+    // its 8 packed columns (lanes 0..7) and the scales of its 64 columns
+    // (lanes 0..31); the other lanes are masked off and write nothing.
+    uint32_t zs_voff = 0x80000000u, s_voff = 0x80000000u;
+    if constexpr (KW == 1) {
+        const int jc = (n0 >> 3) + 8 * wave + (lane & 7);
+        zs_voff = jc < pn ? (uint32_t)jc * 4u : 0x80000000u;
+        const int c = n0 + 64 * wave + 2 * (lane & 31);
+        s_voff = c < a.N ? (uint32_t)c * 2u : 0x80000000u;
+    } else if (wave == 0) {
         const int jc = (n0 >> 3) + (lane & 31);
         zs_voff = jc < pn ? (uint32_t)jc * 4u : 0x80000000u;
     } else if (wave <= 2) {
@@ -188,7 +217,16 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         const uint32_t base = lds0 + (uint32_t)(stage * L::STAGE);
         const int k0 = k_begin + kt * T5_BK;
         const int g = k0 / kGroup;
-        if (wave == 0)
+        if constexpr (KW == 1) {
+            // Partial-wave loads: the lanes left out write no LDS (never all
+            // of them, so both loads issue and count in vmcnt).
+            const uint32_t zb = base + L::X_BYTES + T5_W_BYTES + (uint32_t)(T5_ZS_WAVE * wave);
+            if (lane < 8)
+                buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u), zb);
+            if (lane < 32)
+                buffer_load_lds_x1(rs, s_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
+                                   zb + 32u);
+        } else if (wave == 0)
             buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
                                base + L::X_BYTES + T5_W_BYTES);
         else if (wave <= 2)
@@ -217,11 +255,11 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
 #pragma unroll
         for (int f = 0; f < FM; ++f) acc[c][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // One k-step from stage memory `st`: per k-half, two 16-byte reads give
-    // the lane's 8 weight words, 4 A fragments are formed (the second nibble
-    // of a byte is masked in place and read with the 64.0 magic, so every
-    // column gives the exact q - z and one fp16 rounding of (q - z) * s), then
-    // the 8 B fragments of the wave's x rows, 4 MFMAs each.
+    // KW = 2, one k-step from stage memory `st`: two 16-byte reads give the
+    // lane's 8 weight words of its k-half, 4 A fragments are formed (the
+    // second nibble of a byte is masked in place and read with the 64.0
+    // magic, so every column gives the exact q - z and one fp16 rounding of
+    // (q - z) * s), then the FM B fragments of the wave's x rows, 4 MFMAs each.
     auto compute = [&](const unsigned char* st) {
         const half_t* xs = reinterpret_cast<const half_t*>(st);
         const uint32_t* ws = reinterpret_cast<const uint32_t*>(st + L::X_BYTES);
@@ -234,53 +272,191 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
             zsp[c] = zero_splat_inplace(zw, 4 * hh + c);
             ssp[c] = as_u32(half2_t{s4[c], s4[c]});
         }
+        const int h = kh;
+        const u32x4 w0 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 0) * 32 + jl) * 4]);
+        const u32x4 w1 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 1) * 32 + jl) * 4]);
+        const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+        u32x4 af[4];
 #pragma unroll
-        for (int hs = 0; hs < 3 - KW; ++hs) {
-            const int h = KW == 2 ? kh : hs;
-            const u32x4 w0 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 0) * 32 + jl) * 4]);
-            const u32x4 w1 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 1) * 32 + jl) * 4]);
-            const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-            u32x4 af[4];
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t ev = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_even);
+            const uint32_t od = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_odd);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t ev = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_even);
-                const uint32_t od = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_odd);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, c & 2 ? magic_hi : magic);
-                    af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
-                }
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, c & 2 ? magic_hi : magic);
+                af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
             }
+        }
 #pragma unroll
-            for (int f = 0; f < FM; ++f) {
-                const int r = 16 * f + n16;
-                const half8_t bf = *reinterpret_cast<const half8_t*>(&xs[r * T5_BK + 8 * ((4 * h + kb) ^ (r & 7))]);
+        for (int f = 0; f < FM; ++f) {
+            const int r = 16 * f + n16;
+            const half8_t bf = *reinterpret_cast<const half8_t*>(&xs[r * T5_BK + 8 * ((4 * h + kb) ^ (r & 7))]);
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, af[c]), bf, acc[c][f]);
-            }
+            for (int c = 0; c < 4; ++c)
+                acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, af[c]), bf, acc[c][f]);
         }
     };
 
-    if (KT > 0) {
-        // Prologue: steps 0 .. S - 2 in flight; wait for step 0.
+    if constexpr (KW == 2) {
+        if (KT > 0) {
+            // Prologue: steps 0 .. S - 2 in flight; wait for step 0.
 #pragma unroll
-        for (int j = 0; j < S - 1; ++j)
-            if (j < KT) issue(j, j);
-        wait_batches<L::LOADS, S - 2>(min(S - 2, KT - 1));
-        __syncthreads();
-        int stage = 0;
-        for (int kt = 0; kt < KT; ++kt) {
-            // Step kt + S - 1 into the stage step kt - 1 used (read before the
-            // previous barrier).
-            if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(smem + stage * L::STAGE);
-            // Step kt + 1's loads must have landed before the barrier; those
-            // of steps kt + 2 .. kt + S - 1 that were issued stay in flight.
-            wait_batches<L::LOADS, S - 2>(max(0, min(S - 2, KT - 2 - kt)));
+            for (int j = 0; j < S - 1; ++j)
+                if (j < KT) issue(j, j);
+            wait_batches<L::LOADS, S - 2>(min(S - 2, KT - 1));
             __syncthreads();
-            stage = stage == S - 1 ? 0 : stage + 1;
+            int stage = 0;
+            for (int kt = 0; kt < KT; ++kt) {
+                // Step kt + S - 1 into the stage step kt - 1 used (read before
+                // the previous barrier).
+                if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(smem + stage * L::STAGE);
+                // Step kt + 1's loads must have landed before the barrier;
+                // those of steps kt + 2 .. kt + S - 1 that were issued stay
+                // in flight.
+                wait_batches<L::LOADS, S - 2>(max(0, min(S - 2, KT - 2 - kt)));
+                __syncthreads();
+                stage = stage == S - 1 ? 0 : stage + 1;
+            }
+        }
+    } else {
+        // KW = 1, pipelined across k-steps.  Step kt runs in two phases of FM
+        // chunks; chunk f issues the 4 MFMAs of x rows 16 f .. + 15 against
+        // the phase's k-half, the read of the B fragment two chunks ahead,
+        // and a share of the dequantisation the next phase needs:
+        //   phase 0 (k-half 0): forms k-half 1's A fragments from weight
+        //     words already in registers;
+        //   phase 1 (k-half 1): reads step kt + 1's weight words, zero words
+        //     and scales and forms its k-half 0 A fragments.  The wave loaded
+        //     those itself, so its own vmcnt wait before the phase is all
+        //     they need.
+        // The dequantisation thus runs between the MFMAs of the same wave,
+        // and each B fragment has two chunks of MFMAs to land.  The barrier
+        // ending step kt publishes step kt + 1's x rows (every wave waited
+        // for its own loads of that step) and frees stage kt, which the loads
+        // of step kt + 3, issued after it, overwrite.
+        static_assert(S == 3, "two steps in flight");
+        const int c8 = n16 & 7;
+        // Stage byte offsets of the lane's reads: weight words of (k-half h,
+        // rows 4 ub .. + 3 of its 8) at w_rd + 1024 h + 128 ub; zero word and
+        // 4 scales at z_rd; B fragment of (h, rows 16 f ..) at x_rd[h] + 2048 f.
+        const uint32_t w_rd = (uint32_t)L::X_BYTES + 256u * (uint32_t)(8 * wn + kb) + 16u * (uint32_t)c8;
+        const uint32_t z_rd = (uint32_t)(L::X_BYTES + T5_W_BYTES + T5_ZS_WAVE * wn);
+        const uint32_t x_rd[2] = {128u * (uint32_t)n16 + 16u * (uint32_t)(kb ^ c8),
+                                  128u * (uint32_t)n16 + 16u * (uint32_t)((4 + kb) ^ c8)};
+        auto bfrag = [&](const unsigned char* st, int h, int f) {
+            return *reinterpret_cast<const half8_t*>(st + x_rd[h] + 2048 * f);
+        };
+        auto words = [&](const unsigned char* st, int h, int ub) {
+            return *reinterpret_cast<const u32x4*>(st + w_rd + 1024 * h + 128 * ub);
+        };
+        auto splats = [&](uint32_t zw, half4_t s4, uint32_t (&zsp)[4], uint32_t (&ssp)[4]) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                zsp[c] = zero_splat_inplace(zw, 4 * hh + c);
+                ssp[c] = as_u32(half2_t{s4[c], s4[c]});
+            }
+        };
+        // Dequantisation unit u (0 .. 7) of a k-half: word t = u / 2 of the
+        // A fragments of columns 2 (u % 2) and 2 (u % 2) + 1 (the second
+        // nibble of a byte masked in place and read with the 64.0 magic, so
+        // every column gives the exact q - z and one fp16 rounding of
+        // (q - z) * s).
+        uint32_t pe[4], po[4];
+        auto dq = [&](const u32x4 (&w)[2], const uint32_t (&zsp)[4], const uint32_t (&ssp)[4], u32x4 (&af)[4],
+                      int u) {
+            const int t = u >> 1, cp = u & 1;
+            if (cp == 0) {
+                const uint32_t lo = w[t >> 1][(2 * t) & 3], hi = w[t >> 1][(2 * t + 1) & 3];
+                pe[t] = __builtin_amdgcn_perm(hi, lo, sel_even);
+                po[t] = __builtin_amdgcn_perm(hi, lo, sel_odd);
+            }
+#pragma unroll
+            for (int c = 2 * cp; c < 2 * cp + 2; ++c) {
+                const uint32_t kp =
+                    and_or(c & 1 ? po[t] : pe[t], c & 2 ? 0x00F000F0u : 0x000F000Fu, c & 2 ? magic_hi : magic);
+                af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
+            }
+        };
+        // Phase 1 starts its dequantisation at chunk C0, once the weight
+        // words it read in chunk 0 have had time to land.
+        constexpr int C0 = FM >= 8 ? 2 : 1;
+        if (KT > 0) {
+            issue(0, 0);
+            if (KT > 1) issue(1, 1);
+            wait_batches<L::LOADS, 1>(min(1, KT - 1));
+            u32x4 wc[2];            // k-half 1 weight words of the current step
+            u32x4 afa[4], afb[4];   // A fragments of k-half 0 and 1
+            uint32_t zc[4], sc[4];  // zero and scale splats of the current step
+            {
+                const u32x4 w0[2] = {words(smem, 0, 0), words(smem, 0, 1)};
+                wc[0] = words(smem, 1, 0);
+                wc[1] = words(smem, 1, 1);
+                splats(*reinterpret_cast<const uint32_t*>(smem + z_rd + 4 * c8),
+                       *reinterpret_cast<const half4_t*>(smem + z_rd + 32 + 16 * c8 + 8 * hh), zc, sc);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) dq(w0, zc, sc, afa, u);
+            }
+            __syncthreads();
+            int stage = 0;
+            for (int kt = 0; kt < KT; ++kt) {
+                if (kt + 2 < KT) issue(kt + 2, stage == 0 ? 2 : stage - 1);
+                const unsigned char* st = smem + stage * L::STAGE;
+                const int nstage = stage == 2 ? 0 : stage + 1;
+                const unsigned char* sn = smem + nstage * L::STAGE;
+                half8_t bq[3];  // B fragment i (h = i / FM, rows 16 (i % FM) ..) in bq[i % 3]
+                __builtin_amdgcn_sched_barrier(0);
+                bq[0] = bfrag(st, 0, 0);
+                bq[1] = bfrag(st, 0, 1);
+#pragma unroll
+                for (int f = 0; f < FM; ++f) {
+                    const int i = f + 2;
+                    bq[i % 3] = bfrag(st, i / FM, i % FM);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, afa[c]), bq[f % 3], acc[c][f]);
+#pragma unroll
+                    for (int u = 8 * f / FM; u < 8 * (f + 1) / FM; ++u) dq(wc, zc, sc, afb, u);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // k-half 1's A fragments are formed here, under phase 0's
+                // MFMAs: the empty asm uses them, so the compiler cannot sink
+                // their dequantisation past the wait's branch into phase 1.
+#pragma unroll
+                for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(afb[c]));
+                // This wave's loads of step kt + 1 must have landed; those of
+                // step kt + 2 stay in flight.
+                wait_batches<L::LOADS, 1>(max(0, min(1, KT - 2 - kt)));
+                u32x4 wn0[2];
+                uint32_t zw_n = 0;
+                half4_t s4_n = {};
+#pragma unroll
+                for (int f = 0; f < FM; ++f) {
+                    const int i = FM + f + 2;
+                    if (i < 2 * FM) bq[i % 3] = bfrag(st, 1, i - FM);
+                    if (f == 0) {
+                        zw_n = *reinterpret_cast<const uint32_t*>(sn + z_rd + 4 * c8);
+                        s4_n = *reinterpret_cast<const half4_t*>(sn + z_rd + 32 + 16 * c8 + 8 * hh);
+                        wn0[0] = words(sn, 0, 0);
+                        wn0[1] = words(sn, 0, 1);
+                        wc[0] = words(sn, 1, 0);
+                        wc[1] = words(sn, 1, 1);
+                    }
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, afb[c]), bq[(FM + f) % 3], acc[c][f]);
+                    if (f == C0) splats(zw_n, s4_n, zc, sc);
+                    if (f >= C0) {
+#pragma unroll
+                        for (int u = 8 * (f - C0) / (FM - C0); u < 8 * (f - C0 + 1) / (FM - C0); ++u)
+                            dq(wn0, zc, sc, afa, u);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                __syncthreads();
+                stage = nstage;
+            }
         }
     }
 
