@@ -21,13 +21,13 @@ namespace awq {
 //     k-chunk p ^ (r & 7), so the MFMA fragment reads of 8 consecutive rows
 //     hit 8 distinct chunk positions (all banks once); rows beyond M read as
 //     zeros (buffer range check); a wave's dwordx4 load writes 8 rows.
-//   * packed weights, 64 rows x 32 packed columns.  KW = 1: 64-dword block
-//     8 w + 4 h + kb holds wave w's columns 8 w .. + 7, rows 32 h + 8 kb ..
-//     + 7 as dword 32 ub + 4 c + u = row 32 h + 8 kb + 4 ub + u of column
-//     8 w + c (each wave loads its own block with 8 dword loads).  KW = 2:
-//     dword ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h + 8 kb +
-//     4 ub + u of column j, one dword load covering 4 rows x 16 columns.
-//     Either way the lane that owns column j and rows 8 kb .. + 7 of half h
+//   * packed weights, 64 rows x 32 packed columns.  KW = 1: wave w's 2 KB
+//     holds its packed columns 8 w .. + 7 row-major (32 B a row, the two
+//     16-byte halves of row r swapped when bit 2 of r is set), loaded by two
+//     dwordx4 loads and read back column-wise with LDS transpose reads.
+//     KW = 2: dword ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h +
+//     8 kb + 4 ub + u of column j, one dword load covering 4 rows x 16
+//     columns, so the lane that owns column j and rows 8 kb .. + 7 of half h
 //     reads them as two 16-byte words.
 //   * the group's zero words and scales: KW = 1, per wave its 8 zero words
 //     and 64 scales (160 B); KW = 2, 32 zero words and 256 scales.
@@ -73,7 +73,9 @@ struct T5Layout {
     static constexpr int PER_CU_REG = KW == 2 ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
     static constexpr int PER_CU_LDS = (160 * 1024) / (S * STAGE + 64);
     static constexpr int PER_CU = PER_CU_REG < PER_CU_LDS ? PER_CU_REG : PER_CU_LDS;
-    static constexpr int W_LOADS = T5_W_BYTES / 256 / WAVES;  // dword loads per wave per stage
+    // Packed-weight loads per wave per stage: KW = 1, two dwordx4 (the
+    // wave's own 2 KB); KW = 2, dword loads sharing the stage's 8 KB.
+    static constexpr int W_LOADS = KW == 1 ? 2 : T5_W_BYTES / 256 / WAVES;
     // Loads a wave issues per stage.  KW = 2 does not count the zero/scale
     // load that waves 0..2 add (issued first, so a wait that leaves this many
     // outstanding also covers it); KW = 1 counts its two.
@@ -175,17 +177,18 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
     // Packed weights.  KW = 2: load i of wave w fills 64-dword block B =
     // W_LOADS w + i = ((h * 4 + kb) * 2 + ub) * 2 + jh: lane l brings row
     // 32 h + 8 kb + 4 ub + l % 4 of packed column 16 jh + l / 4.  KW = 1:
-    // wave w loads only its own packed columns 8 w .. 8 w + 7: load i = 4 h +
-    // kb fills block 8 w + i, lane l = 32 ub + 4 c + u bringing row 8 i + 4 ub
-    // + u of packed column 8 w + c (rows 32 h + 8 kb .. + 7 of a column are 8
-    // consecutive dwords).
+    // wave w loads only its own packed columns 8 w .. 8 w + 7, row-major
+    // (32 B a row): dwordx4 load i covers rows 32 i .. + 31, lane l bringing
+    // the 16-byte slot (l % 2) ^ sw(r) (packed columns 4 s .. + 3) of row
+    // r = 32 i + l / 2, sw(r) = bit 2 of r (slots swapped every 4 rows, so
+    // the transpose reads below meet fewer bank conflicts).
     uint32_t w_voff[L::W_LOADS];
 #pragma unroll
     for (int i = 0; i < L::W_LOADS; ++i) {
         int r, jc;
         if constexpr (KW == 1) {
-            r = 8 * i + 4 * (lane >> 5) + (lane & 3);
-            jc = (n0 >> 3) + 8 * wave + ((lane >> 2) & 7);
+            r = 32 * i + (lane >> 1);
+            jc = (n0 >> 3) + 8 * wave + 4 * ((lane & 1) ^ ((r >> 2) & 1));
         } else {
             const int B = L::W_LOADS * wave + i;
             const int jh = B & 1, ub = (B >> 1) & 1, bk = (B >> 2) & 3, bh = B >> 4;
@@ -237,9 +240,14 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
             buffer_load_lds_x4(rx, x_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * 2u),
                                base + 1024u * (uint32_t)(L::X_LOADS * wave + i));
 #pragma unroll
-        for (int i = 0; i < L::W_LOADS; ++i)
-            buffer_load_lds_x1(rw, w_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * (uint32_t)pn * 4u),
-                               base + L::X_BYTES + 256u * (uint32_t)(L::W_LOADS * wave + i));
+        for (int i = 0; i < L::W_LOADS; ++i) {
+            if constexpr (KW == 1)
+                buffer_load_lds_x4(rw, w_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * (uint32_t)pn * 4u),
+                                   base + L::X_BYTES + 2048u * (uint32_t)wave + 1024u * (uint32_t)i);
+            else
+                buffer_load_lds_x1(rw, w_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * (uint32_t)pn * 4u),
+                                   base + L::X_BYTES + 256u * (uint32_t)(L::W_LOADS * wave + i));
+        }
     };
 
     // v_perm selectors (byte 0x0C reads as zero).
@@ -326,77 +334,106 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         // the phase's k-half, the read of the B fragment two chunks ahead,
         // and a share of the dequantisation the next phase needs:
         //   phase 0 (k-half 0): forms k-half 1's A fragments from weight
-        //     words already in registers;
-        //   phase 1 (k-half 1): reads step kt + 1's weight words, zero words
-        //     and scales and forms its k-half 0 A fragments.  The wave loaded
-        //     those itself, so its own vmcnt wait before the phase is all
-        //     they need.
+        //     nibbles already in registers;
+        //   phase 1 (k-half 1): reads step kt + 1's weight nibbles, zero
+        //     words and scales and forms its k-half 0 A fragments.  The wave
+        //     loaded those itself, so its own vmcnt wait before the phase is
+        //     all they need.
         // The dequantisation thus runs between the MFMAs of the same wave,
         // and each B fragment has two chunks of MFMAs to land.  The barrier
         // ending step kt publishes step kt + 1's x rows (every wave waited
         // for its own loads of that step) and frees stage kt, which the loads
         // of step kt + 3, issued after it, overwrite.
+        //
+        // Weights reach the A fragments through transpose reads
+        // (ds_read_b64_tr_b4: within each 16-lane group, lane j receives
+        // nibble j of the 8-byte row slices the group's 16 lanes address).
+        // A fragment c (MFMA row n = lane % 16) is the 16-column chunk c of
+        // the wave's 64 columns: packed columns 2 c and 2 c + 1, nibble n of
+        // the 8-byte slice, i.e. logical column 8 (2 c + n / 8) +
+        // 2 (n % 4) + (n % 8) / 4 (the AWQ nibble order).  Lane 16 kb + p
+        // addresses row 32 (p / 8) + 8 kb + SIG(p % 8), SIG = 0 2 4 6 1 3 5 7,
+        // so of the 64 bits each lane receives, the low dword holds k-half
+        // 0's rows 8 kb .. + 7 in SIG order and the high dword k-half 1's:
+        // masking 0x000F000F then gives rows (8 kb, 8 kb + 1) in one half
+        // pair, 0x00F000F0 (the nibble in place, read with the 64.0 magic)
+        // rows + 2, + 3, and the same on the dword shifted by 8 rows + 4 ..
+        // + 7: the A fragment in k order, every column the exact q - z and
+        // one fp16 rounding of (q - z) * s.
         static_assert(S == 3, "two steps in flight");
+        const int sgi = n16 & 7;
+        const int tr_row = 32 * (n16 >> 3) + 8 * kb + 2 * (sgi & 3) + (sgi >> 2);
+        const int tr_sw = (tr_row >> 2) & 1;
+        // Stage byte offsets of the lane's reads: transpose slices of chunks
+        // 0, 1 at tr_lo + 8 c and 2, 3 at tr_hi + 8 (c - 2); B fragment of
+        // (k-half h, rows 16 f ..) at x_rd[h] + 2048 f; zero word of packed
+        // column 2 c + n16 / 8 at z_rd + 8 c; its scale at s_rd + 32 c.
+        const uint32_t w_rd = (uint32_t)L::X_BYTES + 2048u * (uint32_t)wn + 32u * (uint32_t)tr_row;
+        const uint32_t tr_lo = w_rd + 16u * (uint32_t)tr_sw;
+        const uint32_t tr_hi = w_rd + 16u * (uint32_t)(tr_sw ^ 1);
+        const uint32_t z_base = (uint32_t)(L::X_BYTES + T5_W_BYTES + T5_ZS_WAVE * wn);
+        const uint32_t z_rd = z_base + 4u * (uint32_t)(n16 >> 3);
+        const uint32_t s_rd = z_base + 32u + 16u * (uint32_t)(n16 >> 3) + 2u * (uint32_t)(2 * (sgi & 3) + (sgi >> 2));
+        const uint32_t zsh = 4u * (uint32_t)sgi;
         const int c8 = n16 & 7;
-        // Stage byte offsets of the lane's reads: weight words of (k-half h,
-        // rows 4 ub .. + 3 of its 8) at w_rd + 1024 h + 128 ub; zero word and
-        // 4 scales at z_rd; B fragment of (h, rows 16 f ..) at x_rd[h] + 2048 f.
-        const uint32_t w_rd = (uint32_t)L::X_BYTES + 256u * (uint32_t)(8 * wn + kb) + 16u * (uint32_t)c8;
-        const uint32_t z_rd = (uint32_t)(L::X_BYTES + T5_W_BYTES + T5_ZS_WAVE * wn);
         const uint32_t x_rd[2] = {128u * (uint32_t)n16 + 16u * (uint32_t)(kb ^ c8),
                                   128u * (uint32_t)n16 + 16u * (uint32_t)((4 + kb) ^ c8)};
         auto bfrag = [&](const unsigned char* st, int h, int f) {
             return *reinterpret_cast<const half8_t*>(st + x_rd[h] + 2048 * f);
         };
-        auto words = [&](const unsigned char* st, int h, int ub) {
-            return *reinterpret_cast<const u32x4*>(st + w_rd + 1024 * h + 128 * ub);
+        // The 64 transposed bits of chunk c: [0] k-half 0, [1] k-half 1.
+        auto trread = [&](const unsigned char* st, int c) {
+            typedef int v2i __attribute__((ext_vector_type(2)));
+            const unsigned char* ptr = st + (c < 2 ? tr_lo : tr_hi) + 8 * (c & 1);
+            const v2i v = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+                (__attribute__((address_space(3))) v2i*)(ptr));
+            return v;
         };
-        auto splats = [&](uint32_t zw, half4_t s4, uint32_t (&zsp)[4], uint32_t (&ssp)[4]) {
+        // Zero splats (1024 + z and, for the in-place nibbles, 64 + z) and
+        // the scale pair of the lane's column in each chunk.
+        auto splats = [&](const unsigned char* st, uint32_t (&zl)[4], uint32_t (&zh)[4], uint32_t (&ss)[4]) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                zsp[c] = zero_splat_inplace(zw, 4 * hh + c);
-                ssp[c] = as_u32(half2_t{s4[c], s4[c]});
+                const uint32_t zw = *reinterpret_cast<const uint32_t*>(st + z_rd + 8 * c);
+                const uint32_t sv = *reinterpret_cast<const uint16_t*>(st + s_rd + 32 * c);
+                const uint32_t z = __builtin_amdgcn_ubfe(zw, zsh, 4);
+                zl[c] = z * 0x00010001u + kMagic2;
+                zh[c] = z * 0x00100010u + kMagic2Hi;
+                ss[c] = sv | (sv << 16);
             }
         };
-        // Dequantisation unit u (0 .. 7) of a k-half: word t = u / 2 of the
-        // A fragments of columns 2 (u % 2) and 2 (u % 2) + 1 (the second
-        // nibble of a byte masked in place and read with the 64.0 magic, so
-        // every column gives the exact q - z and one fp16 rounding of
-        // (q - z) * s).
-        uint32_t pe[4], po[4];
-        auto dq = [&](const u32x4 (&w)[2], const uint32_t (&zsp)[4], const uint32_t (&ssp)[4], u32x4 (&af)[4],
-                      int u) {
-            const int t = u >> 1, cp = u & 1;
-            if (cp == 0) {
-                const uint32_t lo = w[t >> 1][(2 * t) & 3], hi = w[t >> 1][(2 * t + 1) & 3];
-                pe[t] = __builtin_amdgcn_perm(hi, lo, sel_even);
-                po[t] = __builtin_amdgcn_perm(hi, lo, sel_odd);
-            }
-#pragma unroll
-            for (int c = 2 * cp; c < 2 * cp + 2; ++c) {
-                const uint32_t kp =
-                    and_or(c & 1 ? po[t] : pe[t], c & 2 ? 0x00F000F0u : 0x000F000Fu, c & 2 ? magic_hi : magic);
-                af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
-            }
+        // Dequantisation unit u (0 .. 7) of a k-half: chunk c = u / 2, words
+        // 2 (u % 2) and 2 (u % 2) + 1 of its A fragment, from the chunk's
+        // transposed dword d of that k-half.
+        auto dq = [&](const uint32_t (&d)[4], const uint32_t (&zl)[4], const uint32_t (&zh)[4],
+                      const uint32_t (&ss)[4], u32x4 (&af)[4], int u) {
+            const int c = u >> 1, part = u & 1;
+            const uint32_t v = part ? d[c] >> 8 : d[c];
+            const uint32_t lo = and_or(v, 0x000F000Fu, magic), hi = and_or(v, 0x00F000F0u, magic_hi);
+            af[c][2 * part] = as_u32((as_h2(lo) - as_h2(zl[c])) * as_h2(ss[c]));
+            af[c][2 * part + 1] = as_u32((as_h2(hi) - as_h2(zh[c])) * as_h2(ss[c]));
         };
-        // Phase 1 starts its dequantisation at chunk C0, once the weight
-        // words it read in chunk 0 have had time to land.
+        // Phase 1 starts its dequantisation at chunk C0, once the reads it
+        // issued in chunk 0 have had time to land.
         constexpr int C0 = FM >= 8 ? 2 : 1;
         if (KT > 0) {
             issue(0, 0);
             if (KT > 1) issue(1, 1);
             wait_batches<L::LOADS, 1>(min(1, KT - 1));
-            u32x4 wc[2];            // k-half 1 weight words of the current step
-            u32x4 afa[4], afb[4];   // A fragments of k-half 0 and 1
-            uint32_t zc[4], sc[4];  // zero and scale splats of the current step
+            uint32_t d1[4];                  // k-half 1 nibbles of the current step
+            u32x4 afa[4], afb[4];            // A fragments of k-half 0 and 1
+            uint32_t zl[4], zh[4], ss[4];    // splats of the current step's group
             {
-                const u32x4 w0[2] = {words(smem, 0, 0), words(smem, 0, 1)};
-                wc[0] = words(smem, 1, 0);
-                wc[1] = words(smem, 1, 1);
-                splats(*reinterpret_cast<const uint32_t*>(smem + z_rd + 4 * c8),
-                       *reinterpret_cast<const half4_t*>(smem + z_rd + 32 + 16 * c8 + 8 * hh), zc, sc);
+                uint32_t d0[4];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) dq(w0, zc, sc, afa, u);
+                for (int c = 0; c < 4; ++c) {
+                    const auto v = trread(smem, c);
+                    d0[c] = (uint32_t)v[0];
+                    d1[c] = (uint32_t)v[1];
+                }
+                splats(smem, zl, zh, ss);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) dq(d0, zl, zh, ss, afa, u);
             }
             __syncthreads();
             int stage = 0;
@@ -417,7 +454,7 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
                     for (int c = 0; c < 4; ++c)
                         acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, afa[c]), bq[f % 3], acc[c][f]);
 #pragma unroll
-                    for (int u = 8 * f / FM; u < 8 * (f + 1) / FM; ++u) dq(wc, zc, sc, afb, u);
+                    for (int u = 8 * f / FM; u < 8 * (f + 1) / FM; ++u) dq(d1, zl, zh, ss, afb, u);
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // k-half 1's A fragments are formed here, under phase 0's
@@ -428,29 +465,27 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
                 // This wave's loads of step kt + 1 must have landed; those of
                 // step kt + 2 stay in flight.
                 wait_batches<L::LOADS, 1>(max(0, min(1, KT - 2 - kt)));
-                u32x4 wn0[2];
-                uint32_t zw_n = 0;
-                half4_t s4_n = {};
+                uint32_t d0[4];
 #pragma unroll
                 for (int f = 0; f < FM; ++f) {
                     const int i = FM + f + 2;
                     if (i < 2 * FM) bq[i % 3] = bfrag(st, 1, i - FM);
                     if (f == 0) {
-                        zw_n = *reinterpret_cast<const uint32_t*>(sn + z_rd + 4 * c8);
-                        s4_n = *reinterpret_cast<const half4_t*>(sn + z_rd + 32 + 16 * c8 + 8 * hh);
-                        wn0[0] = words(sn, 0, 0);
-                        wn0[1] = words(sn, 0, 1);
-                        wc[0] = words(sn, 1, 0);
-                        wc[1] = words(sn, 1, 1);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const auto v = trread(sn, c);
+                            d0[c] = (uint32_t)v[0];
+                            d1[c] = (uint32_t)v[1];
+                        }
                     }
 #pragma unroll
                     for (int c = 0; c < 4; ++c)
                         acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, afb[c]), bq[(FM + f) % 3], acc[c][f]);
-                    if (f == C0) splats(zw_n, s4_n, zc, sc);
+                    if (f == C0) splats(sn, zl, zh, ss);
                     if (f >= C0) {
 #pragma unroll
                         for (int u = 8 * (f - C0) / (FM - C0); u < 8 * (f - C0 + 1) / (FM - C0); ++u)
-                            dq(wn0, zc, sc, afa, u);
+                            dq(d0, zl, zh, ss, afa, u);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -484,9 +519,35 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         }
     }
 
-    // acc[c][f] lane value r: out[m0 + 16 f + n16][8 (n0/8 + 8 wn + 4 (kb & 1) + r) + 4 (kb >> 1) + c].
-    const int pc0 = (n0 >> 3) + 8 * wn + 4 * (kb & 1);
-    const int coff = 4 * (kb >> 1);
+    // Output quads: each lane holds, for every 16-row block f, four quads of
+    // 4 consecutive columns (tile row 16 f + n16).  KW = 2: quad q is lane
+    // value q of acc[0..3][f], columns 64 wn + 32 (kb & 1) + 8 q + 4 (kb >> 1)
+    // .. + 3.  KW = 1: acc[c][f] lane value r is column 64 wn + 16 c +
+    // 8 (kb >> 1) + 2 r + (kb & 1) (the transposed fragments); lanes l and
+    // l ^ 16 trade two values so that acc[c][f] holds columns 64 wn + 16 c +
+    // 8 (kb >> 1) + 4 (kb & 1) .. + 3, quad c.
+    if constexpr (KW == 1) {
+        const bool odd = kb & 1;
+        const int src = (lane ^ 16) << 2;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int f = 0; f < FM; ++f) {
+                const floatx4 v = acc[c][f];
+                const float r0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(odd ? v[0] : v[2])));
+                const float r1 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(odd ? v[1] : v[3])));
+                acc[c][f] = odd ? floatx4{r0, v[2], r1, v[3]} : floatx4{v[0], r0, v[1], r1};
+            }
+    }
+    auto quad = [&](int f, int q, int& col) {
+        if constexpr (KW == 1) {
+            col = 64 * wn + 16 * q + 8 * (kb >> 1) + 4 * (kb & 1);
+            return acc[q][f];
+        } else {
+            col = 64 * wn + 32 * (kb & 1) + 8 * q + 4 * (kb >> 1);
+            return floatx4{acc[0][f][q], acc[1][f][q], acc[2][f][q], acc[3][f][q]};
+        }
+    };
     if (ks == 1) {
         if (kh != 0) return;  // KW = 2: the sums are in waves 0..3
 #pragma unroll
@@ -494,10 +555,12 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
             const int m = m0 + 16 * f + n16;
             if (m >= a.M) continue;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (pc0 + r >= pn) continue;
-                const float v[4] = {acc[0][f][r], acc[1][f][r], acc[2][f][r], acc[3][f][r]};
-                store_out<4>(a.out, a.bias, a.residual, a.N, m, 8 * (pc0 + r) + coff, v);
+            for (int q = 0; q < 4; ++q) {
+                int col;
+                const floatx4 v4 = quad(f, q, col);
+                if (n0 + col >= a.N) continue;
+                const float v[4] = {v4[0], v4[1], v4[2], v4[3]};
+                store_out<4>(a.out, a.bias, a.residual, a.N, m, n0 + col, v);
             }
         }
         return;
@@ -516,11 +579,13 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         const int m = m0 + 16 * f + n16;
         if (m >= a.M || kh != 0) continue;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (pc0 + r >= pn) continue;
-            const uint32_t off = pl.base + (uint32_t)(16 * f + n16) * pl.row_stride +
-                                 (uint32_t)(8 * (pc0 + r) + coff - n0) * 4u + (uint32_t)split * pl.split_stride;
-            buf_store_f4_device(floatx4{acc[0][f][r], acc[1][f][r], acc[2][f][r], acc[3][f][r]}, rp_, off);
+        for (int q = 0; q < 4; ++q) {
+            int col;
+            const floatx4 v4 = quad(f, q, col);
+            if (n0 + col >= a.N) continue;
+            const uint32_t off = pl.base + (uint32_t)(16 * f + n16) * pl.row_stride + (uint32_t)col * 4u +
+                                 (uint32_t)split * pl.split_stride;
+            buf_store_f4_device(v4, rp_, off);
         }
     }
     if constexpr (FIN == 1) return;
