@@ -80,6 +80,13 @@ struct T5Layout {
     // load that waves 0..2 add (issued first, so a wait that leaves this many
     // outstanding also covers it); KW = 1 counts its two.
     static constexpr int LOADS = X_LOADS + W_LOADS + (KW == 1 ? 2 : 0);
+    // KW = 1: the loads of an odd k-step, which brings no zero words or
+    // scales (the two k-steps of a 128-row group share them).
+    static constexpr int LOADS_NZ = X_LOADS + W_LOADS;
+};
+template <bool B>
+struct Parity {
+    static constexpr bool value = B;
 };
 }  // namespace
 
@@ -221,14 +228,20 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         const int k0 = k_begin + kt * T5_BK;
         const int g = k0 / kGroup;
         if constexpr (KW == 1) {
-            // Partial-wave loads: the lanes left out write no LDS (never all
-            // of them, so both loads issue and count in vmcnt).
-            const uint32_t zb = base + L::X_BYTES + T5_W_BYTES + (uint32_t)(T5_ZS_WAVE * wave);
-            if (lane < 8)
-                buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u), zb);
-            if (lane < 32)
-                buffer_load_lds_x1(rs, s_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
-                                   zb + 32u);
+            // Zero words and scales with the first k-step of each group
+            // only (k-steps are 64 rows, groups 128, and every K range
+            // starts on a group).  Partial-wave loads: the lanes left out
+            // write no LDS (never all of them, so both loads issue and count
+            // in vmcnt).
+            if ((kt & 1) == 0) {
+                const uint32_t zb = base + L::X_BYTES + T5_W_BYTES + (uint32_t)(T5_ZS_WAVE * wave);
+                if (lane < 8)
+                    buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
+                                       zb);
+                if (lane < 32)
+                    buffer_load_lds_x1(rs, s_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
+                                       zb + 32u);
+            }
         } else if (wave == 0)
             buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
                                base + L::X_BYTES + T5_W_BYTES);
@@ -241,8 +254,9 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
                                base + 1024u * (uint32_t)(L::X_LOADS * wave + i));
 #pragma unroll
         for (int i = 0; i < L::W_LOADS; ++i) {
-            if constexpr (KW == 1)
-                buffer_load_lds_x4(rw, w_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * (uint32_t)pn * 4u),
+            if constexpr (KW == 1)  // load 1: the rows 32 below load 0's, through the scalar offset
+                buffer_load_lds_x4(rw, w_voff[0],
+                                   __builtin_amdgcn_readfirstlane((uint32_t)(k0 + 32 * i) * (uint32_t)pn * 4u),
                                    base + L::X_BYTES + 2048u * (uint32_t)wave + 1024u * (uint32_t)i);
             else
                 buffer_load_lds_x1(rw, w_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * (uint32_t)pn * 4u),
@@ -416,10 +430,13 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         // Phase 1 starts its dequantisation at chunk C0, once the reads it
         // issued in chunk 0 have had time to land.
         constexpr int C0 = FM >= 8 ? 2 : 1;
+        // KT is even (whole groups), so steps come in (even, odd) pairs: the
+        // even step's loads bring the group's zero words and scales, and the
+        // odd step's phase 1 forms the next group's splats.
         if (KT > 0) {
             issue(0, 0);
             if (KT > 1) issue(1, 1);
-            wait_batches<L::LOADS, 1>(min(1, KT - 1));
+            wait_batches<L::LOADS_NZ, 1>(min(1, KT - 1));
             uint32_t d1[4];                  // k-half 1 nibbles of the current step
             u32x4 afa[4], afb[4];            // A fragments of k-half 0 and 1
             uint32_t zl[4], zh[4], ss[4];    // splats of the current step's group
@@ -437,7 +454,8 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
             }
             __syncthreads();
             int stage = 0;
-            for (int kt = 0; kt < KT; ++kt) {
+            auto step = [&](int kt, auto odd_c) {
+                constexpr bool ODD = decltype(odd_c)::value;
                 if (kt + 2 < KT) issue(kt + 2, stage == 0 ? 2 : stage - 1);
                 const unsigned char* st = smem + stage * L::STAGE;
                 const int nstage = stage == 2 ? 0 : stage + 1;
@@ -463,8 +481,9 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
 #pragma unroll
                 for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(afb[c]));
                 // This wave's loads of step kt + 1 must have landed; those of
-                // step kt + 2 stay in flight.
-                wait_batches<L::LOADS, 1>(max(0, min(1, KT - 2 - kt)));
+                // step kt + 2 (an even step's with the zero words and scales)
+                // stay in flight.
+                wait_batches<ODD ? L::LOADS_NZ : L::LOADS, 1>(max(0, min(1, KT - 2 - kt)));
                 uint32_t d0[4];
 #pragma unroll
                 for (int f = 0; f < FM; ++f) {
@@ -481,7 +500,9 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
 #pragma unroll
                     for (int c = 0; c < 4; ++c)
                         acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, afb[c]), bq[(FM + f) % 3], acc[c][f]);
-                    if (f == C0) splats(sn, zl, zh, ss);
+                    if constexpr (ODD) {
+                        if (f == C0) splats(sn, zl, zh, ss);  // step kt + 1 starts a group
+                    }
                     if (f >= C0) {
 #pragma unroll
                         for (int u = 8 * (f - C0) / (FM - C0); u < 8 * (f - C0 + 1) / (FM - C0); ++u)
@@ -489,8 +510,16 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
+                // Likewise step kt + 1's k-half 0 fragments, formed under
+                // phase 1's MFMAs, not after the barrier.
+#pragma unroll
+                for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(afa[c]));
                 __syncthreads();
                 stage = nstage;
+            };
+            for (int kt = 0; kt < KT; kt += 2) {
+                step(kt, Parity<false>{});
+                step(kt + 1, Parity<true>{});
             }
         }
     }
