@@ -408,51 +408,22 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
 
 // Register-dequant tile variants (tile rows, workgroups per CU, a lone
 // workgroup's time per k-step in microseconds, slowdown per further
-// workgroup on the CU, finish: 1 reduce launch / 0 last arriver).  Variants
-// 10 .. 12 pair a second wave per SIMD from the same workgroup (k-halves),
-// so a lone workgroup's step is shorter.
+// workgroup on the CU, finish: 1 reduce launch / 0 last arriver).  Only the
+// one-wave-per-SIMD tiles with the reduce finish: variant 7 computes exactly
+// what variant 6 does and measured 1 - 5 % faster at every split (split 1
+// included), and the k-half pair tiles (10 - 12) were slower than these on
+// every measured shape.
 struct TileModel {
     int variant, rows, per_cu;
     double t1, eta;
     int reduce;
 };
 constexpr TileModel kTileModels[] = {
-    {6, 128, 2, 1.212, 0.224, 0}, {7, 128, 2, 1.212, 0.224, 1}, {8, 64, 3, 0.958, 0.236, 1},
-    {9, 32, 4, 0.712, 0.294, 1},  {10, 128, 1, 0.967, 0.0, 0},  {11, 128, 1, 0.967, 0.0, 1},
-    {12, 64, 1, 0.736, 0.0, 1},
+    {7, 128, 2, 0.920, 0.243, 1},
+    {8, 64, 3, 0.896, 0.073, 1},
+    {9, 32, 4, 0.768, 0.219, 1},
 };
 
-// Predicted time (microseconds) of a tile plan: a workgroup alone on its CU
-// takes t1 per k-step (its waves expose their own latency: LDS, dependent
-// VALU, barrier); each further workgroup on the CU slows every step by eta;
-// the grid runs in rounds of per_cu x CUs slots; a fixed launch, prologue
-// and epilogue cost; the reduce launch moves split x M x N x 8 bytes
-// (partials written, read, cleared).  The constants were fitted so that the
-// model's choice is fast, not its absolute times: on the four Qwen2-7B GEMMs
-// at M = 24 .. 1024 (576 timings of variants 6 - 12 and 1 - 28 splits; MI355X,
-// random operands, warm clocks) its picks are on average 1.2 % (at worst
-// 9 %) slower than the best measured configuration.
-double tile_cost(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
-    const int64_t wg = tile_tiles((int)M, (int)N, t.variant) * split;
-    const int64_t slots = (int64_t)t.per_cu * cus();
-    const int64_t steps = 2 * ((K / kGroup + split - 1) / split);
-    const int64_t rounds = (wg + slots - 1) / slots;
-    const double c = (double)(wg < slots ? wg : slots) / (double)cus();
-    const double share = 1.0 + t.eta * (c - 1.0);
-    double time = 7.54 + (double)rounds * (double)steps * t.t1 * (share > 1.0 ? share : 1.0);
-    if (split > 1) time += 0.14 + (double)split * (double)M * (double)N * 8.0 / 2.07e6;
-    return time;
-}
-
-// M <= 1024 with variant 6's grid under two workgroups per CU: the variant
-// and split count of least tile_cost (last-arriver variants unsplit only;
-// split no further than 7/4 workgroups per CU).  Above M = 1024: the least
-// busiest-CU time among variant 6 (split-K up to one pass over its 2 * CUs
-// slots, at least 4096 rows of K per split), the 64-row tile and the k-half
-// pair tile (variant 10), or a hybrid (below).  Else (gate||up at M >= 512:
-// variant 6's grid covers two workgroups per CU) variant 6.
-// Measured on the Qwen2-7B prefill GEMMs (qkv, o, gate||up, down) at
-// M = 32 .. 2048.
 // 5 <= M <= 16 on weights the stream path does not take (narrow and
 // shallow: fewer than 16 strips of 512 columns, K < 8192): the 32-row
 // register-dequant tile (variant 9) split 14 ways along K (in whole 128-row
@@ -472,35 +443,35 @@ int small_m_tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return AWQ_OK;
 }
 
-// The same model priced for the CU that holds the most workgroups: the grid
-// runs in rounds of per_cu x CUs workgroup slots, every full round puts
-// per_cu workgroups on each CU, the last one ceil(rest / CUs) on the
-// busiest, and a round costs steps x t1 x (1 + eta (c - 1)) for that CU.
-// tile_cost averages c over the CUs, which fits M <= 1024; above, the
-// busiest CU sets the time: the Qwen2-7B qkv GEMM (3584 x 4608) at M = 2048 /
-// 4096 ran 95.9 / 157 us with the 64-row tile (variant 8: 576 / 1152
-// workgroups, three per CU) against 102 / 175 for variant 6, as this
-// predicts and the average does not, while variant 6 stays the choice for
-// the other three GEMMs (measured best at M = 2048 and 4096).
+// Predicted time (microseconds) of a tile plan, priced for the CU that
+// holds the most workgroups: the grid runs in rounds of per_cu x CUs
+// workgroup slots, every full round puts per_cu workgroups on each CU, the
+// last one ceil(rest / CUs) on the busiest; a round costs steps x t1 x
+// (1 + eta (c - 1)) for a CU holding c workgroups (a workgroup alone takes
+// t1 per k-step: its waves expose their own latency); a fixed launch,
+// prologue and epilogue cost; the reduce launch moves split x M x N x 8
+// bytes (partials written, read, cleared).  Constants fitted so that the
+// model's choice is fast, not its absolute times: over 3800 timings of
+// variants 6 - 14 x 1 - 28 splits on the four Qwen2-7B GEMMs at M = 24 ..
+// 4096 (MI355X, random operands) its picks are on average 1.3 % (at worst
+// 10 %) slower than the best measured configuration.
 double tile_cost_busiest(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
     const int64_t wg = tile_tiles((int)M, (int)N, t.variant) * split;
     const int64_t slots = (int64_t)t.per_cu * cus();
     const int64_t steps = 2 * ((K / kGroup + split - 1) / split);
     const int64_t full = wg / slots, rest = wg % slots;
     const int64_t c_last = (rest + cus() - 1) / cus();
-    double time = 7.54 + (double)full * (double)steps * t.t1 * (1.0 + t.eta * (double)(t.per_cu - 1));
+    double time = 8.94 + (double)full * (double)steps * t.t1 * (1.0 + t.eta * (double)(t.per_cu - 1));
     if (rest > 0) time += (double)steps * t.t1 * (1.0 + t.eta * (double)(c_last - 1));
-    if (split > 1) time += 0.14 + (double)split * (double)M * (double)N * 8.0 / 2.07e6;
+    if (split > 1) time += 0.14 + (double)split * (double)M * (double)N * 8.0 / 3.31e6;
     return time;
 }
 
 // Busiest-CU time of a hybrid plan (variants 13, 14 with the constants of
-// variants 6, 8): `full` whole tiles on every CU, and on L x split CUs one
+// variants 7, 8): `full` whole tiles on every CU, and on L x split CUs one
 // piece of a leftover tile (ceil(groups / split) groups) beside them, whose
 // partials (split x L x rows x 256 x 4 bytes) are added by the pieces' last
-// arrivers while the whole tiles still run -- priced at 2.6 TB/s, which puts
-// the best split of the Qwen2-7B qkv GEMM at M = 2048 where it measured
-// (three: 86.0 us, against 89.5 and 88.3 for two and four).
+// arrivers while the whole tiles still run.
 double tile_cost_hybrid(const TileModel& t, int64_t M, int64_t N, int64_t K, int64_t split) {
     const int64_t tiles = tile_tiles((int)M, (int)N, t.variant);
     const int64_t full = tiles / cus();
@@ -510,7 +481,7 @@ double tile_cost_hybrid(const TileModel& t, int64_t M, int64_t N, int64_t K, int
     const int64_t sk_steps = 2 * ((groups + split - 1) / split);
     return 7.54 + (double)sk_steps * t.t1 * (1.0 + t.eta * (double)full) +
            (double)(steps - sk_steps) * t.t1 * (1.0 + t.eta * (double)(full - 1)) +
-           (double)split * (double)left * (double)t.rows * 256.0 * 4.0 / 2.6e6;
+           (double)split * (double)left * (double)t.rows * 256.0 * 4.0 / 4.56e6;
 }
 
 const TileModel* tile_model(int variant) {
@@ -519,90 +490,50 @@ const TileModel* tile_model(int variant) {
     return nullptr;
 }
 
+// The tile plan of least busiest-CU time over variants 7, 8, 9 and 1 - 32
+// splits (a split grid at most two workgroups per CU).  Where that choice is
+// unsplit and M >= 512, the hybrid of least predicted time instead: an
+// unsplit grid leaves CUs idle or some CUs a whole tile more than others.
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    const int64_t tiles6 = tile_tiles((int)M, (int)N, 6);
-    if (M <= 1024 && tiles6 < 2 * cus()) {
-        const int64_t groups = K / kGroup;
-        double best = 0.0;
-        int64_t best_v = 0, best_s = 0;
-        for (const TileModel& t : kTileModels) {
-            // On deep weights (K >= 8192) the 32-row tile measured slower than
-            // the model predicts above 24 rows (18944 x 3584 at M = 32: 30.3 us
-            // against 26.4 for the 64-row pair tile).
-            if (t.variant == 9 && M > 24 && K >= 8192) continue;
-            for (int64_t sp = 1; sp <= groups && sp <= 32; ++sp) {
-                if (!t.reduce && sp > 1) break;
-                awq_w4a16_plan q;
-                if (fill_tile(M, N, K, t.variant, sp, &q) != AWQ_OK) continue;
-                // Splitting beyond 7/4 workgroups per CU never measured faster.
-                if (sp > 1 && q.grid * 4 > 7 * cus()) continue;
-                const double time = tile_cost(t, M, N, K, sp);
-                if (best_v == 0 || time < best) {
-                    best = time;
-                    best_v = t.variant;
-                    best_s = sp;
-                }
-            }
-        }
-        if (best_v != 0 && fill_tile(M, N, K, best_v, best_s, p) == AWQ_OK) return AWQ_OK;
-    }
-    int64_t split6 = 1;
-    if (tiles6 > 0 && tiles6 < 2 * cus() && tiles6 * 4 <= (int64_t)kCounterBytes) {
-        split6 = (2 * cus()) / tiles6;
-        const int64_t max_split = K / 4096;
-        if (split6 > max_split) split6 = max_split;
-        if (split6 < 1) split6 = 1;
-        const int64_t units = K / kGroup;
-        const int64_t per = (units + split6 - 1) / split6;
-        split6 = (units + per - 1) / per;
-    }
-    if (M > 1024) {
-        // Variant 6 (split as above), the 64-row tile or the 128-row k-half
-        // pair tile, unsplit: the least busiest-CU time.
-        const int64_t cand[3][2] = {{6, split6}, {8, 1}, {10, 1}};
-        double best = 0.0;
-        int best_i = -1;
-        for (int i = 0; i < 3; ++i) {
+    const int64_t groups = K / kGroup;
+    double best = 0.0;
+    int64_t best_v = 0, best_s = 0;
+    for (const TileModel& t : kTileModels) {
+        // On deep weights (K >= 8192) the 32-row tile measured slower than
+        // the model predicts above 24 rows.
+        if (t.variant == 9 && M > 24 && K >= 8192) continue;
+        for (int64_t sp = 1; sp <= groups && sp <= 32; ++sp) {
             awq_w4a16_plan q;
-            const TileModel* t = tile_model((int)cand[i][0]);
-            if (t == nullptr || fill_tile(M, N, K, cand[i][0], cand[i][1], &q) != AWQ_OK) continue;
-            const double time = tile_cost_busiest(*t, M, N, K, cand[i][1]);
-            if (best_i < 0 || time < best) {
+            if (fill_tile(M, N, K, t.variant, sp, &q) != AWQ_OK) continue;
+            if (sp > 1 && q.grid > 2 * (int64_t)cus()) continue;
+            const double time = tile_cost_busiest(t, M, N, K, sp);
+            if (best_v == 0 || time < best) {
                 best = time;
-                best_i = i;
+                best_v = t.variant;
+                best_s = sp;
             }
         }
-        // An unsplit choice leaves CUs idle or some CUs a whole tile more
-        // than others; where a hybrid plan exists, the hybrid of least
-        // predicted time instead.  Measured against the unsplit plans on the
-        // Qwen2-7B GEMMs at M = 1025 - 3072: 3 - 16 % faster on every shape
-        // where it applies (qkv M = 2048: 88.5 against 98.3 us; o M = 2560:
-        // 87.1 against 97.1; down M = 2560: 396 against 471).  Against
-        // variant 6 split along a deep K (down at M = 1280, 1536) it lost
-        // 22 - 24 %, hence unsplit choices only.
-        if (best_i >= 0 && cand[best_i][1] == 1) {
-            double hbest = 0.0;
-            int64_t hv = 0, hs = 0;
-            for (int64_t v = 13; v <= 14; ++v) {
-                const TileModel* t = tile_model(v == 13 ? 6 : 8);
-                for (int64_t sp = 2; sp <= 8; ++sp) {
-                    awq_w4a16_plan q;
-                    if (t == nullptr || fill_tile(M, N, K, v, sp, &q) != AWQ_OK) continue;
-                    const double time = tile_cost_hybrid(*t, M, N, K, sp);
-                    if (hv == 0 || time < hbest) {
-                        hbest = time;
-                        hv = v;
-                        hs = sp;
-                    }
+    }
+    if (best_v != 0 && best_s == 1 && M >= 512) {
+        double hbest = 0.0;
+        int64_t hv = 0, hs = 0;
+        for (int64_t v = 13; v <= 14; ++v) {
+            const TileModel* t = tile_model(v == 13 ? 7 : 8);
+            for (int64_t sp = 2; sp <= 8; ++sp) {
+                awq_w4a16_plan q;
+                if (t == nullptr || fill_tile(M, N, K, v, sp, &q) != AWQ_OK) continue;
+                const double time = tile_cost_hybrid(*t, M, N, K, sp);
+                if (hv == 0 || time < hbest) {
+                    hbest = time;
+                    hv = v;
+                    hs = sp;
                 }
             }
-            if (hv != 0 && fill_tile(M, N, K, hv, hs, p) == AWQ_OK) return AWQ_OK;
         }
-        if (best_i >= 0 && fill_tile(M, N, K, cand[best_i][0], cand[best_i][1], p) == AWQ_OK) return AWQ_OK;
+        if (hv != 0 && fill_tile(M, N, K, hv, hs, p) == AWQ_OK) return AWQ_OK;
     }
-    if (tiles6 * split6 >= cus() && fill_tile(M, N, K, 6, split6, p) == AWQ_OK) return AWQ_OK;
-    if (tiles6 <= cus() && fill_tile(M, N, K, 10, 1, p) == AWQ_OK) return AWQ_OK;
-    return fill_tile(M, N, K, 6, 1, p);
+    if (best_v != 0 && fill_tile(M, N, K, best_v, best_s, p) == AWQ_OK) return AWQ_OK;
+    return fill_tile(M, N, K, 7, 1, p);
 }
 
 // Checks a caller-supplied plan against the shape: it must be exactly what
@@ -748,7 +679,7 @@ int noalloc_plan(int64_t M, int64_t N, int64_t K, int32_t group_size, awq_w4a16_
     }
     // A hybrid needs two splits at least; its unsplit tile needs no workspace.
     awq_w4a16_plan q;
-    if (tile_hybrid(p->variant) && fill_tile(M, N, K, p->variant == 13 ? 6 : 8, 1, &q) == AWQ_OK) {
+    if (tile_hybrid(p->variant) && fill_tile(M, N, K, p->variant == 13 ? 7 : 8, 1, &q) == AWQ_OK) {
         *p = q;
         return AWQ_OK;
     }
