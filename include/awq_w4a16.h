@@ -120,24 +120,23 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
                           int32_t rows_per_wave, int32_t k_waves, int32_t variant,
                           int32_t factored_scale, awq_w4a16_plan* plan);
 
-/* Host-only: a tile-path plan.  Variant 6: 128x256x64 tiles (four wavefronts, two
- * workgroups per CU), each wavefront 128 x rows x 64 columns, weights
- * dequantised straight into MFMA operand registers, x, raw weights and
- * zeros/scales brought by direct global->LDS loads two k-steps ahead into a
- * 3-stage ring; variants 7, 8, 9: 128-, 64- and 32-row tiles of the same
- * kernel (two, three, four workgroups per CU) whose split-K partials are
- * summed by a second, whole-device launch; variants 10, 11, 12: 128-, 128-
- * and 64-row tiles with two wavefronts per SIMD from one workgroup, each
- * taking one k-half of every k-step (10: last-arriver split-K finish, 11 and
- * 12: the second launch); variants 13, 14: hybrids of variants 6 and 8 for
- * grids that do not divide the CUs -- `full` whole tiles on every CU (fewer
- * than a CU holds: one for 13, one or two for 14) and the L leftover tiles
- * split split_k >= 2 ways along K, at most one piece per CU (grid = full x
- * CUs + L x split_k), the pieces' partials compact ([split_k, L, rows, 256]
- * fp32) and added by each leftover tile's last-arriving piece; other shapes
- * get AWQ_ERR_PATH.  Every variant takes split_k >= 1 workgroups along K in
- * whole 128-row groups; the plan's rows_per_wave holds the K rows per split.
- * Other variant numbers (1 .. 5 included): AWQ_ERR_PATH. */
+/* Host-only: a tile-path plan.  Variant 6: 128x256x64 tiles (four
+ * wavefronts, two workgroups per CU), each wavefront 128 x rows x 64
+ * columns, weights dequantised straight into MFMA operand registers, x, raw
+ * weights and zeros/scales brought by direct global->LDS loads two k-steps
+ * ahead into a 3-stage ring, the last-arriving split adding the split-K
+ * partials; variants 7, 8, 9: 128-, 64- and 32-row tiles of the same kernel
+ * (two, three, four workgroups per CU) whose split-K partials are summed by
+ * a second, whole-device launch; variants 13, 14: hybrids of variants 6 and
+ * 8 for grids that do not divide the CUs -- `full` whole tiles on every CU
+ * (fewer than a CU holds: one for 13, one or two for 14) and the L leftover
+ * tiles split split_k >= 2 ways along K, at most one piece per CU (grid =
+ * full x CUs + L x split_k), the pieces' partials compact ([split_k, L,
+ * rows, 256] fp32) and added by each leftover tile's last-arriving piece;
+ * other shapes get AWQ_ERR_PATH.  Every variant takes split_k >= 1
+ * workgroups along K in whole 128-row groups; the plan's rows_per_wave holds
+ * the K rows per split.  Other variant numbers (1 .. 5 and the retired
+ * 10 .. 12 included): AWQ_ERR_PATH. */
 int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
                         int32_t variant, int32_t split_k, awq_w4a16_plan* plan);
 

@@ -8,80 +8,60 @@
 namespace awq {
 
 // ---------------------------------------------------------------------------
-// Variants 6 .. 14: 256 output columns per tile, each wave 64 columns x 32,
-// 64 or 128 x rows, weights dequantised straight into MFMA A registers (never
-// written back to LDS), every global load a direct global->LDS load issued two
-// k-steps ahead into a 3-stage ring.  No VGPR holds data in flight and the
-// compiler sees no global load inside the main loop, so nothing waits on a
-// load before the step that consumes it: the kernel waits itself, once per
-// k-step (vmcnt = the loads issued since).
+// Tile variants 6 .. 9, 13, 14: 256 output columns per tile, four waves of 64
+// columns x 32, 64 or 128 x rows, weights dequantised straight into MFMA A
+// registers (never written back to LDS), every global load a direct
+// global->LDS load issued two k-steps ahead into a 3-stage ring.  No VGPR
+// holds data in flight and the compiler sees no global load inside the main
+// loop, so nothing waits on a load before the step that consumes it: the
+// kernel waits itself, once per k-step (vmcnt = the loads issued since).
 //
 // A stage holds one k-step (64 rows):
 //   * x: BM rows of 128 B, XOR-swizzled: 16-byte chunk p of row r holds
 //     k-chunk p ^ (r & 7), so the MFMA fragment reads of 8 consecutive rows
 //     hit 8 distinct chunk positions (all banks once); rows beyond M read as
 //     zeros (buffer range check); a wave's dwordx4 load writes 8 rows.
-//   * packed weights, 64 rows x 32 packed columns.  KW = 1: wave w's 2 KB
-//     holds its packed columns 8 w .. + 7 row-major (32 B a row, the two
-//     16-byte halves of row r swapped when bit 2 of r is set), loaded by two
-//     dwordx4 loads and read back column-wise with LDS transpose reads.
-//     KW = 2: dword ((((h * 4 + kb) * 2 + ub) * 32 + j) * 4 + u) = row 32 h +
-//     8 kb + 4 ub + u of column j, one dword load covering 4 rows x 16
-//     columns, so the lane that owns column j and rows 8 kb .. + 7 of half h
-//     reads them as two 16-byte words.
-//   * the group's zero words and scales: KW = 1, per wave its 8 zero words
-//     and 64 scales (160 B); KW = 2, 32 zero words and 256 scales.
-// KW = 1 runs each k-step in two phases and overlaps the dequantisation of
-// the next k-half with the MFMAs of the current one (see the main loop).
+//   * packed weights, 64 rows x 32 packed columns: wave w's 2 KB holds its
+//     packed columns 8 w .. + 7 row-major (32 B a row, the two 16-byte halves
+//     of row r swapped when bit 2 of r is set), loaded by two dwordx4 loads
+//     and read back column-wise with LDS transpose reads.
+//   * per wave, the group's 8 zero words and 64 scales of its columns (160 B;
+//     loaded with the first k-step of each 128-row group only).
+// Each k-step runs in two phases that overlap the dequantisation of the next
+// k-half with the MFMAs of the current one (see the main loop).
 // FM: 16-row blocks per wave (8: 128 x rows per wave; 4: 64; 2: 32).
-// KW: 2 -- a second wave per SIMD from the same workgroup: waves w and w + 4
-// take k-half 0 and 1 of every k-step for the same columns and rows (each
-// dequantises only its half) and add their accumulators through LDS at the
-// end; for grids too small to give each CU two workgroups, where a lone
-// wave per SIMD would expose its own latency.
-// Variant 6 = (8, 1): 128 x 256 tiles, four waves, two workgroups per CU,
-// last-arriver split-K finish; 7, 8, 9 = (8, 1), (4, 1), (2, 1): 128, 64
-// and 32 x 256 tiles (two, three, four workgroups per CU)
-// with the reduce-launch finish -- the smaller tiles for M up to about a
-// thousand, where the larger ones would leave MFMA rows idle or the CUs
-// short of work.
+// Variant 6 = FM 8: 128 x 256 tiles, two workgroups per CU, last-arriver
+// split-K finish; 7, 8, 9 = FM 8, 4, 2: 128, 64 and 32 x 256 tiles (two,
+// three, four workgroups per CU) with the reduce-launch finish -- the smaller
+// tiles for small M, where the larger ones would leave MFMA rows idle or the
+// CUs short of work.  (Variants 10 - 12, tiles with a second wave per SIMD
+// taking every other k-half, are retired: slower than these everywhere.)
 namespace {
 constexpr int T5_BK = 64;
 constexpr int T5_BN = 256;
 constexpr int T5_W_BYTES = 64 * 32 * 4;       // packed weights of one k-step
-constexpr int T5_ZS_BYTES = 768;              // 256 B zero words (128 used) + 512 B scales
 constexpr int T5_ZS_WAVE = 160;               // one wave's 8 zero words + 64 scales
 constexpr int T5_GM = 4;
 constexpr int T5_STAGES = 3;
 
-template <int FM, int KW>
+template <int FM>
 struct T5Layout {
     static constexpr int S = T5_STAGES;
-    static constexpr int RW = 16 * FM;  // x rows per wave
-    static constexpr int BM = RW;
+    static constexpr int BM = 16 * FM;  // x rows per tile (every wave reads all of them)
     static constexpr int X_BYTES = BM * T5_BK * 2;
-    // KW = 1: each wave loads the zero words of its own 8 packed columns and
-    // the scales of its 64 columns (32 + 128 B); KW = 2: waves 0..2 load them
-    // for the whole tile.
-    static constexpr int ZS_BYTES = KW == 1 ? 4 * T5_ZS_WAVE : T5_ZS_BYTES;
+    static constexpr int ZS_BYTES = 4 * T5_ZS_WAVE;
     static constexpr int STAGE = X_BYTES + T5_W_BYTES + ZS_BYTES;
-    static constexpr int THREADS = 256 * KW;
-    static constexpr int WAVES = 4 * KW;
-    static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;   // dwordx4 loads per wave per stage (FM / 2)
+    static constexpr int WAVES = 4;
+    static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;  // dwordx4 loads per wave per stage (FM / 2)
     // Workgroups per CU: by registers (accumulators 4 * FM float4 per lane)
     // and by LDS (S stages).
-    static constexpr int PER_CU_REG = KW == 2 ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
+    static constexpr int PER_CU_REG = FM >= 8 ? 2 : (FM >= 4 ? 3 : 4);
     static constexpr int PER_CU_LDS = (160 * 1024) / (S * STAGE + 64);
     static constexpr int PER_CU = PER_CU_REG < PER_CU_LDS ? PER_CU_REG : PER_CU_LDS;
-    // Packed-weight loads per wave per stage: KW = 1, two dwordx4 (the
-    // wave's own 2 KB); KW = 2, dword loads sharing the stage's 8 KB.
-    static constexpr int W_LOADS = KW == 1 ? 2 : T5_W_BYTES / 256 / WAVES;
-    // Loads a wave issues per stage.  KW = 2 does not count the zero/scale
-    // load that waves 0..2 add (issued first, so a wait that leaves this many
-    // outstanding also covers it); KW = 1 counts its two.
-    static constexpr int LOADS = X_LOADS + W_LOADS + (KW == 1 ? 2 : 0);
-    // KW = 1: the loads of an odd k-step, which brings no zero words or
-    // scales (the two k-steps of a 128-row group share them).
+    static constexpr int W_LOADS = 2;  // dwordx4 packed-weight loads per wave per stage (its own 2 KB)
+    // Loads a wave issues per stage: an even k-step's (the first of its
+    // 128-row group) and an odd one's, which brings no zero words or scales.
+    static constexpr int LOADS = X_LOADS + W_LOADS + 2;
     static constexpr int LOADS_NZ = X_LOADS + W_LOADS;
 };
 template <bool B>
@@ -103,10 +83,11 @@ struct Parity {
 // pieces finish early, so their last arrivers add the partials while the
 // whole tiles still run.  The pieces' partials are compact: [split_k][L][BM
 // rows][256 columns] fp32.
-template <int FM, int KW, int FIN, bool HY = false>
-__global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile_kernel_v5(
-    GemmArgs a, int split_k, int k_per_split, uint32_t* counters) {
-    using L = T5Layout<FM, KW>;
+template <int FM, int FIN, bool HY = false>
+__global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(GemmArgs a, int split_k,
+                                                                              int k_per_split,
+                                                                              uint32_t* counters) {
+    using L = T5Layout<FM>;
     constexpr int BM = L::BM;
     constexpr int S = L::S;
     static_assert((S - 2) * L::LOADS <= 63, "vmcnt holds 6 bits");
@@ -119,11 +100,9 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kh = KW == 2 ? wave >> 2 : 0;  // k-half of each step this wave computes (KW = 2)
-    const int wn = wave & 3;
+    const int wn = wave;
     const int n16 = lane & 15;
     const int kb = lane >> 4;
-    const int hh = n16 >> 3;
 
     // ---- work item: XCD-aware grouped tile order (groups of T5_GM row tiles) ----
     const int m_tiles = (a.M + BM - 1) / BM;
@@ -174,102 +153,64 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
 
     // x: load i of wave w writes rows 8 (X_LOADS w + i) .. + 7; lane l brings
     // row 8 b + l / 8, k-chunk (l % 8) ^ (l / 8) to LDS chunk position l % 8.
-    uint32_t x_voff[L::X_LOADS];
-#pragma unroll
-    for (int i = 0; i < L::X_LOADS; ++i) {
-        const int r = 8 * (L::X_LOADS * wave + i) + (lane >> 3);
-        const int q = (lane & 7) ^ (lane >> 3);
-        x_voff[i] = m0 + r < a.M ? (uint32_t)(((size_t)(m0 + r) * a.K + 8 * q) * 2) : 0x80000000u;
-    }
-    // Packed weights.  KW = 2: load i of wave w fills 64-dword block B =
-    // W_LOADS w + i = ((h * 4 + kb) * 2 + ub) * 2 + jh: lane l brings row
-    // 32 h + 8 kb + 4 ub + l % 4 of packed column 16 jh + l / 4.  KW = 1:
-    // wave w loads only its own packed columns 8 w .. 8 w + 7, row-major
-    // (32 B a row): dwordx4 load i covers rows 32 i .. + 31, lane l bringing
-    // the 16-byte slot (l % 2) ^ sw(r) (packed columns 4 s .. + 3) of row
-    // r = 32 i + l / 2, sw(r) = bit 2 of r (slots swapped every 4 rows, so
-    // the transpose reads below meet fewer bank conflicts).
-    uint32_t w_voff[L::W_LOADS];
-#pragma unroll
-    for (int i = 0; i < L::W_LOADS; ++i) {
-        int r, jc;
-        if constexpr (KW == 1) {
-            r = 32 * i + (lane >> 1);
-            jc = (n0 >> 3) + 8 * wave + 4 * ((lane & 1) ^ ((r >> 2) & 1));
-        } else {
-            const int B = L::W_LOADS * wave + i;
-            const int jh = B & 1, ub = (B >> 1) & 1, bk = (B >> 2) & 3, bh = B >> 4;
-            r = 32 * bh + 8 * bk + 4 * ub + (lane & 3);
-            jc = (n0 >> 3) + 16 * jh + (lane >> 2);
-        }
-        w_voff[i] = jc < pn ? (uint32_t)((r * pn + jc) * 4) : 0x80000000u;
-    }
-    // Zero words and scales.  KW = 2: wave 0 loads the zero words (lanes
-    // 0..31 useful, the rest repeat them into the padding), waves 1, 2 the
-    // scales of 128 columns each.  KW = 1: every wave loads the zero words of
-    // its 8 packed columns (lanes 0..7) and the scales of its 64 columns
-    // (lanes 0..31); the other lanes are masked off and write nothing.
-    uint32_t zs_voff = 0x80000000u, s_voff = 0x80000000u;
-    if constexpr (KW == 1) {
-        const int jc = (n0 >> 3) + 8 * wave + (lane & 7);
-        zs_voff = jc < pn ? (uint32_t)jc * 4u : 0x80000000u;
-        const int c = n0 + 64 * wave + 2 * (lane & 31);
-        s_voff = c < a.N ? (uint32_t)c * 2u : 0x80000000u;
-    } else if (wave == 0) {
-        const int jc = (n0 >> 3) + (lane & 31);
-        zs_voff = jc < pn ? (uint32_t)jc * 4u : 0x80000000u;
-    } else if (wave <= 2) {
-        const int c = n0 + 128 * (wave - 1) + 2 * lane;
-        zs_voff = c < a.N ? (uint32_t)c * 2u : 0x80000000u;
+    // A row at or beyond M has an offset at or beyond the buffer's M x K x 2
+    // bytes, so the range check zeroes it; load i's offset is load 0's plus
+    // 8 i rows.
+    const uint32_t x_voff =
+        (uint32_t)(((size_t)(m0 + 8 * L::X_LOADS * wave + (lane >> 3)) * a.K + 8 * ((lane & 7) ^ (lane >> 3))) * 2);
+    // Packed weights: wave w loads only its own packed columns 8 w .. 8 w + 7,
+    // row-major (32 B a row): dwordx4 load i covers rows 32 i .. + 31, lane
+    // l bringing the 16-byte slot (l % 2) ^ sw(r) (packed columns 4 s .. + 3)
+    // of row r = 32 i + l / 2, sw(r) = bit 2 of r (slots swapped every 4
+    // rows, so the transpose reads below meet fewer bank conflicts).  Load 1
+    // uses load 0's offset, its rows 32 further down through the scalar
+    // offset.
+    const int w_row = lane >> 1;
+    const int w_jc = (n0 >> 3) + 8 * wave + 4 * ((lane & 1) ^ ((w_row >> 2) & 1));
+    const uint32_t w_voff = w_jc < pn ? (uint32_t)((w_row * pn + w_jc) * 4) : 0x80000000u;
+    // Zero words and scales: every wave loads the scales of its 64 columns
+    // (lanes 0..31) and the zero words of its 8 packed columns (lanes
+    // 32..39, whose LDS slots the load's base, 128 B lower, puts on the
+    // 32-byte zero area); the other lanes are masked off and write nothing.
+    // One offset register serves both.
+    uint32_t zs_voff;
+    if (lane < 32) {
+        const int s_col = n0 + 64 * wave + 2 * lane;
+        zs_voff = s_col < a.N ? (uint32_t)s_col * 2u : 0x80000000u;
+    } else {
+        const int z_jc = (n0 >> 3) + 8 * wave + (lane & 7);
+        zs_voff = z_jc < pn ? (uint32_t)z_jc * 4u : 0x80000000u;
     }
 
     auto issue = [&](int kt, int stage) {
         const uint32_t base = lds0 + (uint32_t)(stage * L::STAGE);
         const int k0 = k_begin + kt * T5_BK;
         const int g = k0 / kGroup;
-        if constexpr (KW == 1) {
-            // Zero words and scales with the first k-step of each group
-            // only (k-steps are 64 rows, groups 128, and every K range
-            // starts on a group).  Partial-wave loads: the lanes left out
-            // write no LDS (never all of them, so both loads issue and count
-            // in vmcnt).
-            if ((kt & 1) == 0) {
-                const uint32_t zb = base + L::X_BYTES + T5_W_BYTES + (uint32_t)(T5_ZS_WAVE * wave);
-                if (lane < 8)
-                    buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
-                                       zb);
-                if (lane < 32)
-                    buffer_load_lds_x1(rs, s_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
-                                       zb + 32u);
-            }
-        } else if (wave == 0)
-            buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
-                               base + L::X_BYTES + T5_W_BYTES);
-        else if (wave <= 2)
-            buffer_load_lds_x1(rs, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
-                               base + L::X_BYTES + T5_W_BYTES + 256 * wave);
+        // Zero words and scales with the first k-step of each group only
+        // (k-steps are 64 rows, groups 128, and every K range starts on a
+        // group).  Partial-wave loads: the lanes left out write no LDS (never
+        // all of them, so both loads issue and count in vmcnt).
+        if ((kt & 1) == 0) {
+            const uint32_t zb = base + L::X_BYTES + T5_W_BYTES + (uint32_t)(T5_ZS_WAVE * wave);
+            if (lane >= 32 && lane < 40)
+                buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
+                                   zb - 128u);
+            if (lane < 32)
+                buffer_load_lds_x1(rs, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)a.N * 2u),
+                                   zb + 32u);
+        }
 #pragma unroll
         for (int i = 0; i < L::X_LOADS; ++i)
-            buffer_load_lds_x4(rx, x_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * 2u),
+            buffer_load_lds_x4(rx, x_voff + (uint32_t)(16 * i) * (uint32_t)a.K, __builtin_amdgcn_readfirstlane((uint32_t)k0 * 2u),
                                base + 1024u * (uint32_t)(L::X_LOADS * wave + i));
 #pragma unroll
-        for (int i = 0; i < L::W_LOADS; ++i) {
-            if constexpr (KW == 1)  // load 1: the rows 32 below load 0's, through the scalar offset
-                buffer_load_lds_x4(rw, w_voff[0],
-                                   __builtin_amdgcn_readfirstlane((uint32_t)(k0 + 32 * i) * (uint32_t)pn * 4u),
-                                   base + L::X_BYTES + 2048u * (uint32_t)wave + 1024u * (uint32_t)i);
-            else
-                buffer_load_lds_x1(rw, w_voff[i], __builtin_amdgcn_readfirstlane((uint32_t)k0 * (uint32_t)pn * 4u),
-                                   base + L::X_BYTES + 256u * (uint32_t)(L::W_LOADS * wave + i));
-        }
+        for (int i = 0; i < L::W_LOADS; ++i)
+            buffer_load_lds_x4(rw, w_voff, __builtin_amdgcn_readfirstlane((uint32_t)(k0 + 32 * i) * (uint32_t)pn * 4u),
+                               base + L::X_BYTES + 2048u * (uint32_t)wave + 1024u * (uint32_t)i);
     };
 
-    // v_perm selectors (byte 0x0C reads as zero).
     const uint32_t magic = magic_vgpr();        // for one v_and_or_b32 per k-pair
     const uint32_t magic_hi = magic_hi_vgpr();  // (nibbles cut in place)
-    const uint32_t sel_even = hh ? 0x0C050C01u : 0x0C040C00u;
-    const uint32_t sel_odd = hh ? 0x0C070C03u : 0x0C060C02u;
-    const int jl = 8 * wn + (n16 & 7);  // lane's packed column within the tile
 
     floatx4 acc[4][FM];
 #pragma unroll
@@ -277,73 +218,8 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
 #pragma unroll
         for (int f = 0; f < FM; ++f) acc[c][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // KW = 2, one k-step from stage memory `st`: two 16-byte reads give the
-    // lane's 8 weight words of its k-half, 4 A fragments are formed (the
-    // second nibble of a byte is masked in place and read with the 64.0
-    // magic, so every column gives the exact q - z and one fp16 rounding of
-    // (q - z) * s), then the FM B fragments of the wave's x rows, 4 MFMAs each.
-    auto compute = [&](const unsigned char* st) {
-        const half_t* xs = reinterpret_cast<const half_t*>(st);
-        const uint32_t* ws = reinterpret_cast<const uint32_t*>(st + L::X_BYTES);
-        const unsigned char* zs = st + L::X_BYTES + T5_W_BYTES;
-        const uint32_t zw = *reinterpret_cast<const uint32_t*>(zs + 4 * jl);
-        const half4_t s4 = *reinterpret_cast<const half4_t*>(zs + 256 + 2 * (8 * jl + 4 * hh));
-        uint32_t zsp[4], ssp[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            zsp[c] = zero_splat_inplace(zw, 4 * hh + c);
-            ssp[c] = as_u32(half2_t{s4[c], s4[c]});
-        }
-        const int h = kh;
-        const u32x4 w0 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 0) * 32 + jl) * 4]);
-        const u32x4 w1 = *reinterpret_cast<const u32x4*>(&ws[(((h * 4 + kb) * 2 + 1) * 32 + jl) * 4]);
-        const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-        u32x4 af[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t ev = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_even);
-            const uint32_t od = __builtin_amdgcn_perm(wv[2 * t + 1], wv[2 * t], sel_odd);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t kp = and_or(c & 1 ? od : ev, c & 2 ? 0x00F000F0u : 0x000F000Fu, c & 2 ? magic_hi : magic);
-                af[c][t] = as_u32((as_h2(kp) - as_h2(zsp[c])) * as_h2(ssp[c]));
-            }
-        }
-#pragma unroll
-        for (int f = 0; f < FM; ++f) {
-            const int r = 16 * f + n16;
-            const half8_t bf = *reinterpret_cast<const half8_t*>(&xs[r * T5_BK + 8 * ((4 * h + kb) ^ (r & 7))]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                acc[c][f] = mfma16x16x32(__builtin_bit_cast(half8_t, af[c]), bf, acc[c][f]);
-        }
-    };
-
-    if constexpr (KW == 2) {
-        if (KT > 0) {
-            // Prologue: steps 0 .. S - 2 in flight; wait for step 0.
-#pragma unroll
-            for (int j = 0; j < S - 1; ++j)
-                if (j < KT) issue(j, j);
-            wait_batches<L::LOADS, S - 2>(min(S - 2, KT - 1));
-            __syncthreads();
-            int stage = 0;
-            for (int kt = 0; kt < KT; ++kt) {
-                // Step kt + S - 1 into the stage step kt - 1 used (read before
-                // the previous barrier).
-                if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
-                __builtin_amdgcn_sched_barrier(0);
-                compute(smem + stage * L::STAGE);
-                // Step kt + 1's loads must have landed before the barrier;
-                // those of steps kt + 2 .. kt + S - 1 that were issued stay
-                // in flight.
-                wait_batches<L::LOADS, S - 2>(max(0, min(S - 2, KT - 2 - kt)));
-                __syncthreads();
-                stage = stage == S - 1 ? 0 : stage + 1;
-            }
-        }
-    } else {
-        // KW = 1, pipelined across k-steps.  Step kt runs in two phases of FM
+    {
+        // Pipelined across k-steps.  Step kt runs in two phases of FM
         // chunks; chunk f issues the 4 MFMAs of x rows 16 f .. + 15 against
         // the phase's k-half, the read of the B fragment two chunks ahead,
         // and a share of the dequantisation the next phase needs:
@@ -383,22 +259,21 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         // (k-half h, rows 16 f ..) at x_rd[h] + 2048 f; zero word of packed
         // column 2 c + n16 / 8 at z_rd + 8 c; its scale at s_rd + 32 c.
         const uint32_t w_rd = (uint32_t)L::X_BYTES + 2048u * (uint32_t)wn + 32u * (uint32_t)tr_row;
-        const uint32_t tr_lo = w_rd + 16u * (uint32_t)tr_sw;
-        const uint32_t tr_hi = w_rd + 16u * (uint32_t)(tr_sw ^ 1);
+        const uint32_t tr_lo = w_rd + 16u * (uint32_t)tr_sw;  // w_rd is 32-aligned: tr_hi = tr_lo ^ 16
         const uint32_t z_base = (uint32_t)(L::X_BYTES + T5_W_BYTES + T5_ZS_WAVE * wn);
         const uint32_t z_rd = z_base + 4u * (uint32_t)(n16 >> 3);
         const uint32_t s_rd = z_base + 32u + 16u * (uint32_t)(n16 >> 3) + 2u * (uint32_t)(2 * (sgi & 3) + (sgi >> 2));
         const uint32_t zsh = 4u * (uint32_t)sgi;
-        const int c8 = n16 & 7;
-        const uint32_t x_rd[2] = {128u * (uint32_t)n16 + 16u * (uint32_t)(kb ^ c8),
-                                  128u * (uint32_t)n16 + 16u * (uint32_t)((4 + kb) ^ c8)};
+        // k-half 1's chunk is k-half 0's with bit 2 flipped ((4 + kb) ^ c8 =
+        // (kb ^ c8) ^ 4): its byte offset is x_rd ^ 64.
+        const uint32_t x_rd = 128u * (uint32_t)n16 + 16u * (uint32_t)(kb ^ (n16 & 7));
         auto bfrag = [&](const unsigned char* st, int h, int f) {
-            return *reinterpret_cast<const half8_t*>(st + x_rd[h] + 2048 * f);
+            return *reinterpret_cast<const half8_t*>(st + (h ? x_rd ^ 64u : x_rd) + 2048 * f);
         };
         // The 64 transposed bits of chunk c: [0] k-half 0, [1] k-half 1.
         auto trread = [&](const unsigned char* st, int c) {
             typedef int v2i __attribute__((ext_vector_type(2)));
-            const unsigned char* ptr = st + (c < 2 ? tr_lo : tr_hi) + 8 * (c & 1);
+            const unsigned char* ptr = st + (c < 2 ? tr_lo : tr_lo ^ 16u) + 8 * (c & 1);
             const v2i v = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
                 (__attribute__((address_space(3))) v2i*)(ptr));
             return v;
@@ -524,40 +399,18 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
         }
     }
 
-    // KW = 2: wave w + 4 hands its k-half sums to wave w through LDS (two
-    // rounds of two columns; the ring is idle after the last barrier).
-    if constexpr (KW == 2) {
-        floatx4* xch = reinterpret_cast<floatx4*>(smem);
-        static_assert(2 * FM * 4 * 64 * 16 <= S * L::STAGE, "exchange fits the ring");
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            if (kh == 1) {
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                    for (int f = 0; f < FM; ++f) xch[((cc * FM + f) * 4 + wn) * 64 + lane] = acc[2 * r + cc][f];
-            }
-            __syncthreads();
-            if (kh == 0) {
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                    for (int f = 0; f < FM; ++f) acc[2 * r + cc][f] += xch[((cc * FM + f) * 4 + wn) * 64 + lane];
-            }
-            __syncthreads();
-        }
-    }
-
-    // Output quads: each lane holds, for every 16-row block f, four quads of
-    // 4 consecutive columns (tile row 16 f + n16).  KW = 2: quad q is lane
-    // value q of acc[0..3][f], columns 64 wn + 32 (kb & 1) + 8 q + 4 (kb >> 1)
-    // .. + 3.  KW = 1: acc[c][f] lane value r is column 64 wn + 16 c +
-    // 8 (kb >> 1) + 2 r + (kb & 1) (the transposed fragments); lanes l and
-    // l ^ 16 trade two values so that acc[c][f] holds columns 64 wn + 16 c +
-    // 8 (kb >> 1) + 4 (kb & 1) .. + 3, quad c.
-    if constexpr (KW == 1) {
-        const bool odd = kb & 1;
-        const int src = (lane ^ 16) << 2;
+    // Output quads: acc[c][f] lane value r is column 64 wn + 16 c + 8 (kb >>
+    // 1) + 2 r + (kb & 1) of tile row 16 f + n16 (the transposed fragments);
+    // lanes l and l ^ 16 trade two values so that acc[c][f] holds the 4
+    // consecutive columns 64 wn + 16 c + 8 (kb >> 1) + 4 (kb & 1) .. + 3.
+    // The lane's indices are formed again here, the lane number counted
+    // afresh (mbcnt): values shared with the code before the main loop would
+    // otherwise stay in registers across it.
+    const uint32_t eln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int e16 = (int)(eln & 15u), ekb = (int)(eln >> 4);
+    {
+        const bool odd = ekb & 1;
+        const int src = (int)((eln ^ 16u) << 2);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -568,27 +421,17 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
                 acc[c][f] = odd ? floatx4{r0, v[2], r1, v[3]} : floatx4{v[0], r0, v[1], r1};
             }
     }
-    auto quad = [&](int f, int q, int& col) {
-        if constexpr (KW == 1) {
-            col = 64 * wn + 16 * q + 8 * (kb >> 1) + 4 * (kb & 1);
-            return acc[q][f];
-        } else {
-            col = 64 * wn + 32 * (kb & 1) + 8 * q + 4 * (kb >> 1);
-            return floatx4{acc[0][f][q], acc[1][f][q], acc[2][f][q], acc[3][f][q]};
-        }
-    };
+    const int qcol = 64 * wn + 8 * (ekb >> 1) + 4 * (ekb & 1);  // + 16 c: the quad's first column in the tile
     if (ks == 1) {
-        if (kh != 0) return;  // KW = 2: the sums are in waves 0..3
 #pragma unroll
         for (int f = 0; f < FM; ++f) {
-            const int m = m0 + 16 * f + n16;
+            const int m = m0 + 16 * f + e16;
             if (m >= a.M) continue;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                int col;
-                const floatx4 v4 = quad(f, q, col);
+            for (int c = 0; c < 4; ++c) {
+                const int col = qcol + 16 * c;
                 if (n0 + col >= a.N) continue;
-                const float v[4] = {v4[0], v4[1], v4[2], v4[3]};
+                const float v[4] = {acc[c][f][0], acc[c][f][1], acc[c][f][2], acc[c][f][3]};
                 store_out<4>(a.out, a.bias, a.residual, a.N, m, n0 + col, v);
             }
         }
@@ -605,16 +448,15 @@ __global__ __launch_bounds__(256 * KW, (T5Layout<FM, KW>::PER_CU)) void awq_tile
     const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
-        const int m = m0 + 16 * f + n16;
-        if (m >= a.M || kh != 0) continue;
+        const int m = m0 + 16 * f + e16;
+        if (m >= a.M) continue;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            int col;
-            const floatx4 v4 = quad(f, q, col);
+        for (int c = 0; c < 4; ++c) {
+            const int col = qcol + 16 * c;
             if (n0 + col >= a.N) continue;
-            const uint32_t off = pl.base + (uint32_t)(16 * f + n16) * pl.row_stride + (uint32_t)col * 4u +
+            const uint32_t off = pl.base + (uint32_t)(16 * f + e16) * pl.row_stride + (uint32_t)col * 4u +
                                  (uint32_t)split * pl.split_stride;
-            buf_store_f4_device(v4, rp_, off);
+            buf_store_f4_device(acc[c][f], rp_, off);
         }
     }
     if constexpr (FIN == 1) return;
@@ -639,21 +481,18 @@ int64_t tile_tiles(int M, int N, int variant) {
 }
 
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream) {
-    if (cfg.variant >= 6 && cfg.variant <= kTileVariants) {
+    if (tile_variant_served(cfg.variant)) {
         const int64_t blocks = tile_hybrid(cfg.variant) ? cfg.grid : tile_tiles(a.M, a.N, cfg.variant) * cfg.split_k;
         if (blocks == 0) return hipSuccess;
         const dim3 grid((unsigned)blocks);
         bool reduce = false;
         switch (cfg.variant) {
-            case 6: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 1, 0>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 7: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 8: hipLaunchKernelGGL((awq_tile_kernel_v5<4, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 9: hipLaunchKernelGGL((awq_tile_kernel_v5<2, 1, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 10: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 2, 0>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 11: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 12: hipLaunchKernelGGL((awq_tile_kernel_v5<4, 2, 1>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
-            case 13: hipLaunchKernelGGL((awq_tile_kernel_v5<8, 1, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
-            case 14: hipLaunchKernelGGL((awq_tile_kernel_v5<4, 1, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 6: hipLaunchKernelGGL((awq_tile_kernel<8, 0>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 7: hipLaunchKernelGGL((awq_tile_kernel<8, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 8: hipLaunchKernelGGL((awq_tile_kernel<4, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 9: hipLaunchKernelGGL((awq_tile_kernel<2, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 13: hipLaunchKernelGGL((awq_tile_kernel<8, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
+            case 14: hipLaunchKernelGGL((awq_tile_kernel<4, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
             default: return hipErrorInvalidValue;
         }
         const hipError_t e = hipGetLastError();

@@ -34,8 +34,7 @@ def _plans(m, n, k):
         makers += [(f"stream v{v} s4", lambda v=v: _native.plan_stream(m, n, k, 2, 4, variant=v)) for v in (1, 2, 3)]
     if m > 16:
         makers += [(f"tile v{v} s{sp}", lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp))
-                   for v, sp in ((6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (10, 1), (11, 2),
-                                 (12, 2), (13, 2), (14, 3))]
+                   for v, sp in ((6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (13, 2), (14, 3))]
     out = []
     for label, make in makers:
         try:

@@ -102,8 +102,7 @@ def test_auto_plan_invariants(L, m, k, n):
         assert p.path == _native.PATH_TILE
         if m <= 1024 and -(-m // 128) * -(-n // 256) < 512:
             assert p.variant >= 6           # the register-dequant tiles, by the cost model
-            if p.variant in (6, 10):
-                assert p.split_k == 1       # last-arriver variants only unsplit
+            assert p.variant in (7, 8, 9, 13, 14)   # by the cost model; 6 = 7 with the one-launch finish
     assert p.grid > 0 and p.block_threads % 64 == 0 and p.block_threads <= 1024
     if p.split_k > 1:
         if (p.path == _native.PATH_GEMV and p.variant in (4, 5)) or (p.path == _native.PATH_STREAM and p.variant == 1):
@@ -158,7 +157,7 @@ def test_auto_stream_split_keeps_a_group_and_a_half_per_split(L):
 @pytest.mark.parametrize("k,n", SHAPES)
 def test_tile_plans_cover_k_exactly(L, k, n):
     """Every split-K plan gives each split a whole number of 64-row k-steps
-    (variants 6..14: of 128-row groups) and covers K exactly; the tile count fits
+    (variants 6..9, 13, 14: of 128-row groups) and covers K exactly; the tile count fits
     the arrival-counter block.  The hybrids (13, 14) put `full` whole tiles on
     each of the 256 CUs (fewer than a CU holds) and split the leftover tiles,
     at most one piece per CU, with compact partials.  Variant numbers without a
@@ -172,11 +171,11 @@ def test_tile_plans_cover_k_exactly(L, k, n):
                     # no such kernel or split, or partials beyond 2^31 bytes (M = 2048, 8 splits)
                     assert e.status in (_native.AWQ_ERR_PATH, _native.AWQ_ERR_TOO_LARGE)
                     continue
-                assert 6 <= variant <= 14
+                assert variant in (6, 7, 8, 9, 13, 14)
                 per = p.rows_per_wave
                 assert per % 128 == 0
                 assert (split - 1) * per < k <= split * per
-                tm = {6: 128, 7: 128, 8: 64, 9: 32, 12: 64, 14: 64}.get(variant, 128)
+                tm = {6: 128, 7: 128, 8: 64, 9: 32, 14: 64}.get(variant, 128)
                 tn = 256
                 tiles = -(-m // tm) * -(-n // tn)
                 if variant in (13, 14):
