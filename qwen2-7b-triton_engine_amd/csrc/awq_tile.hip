@@ -1,5 +1,5 @@
 // Prefill W4A16 AWQ GEMM (large M) for gfx950: LDS-tiled MFMA kernels
-// (awq_tile_kernel_v5, tile variants 6 .. 14): 256 output columns per tile,
+// (awq_tile_kernel, tile variants 6 .. 9, 13, 14): 256 output columns per tile,
 // weights dequantised straight into MFMA operand registers, every operand
 // streamed into LDS rings by direct global->LDS loads, the reference's exact
 // fp16 weight fp16((q - z) * s) formed next to the load.
