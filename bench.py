@@ -225,7 +225,8 @@ def main():
         awq_gemm_forward(x, *weights[0])
         torch.cuda.synchronize()
         gg = graph_of(torch, lambda: [awq_gemm_forward(x, *w) for w in weights])
-        gg.replay()
+        for _ in range(3):  # warm replays: clocks settle before the timed ones
+            gg.replay()
         t = min(time_graph(torch, gg, 3) for _ in range(3)) / len(weights)
         del gg
         return t
@@ -311,7 +312,7 @@ def main():
                         "GBps": round(b / t / 1e9, 1), "hbm_frac": round(b / t / HBM_PEAK_BPS, 3)})
             return row
 
-        result["prefill_m2048"] = [mfma_point(2048, k, n, rot[name][:4], name) for name, k, n in ENGINE_SHAPES]
+        result["prefill_m2048"] = [mfma_point(2048, k, n, rot[name], name) for name, k, n in ENGINE_SHAPES]
         result["prefill_gate_up"] = next(r for r in result["prefill_m2048"] if r["shape"] == "gate_up_proj")
 
         # The same shapes on torch's dense fp16 GEMM (hipBLASLt; F.linear with an [N, K] fp16
@@ -327,7 +328,8 @@ def main():
             F.linear(xp, dense[0])
             torch.cuda.synchronize()
             gg = graph_of(torch, lambda: [F.linear(xp, w) for w in dense])
-            gg.replay()
+            for _ in range(3):
+                gg.replay()
             t = min(time_graph(torch, gg, 3) for _ in range(3)) / copies
             del gg, dense
             torch.cuda.empty_cache()
@@ -335,7 +337,7 @@ def main():
             row["library_fp16_us"] = round(t * 1e6, 2)
             row["library_fp16_mfma_frac"] = round(f / t / MFMA_F16_DENSE_PEAK_FLOPS, 4)
             log(f"{row['shape']} M=2048 dense fp16 F.linear: {t * 1e6:.2f} us, {f / t / 1e12:.1f} TFLOP/s")
-        result["down_m_sweep"] = [mfma_point(m, INTER, HIDDEN, rot["down_proj"][:4] if m >= 512 else rot["down_proj"])
+        result["down_m_sweep"] = [mfma_point(m, INTER, HIDDEN, rot["down_proj"])
                                   for m in (1, 8, 64, 512, 2048)]
 
         # fp16 lm_head GEMV (vocab x hidden, 1.09 GB per token), next to torch's own F.linear
