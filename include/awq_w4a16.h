@@ -24,7 +24,7 @@
  *
  * A GEMM call is one kernel launch, or two on the same stream when its plan
  * adds split-K partials in a second launch of a reduce kernel: tile
- * variants 7, 8, 9, 11 and 12 and stream variant 3 with split_k > 1.
+ * variants 7, 8 and 9 and stream variant 3 with split_k > 1.
  *
  * Numerics.  Every path computes in fp32 from the exact integer q - z.  The
  * tile paths and the per-weight skinny mode round each weight to fp16 as

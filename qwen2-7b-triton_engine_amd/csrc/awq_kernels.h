@@ -115,7 +115,7 @@ bool stream_fits(int M, int K, int split_k, int k_waves, int layout);
 int64_t stream_threads(int layout, int k_waves);
 
 // split_k > 1 uses the same workspace contract as launch_skinny (counters:
-// one per tile; variants 7, 8, 9, 11, 12 add the partials in a second
+// one per tile; variants 7, 8, 9 add the partials in a second
 // launch of awq_splitk_reduce_kernel on the same stream).
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream);
 int64_t tile_tiles(int M, int N, int variant);

@@ -20,7 +20,7 @@ Triton's masks hide out-of-range reads); only ``group_size == 128`` is served
 (the value the reference always uses, ``model/config.py:22``).  The work runs
 on the caller's current stream: one kernel launch per call, or two when the
 plan adds its split-K partials in a second, reduce launch (tile variants 7,
-8, 9, 11, 12 and stream variant 3 with more than one split).  There is no
+8, 9 and stream variant 3 with more than one split).  There is no
 Triton, no torch dequant and no other fallback: without the HIP library the
 call raises.
 
