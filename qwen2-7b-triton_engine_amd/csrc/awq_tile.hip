@@ -23,7 +23,7 @@ namespace awq {
 //     zeros (buffer range check); a wave's dwordx4 load writes 8 rows.
 //   * packed weights, 64 rows x 32 packed columns: wave w's 2 KB holds its
 //     packed columns 8 w .. + 7 row-major (32 B a row, the two 16-byte halves
-//     of row r swapped when bit 2 of r is set), loaded by two dwordx4 loads
+//     of row r swapped when bit 3 of r is set), loaded by two dwordx4 loads
 //     and read back column-wise with LDS transpose reads.
 //   * per wave, the group's 8 zero words and 64 scales of its columns (160 B;
 //     loaded with the first k-step of each 128-row group only).
@@ -161,12 +161,16 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     // Packed weights: wave w loads only its own packed columns 8 w .. 8 w + 7,
     // row-major (32 B a row): dwordx4 load i covers rows 32 i .. + 31, lane
     // l bringing the 16-byte slot (l % 2) ^ sw(r) (packed columns 4 s .. + 3)
-    // of row r = 32 i + l / 2, sw(r) = bit 2 of r (slots swapped every 4
-    // rows, so the transpose reads below meet fewer bank conflicts).  Load 1
-    // uses load 0's offset, its rows 32 further down through the scalar
-    // offset.
+    // of row r = 32 i + l / 2, sw(r) = bit 3 of r.  A transpose read below
+    // takes 8 bytes at one offset from each of the 64 rows, 32 lanes (rows
+    // r, r + 8, r + 32, r + 40 for each r < 8) through the 64 banks at a
+    // time; a row's banks repeat every 8 rows, so swapping the slots on bit
+    // 3 splits those four rows into two pairs -- a 2-way conflict, the least
+    // 16-byte slots allow (bit 2, which the four rows share, left it 4-way).
+    // Load 1 uses load 0's offset, its rows 32 further down through the
+    // scalar offset.
     const int w_row = lane >> 1;
-    const int w_jc = (n0 >> 3) + 8 * wave + 4 * ((lane & 1) ^ ((w_row >> 2) & 1));
+    const int w_jc = (n0 >> 3) + 8 * wave + 4 * ((lane & 1) ^ ((w_row >> 3) & 1));
     const uint32_t w_voff = w_jc < pn ? (uint32_t)((w_row * pn + w_jc) * 4) : 0x80000000u;
     // Zero words and scales: every wave loads the scales of its 64 columns
     // (lanes 0..31) and the zero words of its 8 packed columns (lanes
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         static_assert(S == 3, "two steps in flight");
         const int sgi = n16 & 7;
         const int tr_row = 32 * (n16 >> 3) + 8 * kb + 2 * (sgi & 3) + (sgi >> 2);
-        const int tr_sw = (tr_row >> 2) & 1;
+        const int tr_sw = (tr_row >> 3) & 1;
         // Stage byte offsets of the lane's reads: transpose slices of chunks
         // 0, 1 at tr_lo + 8 c and 2, 3 at tr_hi + 8 (c - 2); B fragment of
         // (k-half h, rows 16 f ..) at x_rd[h] + 2048 f; zero word of packed
