@@ -439,8 +439,9 @@ def main():
             "kind": "port",
             "sample": "value: layer 0 of the decode sweep at M = 1 and 4 (qkv, o, gate_up, down; 8 of the 336 "
                       "GEMMs of a step) through the torch-CPU restatement of the reference's dequant+matmul "
-                      "(test/compare_benchmark.py:72-95), 1 warm-up + median of 5; per_config: configs 0-3, the "
-                      "M = 2048 gate_up and the down M >= 64 rows timed on 4 / 8 rows of x and projected by FLOP rate",
+                      "(test/compare_benchmark.py:72-95), 1 warm-up + median of 5; per_config: the q_proj GEMV, layer 0 of "
+                      "the decode sweep, the M = 2048 gate_up and the down M-sweep, the M = 2048 gate_up and the "
+                      "down M >= 64 rows timed on 4 / 8 rows of x and projected by FLOP rate",
             "cpu_model": r["cpu_model"],
             "os_cpu_count": r["os_cpu_count"],
             "per_config": rows,

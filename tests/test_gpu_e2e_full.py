@@ -1,4 +1,4 @@
-"""End-to-end decoding at the Qwen2-7B shape against an
+"""End-to-end decoding at the Qwen2-7B shape (28 layers, the greedy decode workload) against an
 independent model: HuggingFace transformers' ``Qwen2ForCausalLM`` (the
 canonical implementation of the architecture the reference reproduces in
 ``model/qwen2.py``), in fp32 with eager attention, loaded with the oracle's
