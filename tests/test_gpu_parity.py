@@ -325,6 +325,41 @@ def test_tile_hybrid_plans(gpu, m, k, n):
     assert tried >= 4
 
 
+def _random_shapes(count, seed, kind="any"):
+    """(M, K, N) drawn from a fixed seed.  "any": M over the decode, small-M
+    and prefill routes, K any multiple of 128 up to 4992, N any multiple of 8
+    up to 9592, at most 3e9 multiply-adds each; "decode": M <= 16 and N a
+    multiple of 32 (the GEMV and stream routes); "prefill": M from 512 to
+    2100, K up to 4992, N up to 12800 (the tile routes and hybrids)."""
+    rng = np.random.default_rng(seed)
+    ms = {"any": [1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 13, 16, 17, 20, 24, 31, 33, 48, 64, 65, 100, 129, 200, 257, 513,
+                  1000],
+          "decode": list(range(1, 17)), "prefill": [512, 600, 1024, 1500, 2048, 2100]}[kind]
+    out = []
+    while len(out) < count:
+        m, k = int(rng.choice(ms)), 128 * int(rng.integers(1, 40))
+        n = 32 * int(rng.integers(1, 400)) if kind == "decode" else 8 * int(rng.integers(1, 1600 if kind == "prefill"
+                                                                                           else 1200))
+        if kind != "any" or m * n * k <= 3e9:
+            out.append((m, k, n))
+    return out
+
+
+@pytest.mark.parametrize("m,k,n", _random_shapes(40, 2027) + _random_shapes(16, 2028, "decode") +
+                         _random_shapes(6, 2029, "prefill"))
+def test_auto_random_shapes(gpu, m, k, n):
+    """AUTO on shapes no other test fixes, drawn at random: every output
+    against the oracle's dequantised product, whichever route and split the
+    dispatcher takes for the shape (N not a multiple of 32 or of a tile,
+    K of a few groups, M between the routes' bounds)."""
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=m + k + n)
+    w = O.dequant_awq(qw, qz, s)
+    y_ref = x.astype(np.float32) @ w.astype(np.float32)
+    p = _native.plan_for(m, n, k)
+    print(f"random shape M={m} K={k} N={n}: {_native.PATH_NAMES[p.path]} v{p.variant} split={p.split_k}", flush=True)
+    _assert_close(_run(gpu, x, qw, qz, s), y_ref, f"random M={m} K={k} N={n}")
+
+
 @pytest.mark.parametrize("m", [1, 2])
 def test_gemv_quad_plans_agree(gpu, m):
     """Column-quad GEMV (balanced K split, fixed-point split-K finish): split
