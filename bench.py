@@ -83,6 +83,14 @@ def kernel_family(_native, m, n, k):
     return _native.PATH_NAMES[_native.plan_for(m, n, k).path]
 
 
+def kernel_family_kernel(_native, m, n, k, name):
+    """`name` when it is a kernel AUTO's plan for (m, n, k) launches, else None
+    (a stale counter profile of another kernel is not attached to a row)."""
+    p = _native.plan_for(m, n, k)
+    prefixes = FAMILY_KERNELS[_native.PATH_NAMES[p.path]]
+    return name if name.startswith(prefixes) else None
+
+
 # Kernels each path family launches (a stream-path GEMM whose split-K partials
 # are added by a second launch runs awq_splitk_reduce_kernel after the main
 # kernel; both count as that GEMM's launch).
@@ -100,21 +108,285 @@ FAMILY_NAMES = {
 }
 
 
+PREFILL_M = 2048
+# Counters of the prefill pass (one rocprofv3 --pmc run: 6 SQ counters, 1 GRBM).
+PREFILL_SQ_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_LDS_IDX_ACTIVE SQ_LDS_BANK_CONFLICT "
+                       "SQ_ACTIVE_INST_LDS SQ_INSTS_LDS GRBM_GUI_ACTIVE")
+PREFILL_LAUNCHES = 3   # eager launches per shape in the prefill counter pass; the last one is summarised
+COPY_BYTES = 64 << 20  # the calibration copy of the counter passes
+
+
+def calibration_copy(torch, dev):
+    """One device-to-device copy of COPY_BYTES (dispatched as the runtime's
+    copyBuffer kernel): the byte counters' reading for it scales them."""
+    src = torch.randint(-2**31, 2**31 - 1, (COPY_BYTES // 4,), device=dev, dtype=torch.int32)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def prefill_counter_pass(torch, dev):
+    """The calibration copy, then PREFILL_LAUNCHES eager launches (synchronised
+    one by one) of each engine shape at M = 2048 on random operands."""
+    from kernels import _native
+    from kernels.awq_gemm import awq_gemm_forward
+
+    calibration_copy(torch, dev)
+    for j, (name, k, n) in enumerate(ENGINE_SHAPES):
+        w = make_weights(torch, dev, k, n, 1000 * 0 + j)
+        x = torch.randn((PREFILL_M, k), device=dev).half()
+        for _ in range(PREFILL_LAUNCHES):
+            awq_gemm_forward(x, *w)
+            torch.cuda.synchronize()
+        del w, x
+    log("prefill counter pass done: copy 67108864 B, then " + ", ".join(
+        f"{name} x{PREFILL_LAUNCHES} {kernel_family(_native, PREFILL_M, n, k)}" for name, k, n in ENGINE_SHAPES))
+
+
+# ---- profile summaries (host only: rocprofv3 CSV -> profiles/) -------------
+def _short_kernel(name):
+    for key in ("awq_splitk_reduce_kernel", "awq_zero_fill_kernel"):
+        if key in name:
+            return key
+    name = name.replace("void awq::", "")
+    return name.split("(")[0]
+
+
+def _counter_csv(d):
+    import glob
+    hits = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not hits:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    return hits[0]
+
+
+def _dispatches(path):
+    """[(dispatch id, kernel, {counter: value}, duration ns)] in dispatch order."""
+    import csv
+    per = {}
+    for r in csv.DictReader(open(path)):
+        d = int(r["Dispatch_Id"])
+        e = per.setdefault(d, [r["Kernel_Name"], {}, int(r["End_Timestamp"]) - int(r["Start_Timestamp"])])
+        e[1][r["Counter_Name"]] = e[1].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [(d, per[d][0], per[d][1], per[d][2]) for d in sorted(per)]
+
+
+def _copy_scale(rows, counter):
+    for _, kname, c, _ in rows:
+        if "copyBuffer" in kname and counter in c:
+            return (COPY_BYTES / 1024) / c[counter], c[counter]
+    raise SystemExit(f"no copyBuffer dispatch with {counter}")
+
+
+def _gemm_groups(rows):
+    """AWQ dispatches grouped per GEMM: a main kernel and, when its split-K
+    partials are added by a second launch, the awq_splitk_reduce_kernel that
+    follows it."""
+    groups = []
+    for row in rows:
+        k = _short_kernel(row[1])
+        if not k.startswith("awq_") or k == "awq_zero_fill_kernel":
+            continue
+        if k == "awq_splitk_reduce_kernel" and groups:
+            groups[-1].append(row)
+        else:
+            groups.append([row])
+    return groups
+
+
+def summarize(argv):
+    kind, dirs = argv[0], argv[1:]
+    from kernels.awq_roofline import HBM_PEAK_BPS, MFMA_F16_DENSE_PEAK_FLOPS, algorithmic_bytes, flops
+    prof = os.path.join(ROOT, "profiles")
+    cmd_head = 'cd /tmp && export TMPDIR=/tmp && cd "$GRAFT_REPO_ROOT"'
+    if kind == "decode-pmc":
+        fetch, write = (_dispatches(_counter_csv(d)) for d in dirs[:2])
+        fs, fcopy = _copy_scale(fetch, "FETCH_SIZE")
+        ws, wcopy = _copy_scale(write, "WRITE_SIZE")
+        gf, gw = _gemm_groups(fetch), _gemm_groups(write)
+        keys = [(m, name, k, n) for m in DECODE_M for name, k, n in ENGINE_SHAPES]
+        assert len(gf) == len(gw) == len(keys), (len(gf), len(gw), len(keys))
+        launches = []
+        for (m, name, k, n), a, b in zip(keys, gf, gw):
+            assert [_short_kernel(r[1]) for r in a] == [_short_kernel(r[1]) for r in b]
+            for j, (ra, rb) in enumerate(zip(a, b)):
+                launches.append({"kernel": _short_kernel(ra[1]), "shape": name, "M": m, "K": k, "N": n,
+                                 "fetch_bytes": round(ra[2]["FETCH_SIZE"] * fs * 1024),
+                                 "write_bytes": round(rb[2]["WRITE_SIZE"] * ws * 1024),
+                                 "algorithmic_bytes": algorithmic_bytes(m, n, k) if j == 0 else 0})
+        cmds = [f"timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -d {dirs[0]} -o fetch --output-format csv -- "
+                "python3 bench.py --counter-pass",
+                f"timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -d {dirs[1]} -o write --output-format csv -- "
+                "python3 bench.py --counter-pass",
+                f"python3 bench.py --summarize decode-pmc {dirs[0]} {dirs[1]}"]
+        json.dump({"source": "profiles/decode_sweep_pmc_traffic.md", "fetch_scale": fs, "write_scale": ws,
+                   "launches": launches}, open(os.path.join(prof, "decode_sweep_pmc_traffic.json"), "w"), indent=1)
+        md = ["# Decode sweep: HBM traffic per launch (rocprofv3 PMC FETCH_SIZE / WRITE_SIZE)", "",
+              "Commands (two counter passes, then the summary; from the repository root on the MI355X box):", "",
+              "```", cmd_head, *cmds, "```", "",
+              "`bench.py --counter-pass` makes the operands, runs one 64 MiB device-to-device copy",
+              "(`torch.Tensor.copy_`, dispatched as `__amd_rocclr_copyBuffer`), then one eager launch of each",
+              "engine shape at M = 1, 4, 16 on layer 0's weights (AUTO plans; a GEMM whose split-K partials are",
+              "added by a second launch shows two dispatches, the main kernel and `awq_splitk_reduce_kernel`).", "",
+              "## Calibration with the copy of known size (67,108,864 B read and written)", "",
+              "| counter | reads for the copy (KiB) | expected (KiB) | scale factor |", "|---|---|---|---|",
+              f"| FETCH_SIZE | {fcopy:.1f} | 65536 | {fs:.4f} |", f"| WRITE_SIZE | {wcopy:.1f} | 65536 | {ws:.4f} |",
+              "", "Fetched and written bytes below are the counter times the factor above.", "",
+              "## Per launch (scaled; MB = 1e6 bytes)", "",
+              "| kernel | shape | M | fetch (MB) | write (MB) | traffic (MB) | algorithmic (MB) | traffic / algorithmic |",
+              "|---|---|---|---|---|---|---|---|"]
+        gemm_traffic = {}
+        for e in launches:
+            gemm_traffic[(e["M"], e["shape"])] = gemm_traffic.get((e["M"], e["shape"]), 0) + e["fetch_bytes"] + e["write_bytes"]
+        for e in launches:
+            t = e["fetch_bytes"] + e["write_bytes"]
+            a = e["algorithmic_bytes"]
+            shp = f"{e['shape']} {e['K']}->{e['N']}"
+            if a:
+                tot = gemm_traffic[(e["M"], e["shape"])]
+                md.append(f"| `{e['kernel']}` | {shp} | {e['M']} | {e['fetch_bytes']/1e6:.2f} | {e['write_bytes']/1e6:.2f} "
+                          f"| {t/1e6:.2f} | {a/1e6:.2f} | {t/a:.2f} (GEMM {tot/a:.2f}) |")
+            else:
+                md.append(f"| `{e['kernel']}` | {shp} | {e['M']} | {e['fetch_bytes']/1e6:.2f} | {e['write_bytes']/1e6:.2f} "
+                          f"| {t/1e6:.2f} | (same GEMM) | |")
+        open(os.path.join(prof, "decode_sweep_pmc_traffic.md"), "w").write("\n".join(md) + "\n")
+        print(f"decode-pmc: {len(launches)} launches")
+    elif kind == "prefill-pmc":
+        sq, fetch, write = (_dispatches(_counter_csv(d)) for d in dirs[:3])
+        fs, fcopy = _copy_scale(fetch, "FETCH_SIZE")
+        ws, wcopy = _copy_scale(write, "WRITE_SIZE")
+        gsq, gf, gw = _gemm_groups(sq), _gemm_groups(fetch), _gemm_groups(write)
+        want = len(ENGINE_SHAPES) * PREFILL_LAUNCHES
+        assert len(gsq) == len(gf) == len(gw) == want, (len(gsq), len(gf), len(gw), want)
+        simds = 256 * 4
+        rows = []
+        for i, (name, k, n) in enumerate(ENGINE_SHAPES):
+            last = (i + 1) * PREFILL_LAUNCHES - 1   # the warm launch
+            a, b, c = gsq[last], gf[last], gw[last]
+            main = a[0]
+            cnt = main[2]
+            dur_ns = main[3]
+            xcds = 8
+            clk_cycles = cnt["GRBM_GUI_ACTIVE"] / xcds
+            busy = cnt["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * clk_cycles)
+            fetch_b = sum(r[2]["FETCH_SIZE"] for r in b) * fs * 1024
+            write_b = sum(r[2]["WRITE_SIZE"] for r in c) * ws * 1024
+            f = flops(PREFILL_M, n, k)
+            rows.append({
+                "shape": name, "M": PREFILL_M, "K": k, "N": n, "kernel": _short_kernel(main[1]),
+                "launches": [_short_kernel(r[1]) for r in a],
+                "duration_us": round(dur_ns / 1e3, 2),
+                "TFLOPs_in_pass": round(f / (dur_ns * 1e-9) / 1e12, 1),
+                "mfma_busy": round(busy, 4),
+                "clock_GHz": round(clk_cycles / (dur_ns * 1e-9) / 1e9, 3),
+                "lds_bank_conflict_per_lds_active": round(cnt["SQ_LDS_BANK_CONFLICT"] / max(cnt["SQ_LDS_IDX_ACTIVE"], 1), 4),
+                "counters": {key: cnt[key] for key in sorted(cnt)},
+                "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
+                "algorithmic_bytes": algorithmic_bytes(PREFILL_M, n, k),
+            })
+        cmds = [f"timeout -s KILL 120 rocprofv3 --pmc {PREFILL_SQ_COUNTERS} -d {dirs[0]} -o sq --output-format csv -- "
+                "python3 bench.py --counter-pass prefill",
+                f"timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -d {dirs[1]} -o fetch --output-format csv -- "
+                "python3 bench.py --counter-pass prefill",
+                f"timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -d {dirs[2]} -o write --output-format csv -- "
+                "python3 bench.py --counter-pass prefill",
+                f"python3 bench.py --summarize prefill-pmc {' '.join(dirs[:3])}"]
+        json.dump({"source": "profiles/prefill_tile_pmc.md", "fetch_scale": fs, "write_scale": ws,
+                   "simds": simds, "xcds": 8, "rows": rows},
+                  open(os.path.join(prof, "prefill_tile_pmc.json"), "w"), indent=1)
+        md = ["# Prefill (M = 2048) on the four Qwen2-7B engine shapes: rocprofv3 counters", "",
+              "Commands (three counter passes, then the summary; from the repository root on the MI355X box):", "",
+              "```", cmd_head, *cmds, "```", "",
+              f"`bench.py --counter-pass prefill` runs one 64 MiB device-to-device copy (the byte counters' "
+              f"calibration), then {PREFILL_LAUNCHES} eager launches of each engine shape at M = 2048 (AUTO plans, "
+              "random operands), synchronised one by one; the last launch of each shape (warm clocks) is the one",
+              "summarised.  Counters are summed over the device per dispatch.", "",
+              "* MFMA busy = `SQ_VALU_MFMA_BUSY_CYCLES` / (1024 SIMDs x `GRBM_GUI_ACTIVE` / 8 XCDs): the share of",
+              "  SIMD cycles with the matrix core busy while the kernel runs.",
+              "* Effective clock = (`GRBM_GUI_ACTIVE` / 8) / kernel duration; the dense fp16 peak (2516.6 TFLOP/s)",
+              "  assumes 2.4 GHz.",
+              "* Durations are the counter run's (serialised dispatches, counters on): the bench's graph-timed",
+              "  figures are the throughput numbers.",
+              f"* Byte counters scaled by the copy: FETCH_SIZE x {fs:.4f} (read {fcopy:.1f} KiB for 65536), "
+              f"WRITE_SIZE x {ws:.4f} (wrote {wcopy:.1f} KiB).", "",
+              "| shape | kernels | duration (us) | TFLOP/s in the pass | MFMA busy | clock (GHz) | LDS bank conflicts / LDS active | "
+              "fetch (MB) | write (MB) | algorithmic (MB) |", "|---|---|---|---|---|---|---|---|---|---|"]
+        for r in rows:
+            md.append(f"| {r['shape']} {r['K']}->{r['N']} | {' + '.join('`' + x + '`' for x in r['launches'])} | "
+                      f"{r['duration_us']:.1f} | {r['TFLOPs_in_pass']:.0f} | {100 * r['mfma_busy']:.1f} % | "
+                      f"{r['clock_GHz']:.2f} | {r['lds_bank_conflict_per_lds_active']:.3f} | {r['fetch_bytes']/1e6:.1f} | "
+                      f"{r['write_bytes']/1e6:.1f} | {r['algorithmic_bytes']/1e6:.1f} |")
+        md += ["", "## Raw counter values of the summarised dispatch (main kernel)", "",
+               "| shape | " + " | ".join(f"`{c}`" for c in PREFILL_SQ_COUNTERS.split()) + " |",
+               "|---|" + "---|" * len(PREFILL_SQ_COUNTERS.split())]
+        for r in rows:
+            md.append(f"| {r['shape']} | " + " | ".join(f"{r['counters'].get(c, float('nan')):.0f}"
+                                                      for c in PREFILL_SQ_COUNTERS.split()) + " |")
+        open(os.path.join(prof, "prefill_tile_pmc.md"), "w").write("\n".join(md) + "\n")
+        print(f"prefill-pmc: {len(rows)} shapes")
+    elif kind == "kernel-trace":
+        import csv
+        import glob
+        import statistics
+        d = dirs[0]
+        stats_path = sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True))[0]
+        trace_path = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))[0]
+        out_name = dirs[1] if len(dirs) > 1 else "decode_sweep_kernel_trace.md"
+        command = (f"rocprofv3 --kernel-trace --stats -d {d} -o bench --output-format csv -- "
+                   "python3 bench.py --no-cpu-baseline --no-extras --steps 5 --warmup 1")
+        all_stats = list(csv.DictReader(open(stats_path)))
+        tot = sum(float(r["TotalDurationNs"]) for r in all_stats)
+        md = [f"# rocprofv3 kernel trace: {out_name.replace('_kernel_trace.md', '').replace('_', ' ')}", "",
+              "Commands (from the repository root on the MI355X box):", "", "```", cmd_head, command,
+              f"python3 bench.py --summarize kernel-trace {d} {out_name}", "```", "",
+              "## Per-kernel statistics (AWQ kernels only)", "",
+              "| kernel | calls | average (us) | min (us) | max (us) | share of GPU time |", "|---|---|---|---|---|---|"]
+        for r in all_stats:
+            if "awq" not in r["Name"]:
+                continue
+            md.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | "
+                      f"{float(r['MinNs'])/1e3:.2f} | {float(r['MaxNs'])/1e3:.2f} | {100*float(r['TotalDurationNs'])/tot:.1f} % |")
+        groups = {}
+        for r in csv.DictReader(open(trace_path)):
+            if "awq" not in r["Kernel_Name"]:
+                continue
+            key = (_short_kernel(r["Kernel_Name"]), int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
+            groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        md += ["", "## Per launch configuration (grid in threads)", "",
+               "| kernel | grid | workgroup | launches | median (us) | mean (us) |", "|---|---|---|---|---|---|"]
+        for (k, g, w), v in sorted(groups.items()):
+            md.append(f"| `{k}` | {g} | {w} | {len(v)} | {statistics.median(v):.2f} | {statistics.mean(v):.2f} |")
+        open(os.path.join(prof, out_name), "w").write("\n".join(md) + "\n")
+        print(f"kernel-trace: {len(groups)} launch configurations -> profiles/{out_name}")
+    else:
+        raise SystemExit(f"unknown summary kind {kind!r}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=90.0,
+    ap.add_argument("--cpu-budget", type=float, default=120.0,
                     help="seconds of CPU baseline work after which each remaining config gets one timed run")
     ap.add_argument("--no-extras", action="store_true", help="headline only (for profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the end-to-end decode extra (its ~230k kernel launches swamp a kernel trace)")
-    ap.add_argument("--counter-pass", action="store_true",
-                    help="for rocprofv3 --pmc runs: a 64 MiB device copy (calibrates the byte counters), "
-                         "then one eager launch of every engine shape at M in {1,4,16}; no timing output")
+    ap.add_argument("--counter-pass", nargs="?", const="decode", choices=("decode", "prefill"),
+                    help="for rocprofv3 --pmc runs: a 64 MiB device copy (calibrates the byte counters), then "
+                         "'decode' (default): one eager launch of every engine shape at M in {1,4,16}; "
+                         "'prefill': three eager launches of every engine shape at M = 2048 (the third, on warm "
+                         "clocks, is the one summarised); no timing output")
+    ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
+                    help="host only: turn rocprofv3 CSV output into the profiles/ summaries. "
+                         "'decode-pmc FETCH_DIR WRITE_DIR', 'prefill-pmc SQ_DIR FETCH_DIR WRITE_DIR' "
+                         "(directories of --counter-pass runs) or 'kernel-trace DIR' (a --kernel-trace --stats run)")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
@@ -131,6 +403,10 @@ def main():
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} CUs={props.multi_processor_count}")
+
+    if args.counter_pass == "prefill":
+        prefill_counter_pass(torch, dev)
+        return
 
     # ---- synthetic operands: 28 layers x 4 fused projections ---------------
     t0 = time.time()
@@ -152,7 +428,7 @@ def main():
                     outs.append(awq_gemm_forward(xs[(m, k)], *layers[li][name]))
         return outs
 
-    if args.counter_pass:
+    if args.counter_pass == "decode":
         src = torch.randint(-2**31, 2**31 - 1, (16 << 20,), device=dev, dtype=torch.int32)  # 64 MiB
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -246,6 +522,34 @@ def main():
             family_time[fam] = family_time.get(fam, 0.0) + t * LAYERS
             family_bytes[fam] = family_bytes.get(fam, 0) + b * LAYERS
             family_launches[fam] = family_launches.get(fam, 0) + LAYERS
+    # Eager calls, as the reference engine makes them (112 awq_gemm_forward calls per token,
+    # model/qwen2.py:44,104,183, never graph-replayed, inference/engine.py:114-139): the wall time
+    # per call of EAGER_CALLS back-to-back calls over the 28 layers' weights (host work and kernels
+    # overlap; a loop bound by the host shows eager_us above the graph-timed us), and the host
+    # time to issue one call (Python entry, checks, plan lookup, ctypes, launch).
+    EAGER_CALLS = 3 * LAYERS
+    for row in per_gemm:
+        m, k, n, name = row["M"], row["K"], row["N"], row["shape"]
+        x = xs[(m, k)]
+        ws = [layers[li][name] for li in range(LAYERS)]
+        for w in ws[:4]:
+            awq_gemm_forward(x, *w)
+        torch.cuda.synchronize()
+        best_wall, best_host = float("inf"), float("inf")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for i in range(EAGER_CALLS):
+                awq_gemm_forward(x, *ws[i % LAYERS])
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            best_wall = min(best_wall, (t2 - t0) / EAGER_CALLS)
+            best_host = min(best_host, (t1 - t0) / EAGER_CALLS)
+        row["eager_us"] = round(best_wall * 1e6, 2)
+        row["eager_host_us"] = round(best_host * 1e6, 2)
+        log(f"{name} M={m}: eager {row['eager_us']} us per call (host {row['eager_host_us']} us), "
+            f"graph {row['us']} us")
+
     dom = max(family_time, key=family_time.get)
     avg_t = family_time[dom] / family_launches[dom]
     avg_b = family_bytes[dom] / family_launches[dom]
@@ -313,6 +617,19 @@ def main():
             return row
 
         result["prefill_m2048"] = [mfma_point(2048, k, n, rot[name], name) for name, k, n in ENGINE_SHAPES]
+        # MFMA utilisation and effective clock of each shape's kernel, from the committed counter
+        # profile (bench.py --counter-pass prefill under rocprofv3 --pmc), the way the decode
+        # roofline carries its traffic.
+        pmc_path = os.path.join(ROOT, "profiles", "prefill_tile_pmc.json")
+        if os.path.exists(pmc_path):
+            with open(pmc_path) as f:
+                pmc_rows = {r["shape"]: r for r in json.load(f)["rows"]}
+            for row in result["prefill_m2048"]:
+                r = pmc_rows.get(row["shape"])
+                if r is not None and r["kernel"] == kernel_family_kernel(_native, 2048, row["N"], row["K"], r["kernel"]):
+                    row["mfma_busy"] = r["mfma_busy"]
+                    row["clock_GHz"] = r["clock_GHz"]
+                    row["counters_source"] = "profiles/prefill_tile_pmc.md"
         result["prefill_gate_up"] = next(r for r in result["prefill_m2048"] if r["shape"] == "gate_up_proj")
 
         # The same shapes on torch's dense fp16 GEMM (hipBLASLt; F.linear with an [N, K] fp16
@@ -403,7 +720,7 @@ def main():
         # (config, shape, full M, sampled rows, K, N, weights)
         samples = [("0: q_proj GEMV (a 3584 x 3584 weight)", "q_proj", 1, 1, HIDDEN, HIDDEN, layers[0]["o_proj"])]
         samples += [("1: decode sweep, layer 0", name, m, m, k, n, layers[0][name])
-                    for m in (1, 4) for name, k, n in ENGINE_SHAPES]
+                    for m in DECODE_M for name, k, n in ENGINE_SHAPES]
         samples += [("2: prefill gate_up", "gate_up_proj", 2048, 4, HIDDEN, 2 * INTER, layers[0]["gate_up_proj"])]
         samples += [("3: down_proj M-sweep", "down_proj", m, min(m, 8), INTER, HIDDEN, layers[0]["down_proj"])
                     for m in (1, 8, 64, 512, 2048)]
@@ -415,7 +732,7 @@ def main():
                 qw, qz, sc = (t.cpu() for t in w)
                 x = torch.randn((ms, k), generator=gen, device=dev).half().cpu()
                 t0 = time.perf_counter()
-                r = time_cpu_baseline(x, qw, qz, sc, reps=3 if m >= 512 else 5, warmup=1, threads=threads,
+                r = time_cpu_baseline(x, qw, qz, sc, reps=3 if m >= 16 else 5, warmup=1, threads=threads,
                                       budget_s=max(1e-3, args.cpu_budget - spent))
                 spent += time.perf_counter() - t0
                 cache[(name, ms, k, n)] = r
@@ -437,11 +754,12 @@ def main():
             "unit": "GB/s",
             "cores": r["threads"],
             "kind": "port",
-            "sample": "value: layer 0 of the decode sweep at M = 1 and 4 (qkv, o, gate_up, down; 8 of the 336 "
-                      "GEMMs of a step) through the torch-CPU restatement of the reference's dequant+matmul "
-                      "(test/compare_benchmark.py:72-95), 1 warm-up + median of 5; per_config: the q_proj GEMV, layer 0 of "
-                      "the decode sweep, the M = 2048 gate_up and the down M-sweep, the M = 2048 gate_up and the "
-                      "down M >= 64 rows timed on 4 / 8 rows of x and projected by FLOP rate",
+            "sample": "value: layer 0 of the decode sweep at M = 1, 4 and 16 (qkv, o, gate_up, down; 12 of the "
+                      "336 GEMMs of a step, the same mix of shapes and M as the headline) through the torch-CPU "
+                      "restatement of the reference's dequant+matmul (test/compare_benchmark.py:72-95), 1 warm-up "
+                      "+ median of 5 (3 at M = 16); per_config: the q_proj GEMV, layer 0 of the decode sweep, the "
+                      "M = 2048 gate_up and the down M-sweep, the M = 2048 gate_up and the down M >= 64 rows timed "
+                      "on 4 / 8 rows of x and projected by FLOP rate",
             "cpu_model": r["cpu_model"],
             "os_cpu_count": r["os_cpu_count"],
             "per_config": rows,

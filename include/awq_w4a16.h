@@ -61,7 +61,8 @@ typedef enum awq_w4a16_status {
     AWQ_ERR_LAUNCH = -6,         /* the HIP runtime rejected a kernel launch           */
     AWQ_ERR_PATH = -7,           /* unknown kernel path, or path cannot serve this M   */
     AWQ_ERR_TOO_LARGE = -8,      /* M > 2^30, K > 2^22, N > 2^20 or operand > 2^31-1 B */
-    AWQ_ERR_SCRATCH = -9         /* awq_w4a16_gemm_noalloc: workspace > the static scratch */
+    AWQ_ERR_SCRATCH = -9,        /* awq_w4a16_gemm_noalloc: workspace > the static scratch */
+    AWQ_ERR_CAPTURE = -10        /* awq_w4a16_gemm_noalloc: first split-K call on a device under capture */
 } awq_w4a16_status;
 
 /* Kernel paths.  AUTO lets the shape dispatcher choose (the reference's own
@@ -245,8 +246,12 @@ int awq_w4a16_gemm_planned(const void* x, const int32_t* qweight, const int32_t*
  * memory -- code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  The split-K workspace is a static device array of
  * AWQ_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on every GPU it
- * runs on until the process ends; the first call on a device looks up its
- * address and clears it (one fill kernel on `stream`).  The plan is the AUTO
+ * runs on until the process ends.  The first call on a device that needs a
+ * split-K workspace looks up the device's address of the array (the device
+ * `stream` belongs to), clears its counter and slot regions with one fill
+ * kernel on `stream` and waits for it; that first call must not be made
+ * under graph capture (AWQ_ERR_CAPTURE: make one eager call on each device
+ * before capturing), later calls may be captured.  The plan is the AUTO
  * plan, except that a tile plan whose workspace would exceed the scratch
  * takes the largest split-K count that fits (so results can differ from
  * awq_w4a16_gemm in the last bits there); a decode plan that does not fit

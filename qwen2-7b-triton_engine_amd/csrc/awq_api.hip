@@ -659,8 +659,8 @@ std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device, once set up
 
 // This device's scratch address; the first call on a device looks it up and
-// clears the array with a fill kernel on the caller's stream (a kernel, not
-// hipMemsetAsync, so that a call under graph capture records no memset node).
+// clears the counter and slot regions with a fill kernel on the caller's
+// stream (see the definition below).
 int device_scratch(hipStream_t stream, void** ptr_out);
 
 // The AUTO plan, with the tile path's split-K count lowered until its
@@ -692,16 +692,41 @@ int noalloc_plan(int64_t M, int64_t N, int64_t K, int32_t group_size, awq_w4a16_
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
+// Set-up on the stream's device (the current device for the null stream):
+// look up the device's copy of `scratch` with that device current, clear the
+// regions that must start at zero -- the arrival counters and the
+// fixed-point slots, the first kPartialsOffset bytes (every call writes the
+// partials it reads before reading them, so the rest needs no clearing) --
+// and wait for the clear, so that a later call on any stream finds them
+// zero.  Refused while the stream is being captured (AWQ_ERR_CAPTURE): the
+// fill kernel would become a node of the caller's graph and the wait is not
+// allowed there; one eager call per device must come first.
 int device_scratch(hipStream_t stream, void** ptr_out) {
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return AWQ_ERR_LAUNCH;
+    if (stream != nullptr) {
+        if (hipStreamGetDevice(stream, &dev) != hipSuccess) return AWQ_ERR_LAUNCH;
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return AWQ_ERR_LAUNCH;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return AWQ_ERR_LAUNCH;
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (!g_scratch_ptr[dev]) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return AWQ_ERR_LAUNCH;
+        if (cap != hipStreamCaptureStatusNone) return AWQ_ERR_CAPTURE;
+        int prev = -1;
+        if (hipGetDevice(&prev) != hipSuccess) return AWQ_ERR_LAUNCH;
+        if (prev != dev && hipSetDevice(dev) != hipSuccess) return AWQ_ERR_LAUNCH;
         void* ptr = nullptr;
-        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return AWQ_ERR_LAUNCH;
-        hipLaunchKernelGGL(awq_zero_fill_kernel, dim3(1024), dim3(256), 0, stream, static_cast<u32x4*>(ptr),
-                           kScratchBytes / 16);
-        if (hipGetLastError() != hipSuccess) return AWQ_ERR_LAUNCH;
+        const bool found = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess && ptr != nullptr;
+        int st = found ? AWQ_OK : AWQ_ERR_LAUNCH;
+        if (found) {
+            hipLaunchKernelGGL(awq_zero_fill_kernel, dim3(64), dim3(256), 0, stream, static_cast<u32x4*>(ptr),
+                               kPartialsOffset / 16);
+            if (hipGetLastError() != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) st = AWQ_ERR_LAUNCH;
+        }
+        if (prev != dev && hipSetDevice(prev) != hipSuccess) st = AWQ_ERR_LAUNCH;
+        if (st != AWQ_OK) return st;
         g_scratch_ptr[dev] = ptr;
     }
     *ptr_out = g_scratch_ptr[dev];
@@ -727,6 +752,9 @@ const char* awq_w4a16_error_string(int status) {
         case AWQ_ERR_SCRATCH:
             return "the shape's split-K workspace exceeds the allocation-free entry point's static scratch "
                    "(AWQ_NOALLOC_SCRATCH_BYTES); call awq_w4a16_gemm with a workspace instead";
+        case AWQ_ERR_CAPTURE:
+            return "the allocation-free entry point's first split-K call on a device was made under graph "
+                   "capture; make one call outside capture on that device first (it clears the scratch)";
         default: return "unknown status";
     }
 }

@@ -88,6 +88,18 @@ def _greedy_token(logits: torch.Tensor) -> torch.Tensor:
     return row * 256 + idx.index_select(0, row)
 
 
+def _checked_token(tok: torch.Tensor, vocab_size: int, bad: torch.Tensor) -> torch.Tensor:
+    """``tok`` clamped into ``[0, vocab_size)``, counting out-of-range tokens
+    in the device flag ``bad`` (int32 [1]).  The decode step feeds the token
+    it generates straight into the embedding lookup of the next step, inside
+    a replayed graph with no host check in between: an index past the table
+    would make that lookup read outside it.  Clamped, the lookup stays in
+    range, and ``generate`` raises from the flag after the replays.  Both
+    operations are elementwise on one element: graph-safe, no host sync."""
+    bad.add_(torch.logical_or(tok < 0, tok >= vocab_size).to(torch.int32))
+    return tok.clamp(0, vocab_size - 1)
+
+
 def _rotate_half(x: torch.Tensor) -> torch.Tensor:
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
@@ -220,10 +232,11 @@ class Qwen2AwqDecoder:
         self._tok = torch.zeros(1, dtype=torch.int64, device=self.dev)
         self._pos = torch.zeros(1, dtype=torch.int64, device=self.dev)
         self._out = torch.zeros(self.max_seq_len, dtype=torch.int64, device=self.dev)
+        self._bad = torch.zeros(1, dtype=torch.int32, device=self.dev)
 
         def step():
             logits = self._forward(self._tok, self._pos, causal=False)
-            nxt = _greedy_token(logits)
+            nxt = _checked_token(_greedy_token(logits), self.s.vocab_size, self._bad)
             self._out.index_copy_(0, self._pos, nxt)       # out[p] = token generated at position p + 1
             self._tok.copy_(nxt)
             self._pos.add_(1)
@@ -252,6 +265,7 @@ class Qwen2AwqDecoder:
             self._capture()
         self.k_cache.zero_()
         self.v_cache.zero_()
+        self._bad.zero_()
         torch.cuda.synchronize(self.dev)
         t0 = time.perf_counter()
         logits = self.prefill(prompt)
@@ -264,6 +278,9 @@ class Qwen2AwqDecoder:
             self._graph.replay()
         torch.cuda.synchronize(self.dev)
         t2 = time.perf_counter()
+        if int(self._bad.item()) != 0:
+            raise RuntimeError(f"{int(self._bad.item())} decode step(s) produced a token outside the vocabulary "
+                               f"[0, {self.s.vocab_size}); the lookups were clamped, the tokens are not valid")
         tokens = torch.cat([first, self._out[S:S + new_tokens - 1]]).cpu()
         decode_s = t2 - t1
         return {"tokens": tokens, "prefill_s": t1 - t0, "decode_s": decode_s,

@@ -23,6 +23,7 @@ AWQ_ERR_LAUNCH = -6
 AWQ_ERR_PATH = -7
 AWQ_ERR_TOO_LARGE = -8
 AWQ_ERR_SCRATCH = -9
+AWQ_ERR_CAPTURE = -10
 NOALLOC_SCRATCH_BYTES = 32 << 20
 SLOT_BYTES = 2 << 20   # fixed-point slot region of a workspace (AWQ_W4A16_SLOT_BYTES)
 

@@ -107,48 +107,90 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """``t`` itself when its data starts on a 16-byte boundary, else a copy
+    (a fresh allocation is aligned).  The kernels read x, scales and out with
+    16-byte loads and stores and the C ABI refuses other addresses; the
+    reference's Triton path takes any fp16 view, so an odd storage offset is
+    copied here rather than refused."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _prepare(x, qweight, qzeros, scales, group_size):
     K, N = _check_operands(x, qweight, qzeros, scales, group_size)
     dev = _check_device(x, qweight, qzeros, scales)
     in_shape = x.shape
-    x_flat = x.reshape(-1, K).contiguous()          # kernels/awq_gemm.py:244-246
+    x_flat = _aligned16(x.reshape(-1, K).contiguous())          # kernels/awq_gemm.py:244-246
     # The reference passes strides to Triton; the C ABI takes dense operands.
     qweight = qweight.contiguous()
     qzeros = qzeros.contiguous()
-    scales = scales.contiguous()
+    scales = _aligned16(scales.contiguous())
     return in_shape, x_flat, qweight, qzeros, scales, K, N, dev
+
+
+# Plans of the AUTO dispatcher (or a forced path) per (M, N, K, group size,
+# path, device): the planner's choice depends only on these and on the
+# device's compute-unit count, so an eager call looks it up once instead of
+# planning in C on every call.  Bounded: cleared when it grows past _PLAN_CACHE_MAX.
+_plans: dict = {}
+_PLAN_CACHE_MAX = 4096
+
+
+class _OnDevice:
+    """``torch.cuda.device(dev)`` unless ``dev`` is already current (the
+    context manager costs a device switch and back on every call)."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, dev: torch.device):
+        self.idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _plan_cached(M: int, N: int, K: int, group_size: int, path: int, dev: torch.device) -> "_native.Plan":
+    key = (M, N, K, group_size, path, dev.index)
+    p = _plans.get(key)
+    if p is None:
+        with _OnDevice(dev):
+            p = _native.plan_for(M, N, K, group_size, path)
+        if len(_plans) >= _PLAN_CACHE_MAX:
+            _plans.clear()
+        _plans[key] = p
+    return p
 
 
 def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=None, plan_obj=None,
             bias=None, residual=None):
     L = _native.lib()
-    if (bias is not None or residual is not None) and plan_obj is None:
-        plan_obj = _native.plan_for(M, N, K, group_size, _native.PATH_AUTO if path is None else path)
-    if plan_obj is not None:
-        ws_bytes = int(plan_obj.workspace_bytes)
-    else:
-        ws_bytes = _native.workspace_bytes(M, N, K, group_size, _native.PATH_AUTO if path is None else path)
+    p = plan_obj if plan_obj is not None else _plan_cached(
+        M, N, K, group_size, _native.PATH_AUTO if path is None else path, dev)
+    ws_bytes = int(p.workspace_bytes)
     ws = _workspace(dev, ws_bytes) if ws_bytes else None
     if ws is not None:
         ws_bytes = ws.numel() * 4
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    args = (_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out), M, N, K, group_size,
-            _ptr(ws), ws_bytes)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         if bias is not None or residual is not None:
             st = L.awq_w4a16_gemm_epilogue(_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(bias),
                                            _ptr(residual), _ptr(out), M, N, K, group_size, _ptr(ws), ws_bytes,
-                                           ctypes.byref(plan_obj), stream)
+                                           ctypes.byref(p), stream)
             where = "awq_w4a16_gemm_epilogue"
-        elif plan_obj is not None:
-            st = L.awq_w4a16_gemm_planned(*args, ctypes.byref(plan_obj), stream)
-            where = "awq_w4a16_gemm_planned"
-        elif path is None:
-            st = L.awq_w4a16_gemm(*args, stream)
-            where = "awq_w4a16_gemm"
         else:
-            st = L.awq_w4a16_gemm_ex(*args, path, stream)
-            where = "awq_w4a16_gemm_ex"
+            st = L.awq_w4a16_gemm_planned(_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out),
+                                          M, N, K, group_size, _ptr(ws), ws_bytes, ctypes.byref(p), stream)
+            where = "awq_w4a16_gemm_planned"
     _native.check(st, where)
 
 
@@ -178,6 +220,14 @@ def awq_gemm_forward_ex(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Te
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
     elif out.dtype != torch.float16 or out.numel() != M * N or not out.is_contiguous() or out.device != dev:
         raise ValueError("out must be a contiguous fp16 [M, N] tensor on the operands' device")
+    elif out.data_ptr() % 16 != 0:
+        # The kernels store 16-byte vectors: compute into an aligned buffer and copy back.
+        if residual is not None and residual.data_ptr() == out.data_ptr():
+            residual = residual.clone()
+        tmp = awq_gemm_forward_ex(x, qweight, qzeros, scales, group_size, path=path, plan_obj=plan_obj,
+                                  bias=bias, residual=residual)
+        out.view(tmp.shape).copy_(tmp)
+        return out.view(*in_shape[:-1], N)
     if bias is not None:
         if bias.dtype != torch.float16 or bias.numel() != N or bias.device != dev:
             raise ValueError(f"bias must be an fp16 [N={N}] tensor on {dev}")
@@ -202,9 +252,9 @@ def _dequant_to_fp16(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.
     dev = _check_device(qweight, qzeros, scales, out_buf)
     if out_buf.dtype != torch.float16 or tuple(out_buf.shape) != (K, N) or not out_buf.is_contiguous():
         raise ValueError(f"out_buf must be a contiguous fp16 tensor of shape {(K, N)}")
-    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
+    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), _aligned16(scales.contiguous())
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         st = _native.lib().awq_w4a16_dequant(_ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out_buf),
                                              N, K, group_size, stream)
     _native.check(st, "awq_w4a16_dequant")

@@ -23,7 +23,7 @@ import ctypes
 import torch
 
 from . import _native
-from .awq_gemm import _check_device, _ptr
+from .awq_gemm import _check_device, _ptr, _OnDevice, _aligned16
 
 __all__ = ["lm_head_forward", "MAX_ROWS"]
 
@@ -42,17 +42,17 @@ def lm_head_forward(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | N
         raise ValueError(f"x has K = {x.shape[-1]}, weight has K = {K}")
     dev = _check_device(x, weight)
     in_shape = x.shape
-    x_flat = x.reshape(-1, K).contiguous()
+    x_flat = _aligned16(x.reshape(-1, K).contiguous())
     M = x_flat.shape[0]
     if M > MAX_ROWS:
         raise ValueError(f"lm_head_forward serves at most {MAX_ROWS} rows, got {M}")
-    weight = weight.contiguous()
+    weight = _aligned16(weight.contiguous())
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
     elif out.dtype != torch.float16 or tuple(out.shape) != (M, N) or not out.is_contiguous() or out.device != dev:
         raise ValueError("out must be a contiguous fp16 [M, N] tensor on the operands' device")
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         st = _native.lib().awq_fp16_linear(_ptr(x_flat), _ptr(weight), _ptr(out), M, N, K, stream)
     if st in (_native.AWQ_ERR_BAD_DIMS, _native.AWQ_ERR_TOO_LARGE, _native.AWQ_ERR_PATH,
               _native.AWQ_ERR_MISALIGNED):

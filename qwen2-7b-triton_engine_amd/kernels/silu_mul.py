@@ -16,7 +16,7 @@ import ctypes
 import torch
 
 from . import _native
-from .awq_gemm import _check_device, _ptr
+from .awq_gemm import _check_device, _ptr, _OnDevice, _aligned16
 
 __all__ = ["silu_mul_gate_up", "silu_mul_forward"]
 
@@ -30,14 +30,14 @@ def silu_mul_gate_up(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> 
         raise ValueError(f"the last dimension (2I = {two_i}) must be a multiple of 16")
     dev = _check_device(gate_up)
     I = two_i // 2
-    g = gate_up.reshape(-1, two_i).contiguous()
+    g = _aligned16(gate_up.reshape(-1, two_i).contiguous())
     M = g.shape[0]
     if out is None:
         out = torch.empty((M, I), dtype=torch.float16, device=dev)
     elif out.dtype != torch.float16 or out.numel() != M * I or not out.is_contiguous() or out.device != dev:
         raise ValueError("out must be a contiguous fp16 tensor of M*I elements on the operand's device")
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         st = _native.lib().awq_silu_mul(_ptr(g), _ptr(out), M, I, stream)
     _native.check(st, "awq_silu_mul")
     return out.view(*gate_up.shape[:-1], I)

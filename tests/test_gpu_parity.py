@@ -448,7 +448,11 @@ def test_split_k_workspace_left_zero(gpu):
     """Every split-K finish leaves the counter block and the fixed-point
     slot region of the shared workspace zero (arrival counters reset, slots
     cleared), so it is ready for the next call of any path and for graph
-    replays; the partials region is rewritten by every call that reads it."""
+    replays.  The partials region is never cleared: every call writes each
+    partial it reads.  To show that no finish reads a partial before writing
+    it, each case runs on a zeroed workspace, then again with the whole
+    partials region filled with NaN, and the two outputs must be finite and
+    bit-identical."""
     from kernels import awq_gemm as G
     k, n = 3584, 4608
     cases = [(m, _native.plan_for(m, n, k, path=path))
@@ -457,18 +461,25 @@ def test_split_k_workspace_left_zero(gpu):
     cases += [(m, _native.plan_stream(m, n, k, 4, sp, variant=v)) for m, v, sp in ((2, 1, 28), (4, 2, 8), (16, 2, 2))]
     cases += [(m, _native.plan_stream(m, n, k, kw, sp, variant=v, layout="row", depth=d))
               for m, v, sp, kw, d in ((3, 1, 28, 8, 1), (5, 2, 6, 8, 2), (8, 3, 28, 8, 1))]
+    cases += [(m, _native.plan_stream(m, n, k, 3, 14, variant=3)) for m in (9, 16)]
+    cases += [(m, _native.plan_gemv(m, n, k, 16, 8, variant=2, split_k=sp, depth=3)) for m, sp in ((1, 7), (2, 14))]
     cases += [(m, _native.plan_tile(m, n, k, v, sp)) for m, v, sp in
               ((100, 6, 4), (200, 7, 3), (100, 8, 4), (70, 9, 7), (2048, 13, 2), (2048, 14, 3))]
+    ws = G._workspace(gpu, max(int(p.workspace_bytes) for _, p in cases))
+    kept_zero = (_native.counter_bytes() + _native.SLOT_BYTES) // 4
     for m, p in cases:
         x, qw, qz, s = O.make_inputs(m, k, n, seed=6)
         assert p.split_k > 1, (m, p.path)
-        name = f"{_native.PATH_NAMES[p.path]} v={p.variant}"
-        print(f"workspace check M={m} path={name} split={p.split_k}", flush=True)
+        name = f"{_native.PATH_NAMES[p.path]} v={p.variant} M={m} split={p.split_k}"
+        print(f"workspace check {name}", flush=True)
+        ws.zero_()
         y = _run(gpu, x, qw, qz, s, plan_obj=p)
-        ws = G._workspaces[gpu.index][-1]
-        kept_zero = (_native.counter_bytes() + _native.SLOT_BYTES) // 4
+        assert G._workspaces[gpu.index][-1] is ws, "the workspace was replaced"
         assert int((ws.view(torch.int32)[:kept_zero] != 0).sum().item()) == 0, name
+        ws[kept_zero:].fill_(float("nan"))
         y2 = _run(gpu, x, qw, qz, s, plan_obj=p)
+        assert int((ws.view(torch.int32)[:kept_zero] != 0).sum().item()) == 0, name
+        assert np.isfinite(y).all() and np.isfinite(y2).all(), name
         assert np.array_equal(y.view(np.uint16), y2.view(np.uint16)), name
 
 
@@ -503,6 +514,38 @@ def test_noncontiguous_operands(gpu):
     x_wide[:, :k] = _t(x, gpu)
     y = awq_gemm_forward(x_wide[:, :k], qw_t, _t(qz, gpu), s_t)
     _assert_close(y.cpu().numpy(), y_ref, "non-contiguous")
+
+
+def test_misaligned_operands_are_copied(gpu):
+    """x, scales and a caller's out= at storage offsets that are not 16-byte
+    aligned (the reference's Triton path takes any fp16 view): the entry
+    points copy to aligned buffers instead of raising, and the results are
+    bit-identical to the aligned call, including an in-place residual add
+    into a misaligned out."""
+    k, n, m = 3584, 4608, 3
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=17)
+    X, QW, QZ, S = (_t(a, gpu) for a in (x, qw, qz, s))
+    want = awq_gemm_forward(X, QW, QZ, S)
+    xbuf = torch.empty(m * k + 1, dtype=torch.float16, device=gpu)
+    xo = xbuf[1:].view(m, k)
+    xo.copy_(X)
+    sbuf = torch.empty(S.numel() + 3, dtype=torch.float16, device=gpu)
+    so = sbuf[3:].view(S.shape)
+    so.copy_(S)
+    assert xo.data_ptr() % 16 and so.data_ptr() % 16
+    for xx, ss, what in ((xo, S, "x"), (X, so, "scales"), (xo, so, "x and scales")):
+        got = awq_gemm_forward(xx, QW, QZ, ss)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), what
+    obuf = torch.empty(m * n + 1, dtype=torch.float16, device=gpu)
+    oo = obuf[1:].view(m, n)
+    got = awq_gemm_forward_ex(xo, QW, QZ, S, out=oo)
+    assert got.data_ptr() == oo.data_ptr() and torch.equal(oo, want), "out="
+    res = torch.randn((m, n), device=gpu).half()
+    oo.copy_(res)
+    awq_gemm_forward_ex(X, QW, QZ, S, out=oo, residual=oo)
+    torch.cuda.synchronize()
+    assert torch.equal(oo, (res.float() + want.float()).half()), "out= with residual=out"
 
 
 def test_errors_raise(gpu):

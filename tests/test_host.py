@@ -55,7 +55,8 @@ def test_abi_version_and_error_strings(L):
     assert L.awq_w4a16_abi_version() == _native.ABI_VERSION
     codes = [_native.AWQ_OK, _native.AWQ_ERR_NULL_POINTER, _native.AWQ_ERR_BAD_DIMS,
              _native.AWQ_ERR_GROUP_SIZE, _native.AWQ_ERR_MISALIGNED, _native.AWQ_ERR_WORKSPACE,
-             _native.AWQ_ERR_LAUNCH, _native.AWQ_ERR_PATH, _native.AWQ_ERR_TOO_LARGE]
+             _native.AWQ_ERR_LAUNCH, _native.AWQ_ERR_PATH, _native.AWQ_ERR_TOO_LARGE,
+             _native.AWQ_ERR_SCRATCH, _native.AWQ_ERR_CAPTURE]
     msgs = [_native.error_string(c) for c in codes]
     assert len(set(msgs)) == len(msgs)
     assert _native.error_string(-99) == "unknown status"
@@ -444,3 +445,56 @@ def test_greedy_token_is_first_argmax():
             if t % 3 == 0:
                 x[torch.randint(0, n, (3,), generator=g)] = x.max()
             assert int(_greedy_token(x)) == int(torch.argmax(x)), (n, t)
+
+
+def test_greedy_token_non_finite_logits():
+    """NaN and +-inf logits: the pick is torch.argmax's (a NaN counts as the
+    largest value, its first occurrence wins; +inf beats every finite logit;
+    an all -inf row gives index 0), and it is always inside the vocabulary."""
+    sys.path.insert(0, os.path.join(ROOT, "qwen2-7b-triton_engine_amd"))
+    from engine.qwen2_decode import _greedy_token
+
+    g = torch.Generator().manual_seed(1)
+    for n in (256, 257, 1000, 152064):
+        cases = []
+        x = torch.randn(n, generator=g).half()
+        x[n // 3] = float("nan")
+        cases.append(x)
+        x = torch.randn(n, generator=g).half()
+        x[n - 1] = float("nan")
+        x[n // 2] = float("nan")
+        cases.append(x)
+        x = torch.randn(n, generator=g).half()
+        x[n // 5] = float("inf")
+        x[n // 4] = float("inf")
+        cases.append(x)
+        x = torch.randn(n, generator=g).half()
+        x[n // 7] = float("inf")
+        x[n - 2] = float("nan")
+        cases.append(x)
+        cases.append(torch.full((n,), float("-inf")).half())
+        x = torch.full((n,), float("-inf")).half()
+        x[n - 1] = -1.0
+        cases.append(x)
+        cases.append(torch.full((n,), float("nan")).half())
+        for i, x in enumerate(cases):
+            got = int(_greedy_token(x))
+            assert 0 <= got < n, (n, i, got)
+            assert got == int(torch.argmax(x)), (n, i, got, int(torch.argmax(x)))
+
+
+def test_checked_token_clamps_and_counts():
+    """The decode step's token guard: tokens inside the vocabulary pass
+    unchanged and leave the flag alone; a token below 0 or at / past the
+    vocabulary size is clamped into range and counted in the flag."""
+    sys.path.insert(0, os.path.join(ROOT, "qwen2-7b-triton_engine_amd"))
+    from engine.qwen2_decode import _checked_token
+
+    bad = torch.zeros(1, dtype=torch.int32)
+    for t in (0, 1, 151999, 152063):
+        out = _checked_token(torch.tensor([t]), 152064, bad)
+        assert int(out) == t and int(bad) == 0
+    expected = {-1: 0, -(2**40): 0, 152064: 152063, 152065: 152063, 2**62: 152063}
+    for i, (t, want) in enumerate(expected.items()):
+        out = _checked_token(torch.tensor([t]), 152064, bad)
+        assert int(out) == want and int(bad) == i + 1, (t, int(out), int(bad))

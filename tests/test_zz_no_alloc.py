@@ -10,6 +10,9 @@ a smaller input, and checks both: a scratch left dirty by the first call
 (counters, fixed-point slots, partials) would corrupt the second.
 """
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -105,3 +108,70 @@ def test_noalloc_repeats_and_graph_replay(gpu):
         eager = _noalloc(x[:4].contiguous(), qw, qz, s)
         torch.cuda.synchronize()
         assert torch.equal(eager, awq_gemm_forward(x[:4], qw, qz, s))
+
+
+_FRESH_PROCESS = r"""
+import ctypes, sys
+sys.path[:0] = sys.argv[1:3]
+import torch
+from kernels import _native
+from kernels.awq_gemm import awq_gemm_forward
+
+dev = torch.device("cuda:0")
+k, n, m = 3584, 4608, 16
+g = torch.Generator(device=dev)
+g.manual_seed(3)
+qw = torch.randint(-2**31, 2**31 - 1, (k, n // 8), generator=g, device=dev, dtype=torch.int32)
+qz = torch.randint(-2**31, 2**31 - 1, (k // 128, n // 8), generator=g, device=dev, dtype=torch.int32)
+s = (torch.rand((k // 128, n), generator=g, device=dev) * 0.018 + 0.002).half()
+x = torch.randn((m, k), generator=g, device=dev).half()
+out = torch.zeros((m, n), dtype=torch.float16, device=dev)
+assert _native.plan_for(m, n, k).workspace_bytes > 0
+P = lambda t: ctypes.c_void_p(t.data_ptr())
+L = _native.lib()
+
+def call(stream):
+    return L.awq_w4a16_gemm_noalloc(P(x), P(qw), P(qz), P(s), P(out), m, n, k, 128,
+                                    ctypes.c_void_p(stream.cuda_stream))
+
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=side):
+    out.zero_()
+    st_captured_first = call(side)
+torch.cuda.synchronize()
+print("first call under capture:", st_captured_first, flush=True)
+assert st_captured_first == _native.AWQ_ERR_CAPTURE, st_captured_first
+st = call(torch.cuda.current_stream())
+torch.cuda.synchronize()
+assert st == _native.AWQ_OK, st
+ref = awq_gemm_forward(x, qw, qz, s)
+torch.cuda.synchronize()
+assert torch.equal(out, ref)
+graph2 = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph2, stream=side):
+    st2 = call(side)
+assert st2 == _native.AWQ_OK, st2
+for i in range(3):
+    out.zero_()
+    graph2.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), i
+print("ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_is_refused(gpu):
+    """In a fresh process (no earlier call has set the scratch up): the first
+    split-K call of the allocation-free entry point, made under graph
+    capture, is refused with AWQ_ERR_CAPTURE and records nothing; after one
+    eager call on the device (which sets the scratch up) the same call
+    matches awq_w4a16_gemm and can be captured and replayed."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "qwen2-7b-triton_engine_amd")
+    print("noalloc capture refusal: fresh process", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FRESH_PROCESS, pkg, root], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
