@@ -45,31 +45,35 @@ from . import _native
 __all__ = ["awq_gemm_forward", "awq_gemm_forward_ex", "_dequant_to_fp16", "plan"]
 
 
+_F16, _I32 = torch.float16, torch.int32
+
+
 def _check_operands(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
                     scales: torch.Tensor, group_size: int):
     """Shape/dtype checks shared by every entry point; returns (K, N)."""
-    if x.dtype != torch.float16:
+    if x.dtype is not _F16:
         raise ValueError(f"x must be float16, got {x.dtype}")
-    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
+    if qweight.dtype is not _I32 or qzeros.dtype is not _I32:
         raise ValueError(f"qweight/qzeros must be int32, got {qweight.dtype}/{qzeros.dtype}")
-    if scales.dtype != torch.float16:
+    if scales.dtype is not _F16:
         raise ValueError(f"scales must be float16, got {scales.dtype}")
-    if qweight.dim() != 2 or qzeros.dim() != 2 or scales.dim() != 2 or x.dim() < 1:
-        raise ValueError("qweight, qzeros and scales must be 2-D and x at least 1-D")
     if group_size != 128:
         raise ValueError(f"group_size {group_size} is not served (only 128)")
+    ws, zs, ss = qweight.shape, qzeros.shape, scales.shape
+    if len(ws) != 2 or len(zs) != 2 or len(ss) != 2 or x.dim() < 1:
+        raise ValueError("qweight, qzeros and scales must be 2-D and x at least 1-D")
     K = x.shape[-1]
-    N = scales.shape[1]
+    N = ss[1]
     if N % 8 != 0 or N == 0:
         raise ValueError(f"N = scales.shape[1] = {N} must be a positive multiple of 8")
     if K == 0 or K % group_size != 0:
         raise ValueError(f"K = {K} must be a positive multiple of group_size {group_size}")
-    if tuple(qweight.shape) != (K, N // 8):
-        raise ValueError(f"qweight shape {tuple(qweight.shape)} != (K, N/8) = {(K, N // 8)}")
-    if tuple(qzeros.shape) != (K // group_size, N // 8):
-        raise ValueError(f"qzeros shape {tuple(qzeros.shape)} != (K/G, N/8) = {(K // group_size, N // 8)}")
-    if tuple(scales.shape) != (K // group_size, N):
-        raise ValueError(f"scales shape {tuple(scales.shape)} != (K/G, N) = {(K // group_size, N)}")
+    if ws != (K, N // 8):
+        raise ValueError(f"qweight shape {tuple(ws)} != (K, N/8) = {(K, N // 8)}")
+    if zs != (K // group_size, N // 8):
+        raise ValueError(f"qzeros shape {tuple(zs)} != (K/G, N/8) = {(K // group_size, N // 8)}")
+    if ss != (K // group_size, N):
+        raise ValueError(f"scales shape {tuple(ss)} != (K/G, N) = {(K // group_size, N)}")
     return K, N
 
 
@@ -120,12 +124,28 @@ def _prepare(x, qweight, qzeros, scales, group_size):
     K, N = _check_operands(x, qweight, qzeros, scales, group_size)
     dev = _check_device(x, qweight, qzeros, scales)
     in_shape = x.shape
-    x_flat = _aligned16(x.reshape(-1, K).contiguous())          # kernels/awq_gemm.py:244-246
+    x_flat = x if len(in_shape) == 2 else x.reshape(-1, K)     # kernels/awq_gemm.py:244-246
     # The reference passes strides to Triton; the C ABI takes dense operands.
+    x_flat = _aligned16(x_flat.contiguous())
     qweight = qweight.contiguous()
     qzeros = qzeros.contiguous()
     scales = _aligned16(scales.contiguous())
     return in_shape, x_flat, qweight, qzeros, scales, K, N, dev
+
+
+def _shaped(out: torch.Tensor, in_shape, N: int) -> torch.Tensor:
+    """``out`` [M, N] viewed as ``[*in_shape[:-1], N]`` (kernels/awq_gemm.py:284)."""
+    return out if len(in_shape) == 2 else out.view(*in_shape[:-1], N)
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_handle(dev: torch.device) -> int:
+    """The current stream of ``dev`` as a raw hipStream_t value."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index)
+    return torch.cuda.current_stream(dev).cuda_stream
 
 
 # Plans of the AUTO dispatcher (or a forced path) per (M, N, K, group size,
@@ -159,39 +179,46 @@ class _OnDevice:
         return False
 
 
-def _plan_cached(M: int, N: int, K: int, group_size: int, path: int, dev: torch.device) -> "_native.Plan":
+def _plan_cached(M: int, N: int, K: int, group_size: int, path: int, dev: torch.device):
+    """(plan, ctypes reference to it) for the shape on ``dev``."""
     key = (M, N, K, group_size, path, dev.index)
-    p = _plans.get(key)
-    if p is None:
+    e = _plans.get(key)
+    if e is None:
         with _OnDevice(dev):
             p = _native.plan_for(M, N, K, group_size, path)
         if len(_plans) >= _PLAN_CACHE_MAX:
             _plans.clear()
-        _plans[key] = p
-    return p
+        e = _plans[key] = (p, ctypes.byref(p))
+    return e
 
 
 def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path=None, plan_obj=None,
             bias=None, residual=None):
     L = _native.lib()
-    p = plan_obj if plan_obj is not None else _plan_cached(
-        M, N, K, group_size, _native.PATH_AUTO if path is None else path, dev)
-    ws_bytes = int(p.workspace_bytes)
-    ws = _workspace(dev, ws_bytes) if ws_bytes else None
-    if ws is not None:
-        ws_bytes = ws.numel() * 4
-    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    if plan_obj is not None:
+        p, pref = plan_obj, ctypes.byref(plan_obj)
+    else:
+        p, pref = _plan_cached(M, N, K, group_size, _native.PATH_AUTO if path is None else path, dev)
+    ws_bytes = p.workspace_bytes
+    ws_ptr = 0
+    if ws_bytes:
+        ws = _workspace(dev, ws_bytes)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel() * 4
+    stream = _stream_handle(dev)
     with _OnDevice(dev):
         if bias is not None or residual is not None:
-            st = L.awq_w4a16_gemm_epilogue(_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(bias),
-                                           _ptr(residual), _ptr(out), M, N, K, group_size, _ptr(ws), ws_bytes,
-                                           ctypes.byref(p), stream)
+            st = L.awq_w4a16_gemm_epilogue(x_flat.data_ptr(), qweight.data_ptr(), qzeros.data_ptr(),
+                                           scales.data_ptr(), 0 if bias is None else bias.data_ptr(),
+                                           0 if residual is None else residual.data_ptr(), out.data_ptr(),
+                                           M, N, K, group_size, ws_ptr, ws_bytes, pref, stream)
             where = "awq_w4a16_gemm_epilogue"
         else:
-            st = L.awq_w4a16_gemm_planned(_ptr(x_flat), _ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(out),
-                                          M, N, K, group_size, _ptr(ws), ws_bytes, ctypes.byref(p), stream)
+            st = L.awq_w4a16_gemm_planned(x_flat.data_ptr(), qweight.data_ptr(), qzeros.data_ptr(),
+                                          scales.data_ptr(), out.data_ptr(), M, N, K, group_size, ws_ptr,
+                                          ws_bytes, pref, stream)
             where = "awq_w4a16_gemm_planned"
-    _native.check(st, where)
+    if st:
+        _native.check(st, where)
 
 
 def awq_gemm_forward(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
@@ -199,9 +226,9 @@ def awq_gemm_forward(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tenso
     """``x @ dequant(qweight, qzeros, scales)`` in fp16 (kernels/awq_gemm.py:237-284)."""
     in_shape, x_flat, qweight, qzeros, scales, K, N, dev = _prepare(x, qweight, qzeros, scales, group_size)
     M = x_flat.shape[0]
-    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    out = torch.empty((M, N), dtype=_F16, device=dev)
     _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev)
-    return out.view(*in_shape[:-1], N)
+    return _shaped(out, in_shape, N)
 
 
 def awq_gemm_forward_ex(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
