@@ -36,8 +36,14 @@
  * clamps each workgroup's partial sum to +-2^22 and turns a NaN partial
  * into +2^22, so a NaN or an infinity in x gives +-inf (never NaN) on those
  * paths -- except that a +inf and a -inf partial of different splits cancel,
- * so such an output can come out finite where the reference gives NaN;
- * partials are added in 2^-24 steps.
+ * so such an output can come out finite where the reference gives NaN.
+ * The clamp can also change a finite result without a sign: partials of
+ * opposite signs beyond 2^22 in magnitude (+5e6 and -4.99e6, say) are added
+ * as +-2^22 and give 0 where the fp32 sum is about 1e4.  Partials that large
+ * need |x| * |(q - z) * s| summed over one split's rows to exceed 4 million
+ * (AWQ scales are below 1, q - z at most 15), far outside fp16 activations
+ * of a working model; the other finishes have no such limit.  Partials are
+ * added in 2^-24 steps.
  */
 #ifndef AWQ_W4A16_H
 #define AWQ_W4A16_H
