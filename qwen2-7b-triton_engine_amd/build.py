@@ -1,8 +1,10 @@
 """Build recipe for the W4A16 AWQ HIP library (gfx950).
 
 ``python qwen2-7b-triton_engine_amd/build.py`` compiles every ``csrc/*.hip``
-with hipcc for gfx950 and links ``lib/libawq_w4a16.so``.  Objects go to
-``_build/`` next to this file.  hipcc cross-compiles without a GPU.
+with hipcc for gfx950 and links ``lib/libawq_w4a16.so``, then compiles the
+torch binding of the eager entry point (``csrc/awq_torch_binding.cpp``, host
+C++) into ``lib/_awq_torch*.so``.  Objects go to ``_build/`` next to this
+file.  hipcc cross-compiles without a GPU.
 """
 from __future__ import annotations
 
@@ -66,6 +68,42 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
+# The torch binding of the eager entry point (csrc/awq_torch_binding.cpp):
+# host C++ against torch's headers and libraries, linked to the library
+# above and found next to it at run time.
+BINDING_SRC = os.path.join(CSRC, "awq_torch_binding.cpp")
+
+
+def _binding_path() -> str:
+    import sysconfig
+    return os.path.join(LIB_DIR, "_awq_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_binding(verbose: bool = False) -> str:
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    out = _binding_path()
+    tmp = out + ".tmp"
+    torch_lib = cpp_extension.library_paths()[0]
+    incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], "/opt/rocm/include"]
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+           "-DTORCH_EXTENSION_NAME=_awq_torch", "-DTORCH_API_INCLUDE_EXTENSION_H", "-D__HIP_PLATFORM_AMD__=1",
+           "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-isystem{d}" for d in incs], BINDING_SRC, "-o", tmp,
+           f"-L{LIB_DIR}", "-lawq_w4a16", f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"building the torch binding failed:\n{r.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
@@ -78,6 +116,7 @@ def build(verbose: bool = False) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    build_binding(verbose)
     return LIB
 
 

@@ -95,6 +95,34 @@ SIGNATURES = {
 }
 
 _lib = None
+_binding = None
+
+
+def binding():
+    """The torch binding of the eager entry point (``lib/_awq_torch*.so``,
+    built from ``csrc/awq_torch_binding.cpp``): ``awq_gemm_forward`` with
+    checks, allocation, plan and workspace in C++, and the per-device
+    workspace registry every entry point shares.  Missing, it raises: there
+    is no fallback path."""
+    global _binding
+    if _binding is None:
+        import importlib.util
+        import sysconfig
+
+        import torch  # noqa: F401  (the binding links torch's libraries)
+
+        lib()  # the C ABI it calls, ABI-checked first
+        path = os.path.join(_PKG_ROOT, "lib", "_awq_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+        if not os.path.exists(path):
+            raise RuntimeError(f"torch binding not found at {path}; build it with "
+                               "`python qwen2-7b-triton_engine_amd/build.py` (there is no fallback path)")
+        spec = importlib.util.spec_from_file_location("_awq_torch", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        if mod.abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{path} was built against ABI {mod.abi_version()}, expected {ABI_VERSION}")
+        _binding = mod
+    return _binding
 
 
 class AwqNativeError(RuntimeError):

@@ -25,9 +25,10 @@ Triton, no torch dequant and no other fallback: without the HIP library the
 call raises.
 
 Workspace: like the reference's module-global ``_dequant_buffer``
-(kernels/awq_gemm.py:234,255-262) the module keeps one buffer per device,
-grown on demand -- here it holds split-K partial sums and the kernels'
-arrival counters (zero-filled once; each call leaves them zero).  Calls that
+(kernels/awq_gemm.py:234,255-262) one buffer per device, grown on demand,
+held by the torch binding's registry and shared by every entry point -- here
+it holds split-K partial sums, the kernels' arrival counters and fixed-point
+slots (zero-filled once; each call leaves the counters and slots zero).  Calls that
 share a device must therefore not run concurrently on different streams, the
 same single-stream use the reference makes of its buffer.  The buffer is
 graph-capture safe once it is large enough: capture after one eager call of
@@ -91,24 +92,18 @@ def _ptr(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
 
 
-# Per-device workspace buffers.  Earlier (smaller) buffers stay referenced so
-# that graphs captured with them keep valid memory.
-_workspaces: dict = {}
-_WS_ALIGN = 1 << 20
-
-
+# Per-device workspace buffers live in the torch binding's registry, shared
+# by every entry point; earlier (smaller) buffers stay referenced so that
+# graphs captured with them keep valid memory.
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    bufs = _workspaces.setdefault(dev.index, [])
-    if bufs and bufs[-1].numel() * 4 >= nbytes:
-        return bufs[-1]
-    if torch.cuda.is_current_stream_capturing():
-        raise RuntimeError(
-            f"awq_gemm workspace must grow to {nbytes} bytes during graph capture; run the "
-            "largest shape once eagerly before capturing")
-    size = (nbytes + _WS_ALIGN - 1) // _WS_ALIGN * _WS_ALIGN
-    buf = torch.zeros(size // 4, dtype=torch.float32, device=dev)
-    bufs.append(buf)
-    return buf
+    """The device's workspace buffer, grown to at least ``nbytes`` (zero
+    filled; refused while the current stream is being captured)."""
+    return _native.binding().workspace(dev.index, int(nbytes))
+
+
+def _workspace_buffers(dev: torch.device) -> list:
+    """Every workspace buffer the device holds, oldest first."""
+    return _native.binding().workspace_buffers(dev.index)
 
 
 def _aligned16(t: torch.Tensor) -> torch.Tensor:
@@ -223,12 +218,19 @@ def _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev, path
 
 def awq_gemm_forward(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,
                      scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
-    """``x @ dequant(qweight, qzeros, scales)`` in fp16 (kernels/awq_gemm.py:237-284)."""
-    in_shape, x_flat, qweight, qzeros, scales, K, N, dev = _prepare(x, qweight, qzeros, scales, group_size)
-    M = x_flat.shape[0]
-    out = torch.empty((M, N), dtype=_F16, device=dev)
-    _launch(x_flat, qweight, qzeros, scales, out, M, N, K, group_size, dev)
-    return _shaped(out, in_shape, N)
+    """``x @ dequant(qweight, qzeros, scales)`` in fp16 (kernels/awq_gemm.py:237-284).
+
+    One call into the torch binding: the same checks as ``awq_gemm_forward_ex``
+    (ValueError for a bad operand), the [M, K] flattening, the fp16 output, the
+    AUTO plan (cached per shape and device), the shared workspace and the
+    current stream, then the C ABI's ``awq_w4a16_gemm_planned``."""
+    return _gemm(x, qweight, qzeros, scales, group_size)
+
+
+def _gemm(x, qweight, qzeros, scales, group_size):
+    global _gemm
+    _gemm = _native.binding().awq_gemm_forward   # bound once: later calls go straight to C++
+    return _gemm(x, qweight, qzeros, scales, group_size)
 
 
 def awq_gemm_forward_ex(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor,

@@ -474,7 +474,7 @@ def test_split_k_workspace_left_zero(gpu):
         print(f"workspace check {name}", flush=True)
         ws.zero_()
         y = _run(gpu, x, qw, qz, s, plan_obj=p)
-        assert G._workspaces[gpu.index][-1] is ws, "the workspace was replaced"
+        assert G._workspace_buffers(gpu)[-1].data_ptr() == ws.data_ptr(), "the workspace was replaced"
         assert int((ws.view(torch.int32)[:kept_zero] != 0).sum().item()) == 0, name
         ws[kept_zero:].fill_(float("nan"))
         y2 = _run(gpu, x, qw, qz, s, plan_obj=p)

@@ -498,3 +498,35 @@ def test_checked_token_clamps_and_counts():
     for i, (t, want) in enumerate(expected.items()):
         out = _checked_token(torch.tensor([t]), 152064, bad)
         assert int(out) == want and int(bad) == i + 1, (t, int(out), int(bad))
+
+
+def test_torch_binding_loads_and_checks_operands():
+    """The torch binding of the eager entry point loads next to the library,
+    was built against the same ABI, and refuses bad operands with the same
+    ValueErrors as the Python checks before touching a GPU (here the operands
+    are CPU tensors, so even good ones end at the device check)."""
+    from kernels.awq_gemm import awq_gemm_forward
+
+    b = _native.binding()
+    assert b.abi_version() == _native.ABI_VERSION
+    for name in ("awq_gemm_forward", "workspace", "workspace_buffers"):
+        assert hasattr(b, name)
+    k, n = 256, 64
+    x = torch.zeros((2, k), dtype=torch.float16)
+    qw = torch.zeros((k, n // 8), dtype=torch.int32)
+    qz = torch.zeros((k // 128, n // 8), dtype=torch.int32)
+    s = torch.zeros((k // 128, n), dtype=torch.float16)
+    cases = [
+        ((x.float(), qw, qz, s, 128), "x must be float16"),
+        ((x, qw.float(), qz, s, 128), "qweight/qzeros must be int32"),
+        ((x, qw, qz, s.float(), 128), "scales must be float16"),
+        ((x, qw, qz, s, 64), "group_size 64 is not served"),
+        ((x, qw[:, :4], qz, s, 128), "qweight shape"),
+        ((x, qw, qz[:1], s, 128), "qzeros shape"),
+        ((x[:, :200], qw, qz, s, 128), "must be a positive multiple of group_size"),
+        ((x, qw, qz, s[:, :60], 128), "must be a positive multiple of 8"),
+        ((x, qw, qz, s, 128), "operands must be on a ROCm device"),
+    ]
+    for args, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            awq_gemm_forward(*args)
