@@ -464,6 +464,18 @@ def main():
     log(f"decode step: {t_step * 1e3:.3f} ms, {value:.1f} GB/s ({value / (HBM_PEAK_BPS / 1e9):.3f} of HBM peak)")
     del g
 
+    # The same step as eager calls, the way the reference engine issues them (no graph):
+    # wall time of `steps` steps after `warmup` eager ones, synchronised on both sides.
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t_eager = (time.perf_counter() - t0) / args.steps
+    log(f"decode step, eager calls: {t_eager * 1e3:.3f} ms, {step_bytes / t_eager / 1e9:.1f} GB/s")
+
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -486,6 +498,9 @@ def main():
         },
         "roofline": None,
         "cpu_baseline": None,
+        "eager_step": {"ms_per_step": round(t_eager * 1e3, 4), "GBps": round(step_bytes / t_eager / 1e9, 2),
+                       "note": "the same 336 GEMMs as awq_gemm_forward calls issued eagerly (the reference "
+                               "engine's usage), wall time per step"},
     }
 
     # ---- per-GEMM times: each (M, shape) over >= 640 MB of weights in one graph
