@@ -1,0 +1,102 @@
+"""The eager entry point through the torch binding (csrc/awq_torch_binding.cpp)
+against the same AUTO plan through the ctypes path (awq_gemm_forward_ex):
+bit-identical outputs on every decode and prefill route, leading batch
+dimensions, M = 0, non-contiguous and misaligned operands; the binding's
+workspace registry is the one the ctypes path uses; growing it under graph
+capture is refused, and a capture after an eager warm-up replays correctly."""
+import numpy as np
+import pytest
+import torch
+
+from kernels import _native
+from kernels.awq_gemm import _workspace_buffers, awq_gemm_forward, awq_gemm_forward_ex
+from oracle import awq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 3584, 4608), (2, 3584, 3584), (4, 3584, 37888), (7, 18944, 3584),
+                                   (16, 3584, 4608), (16, 18944, 3584), (33, 1024, 1032), (300, 3584, 3584),
+                                   (2048, 3584, 4608), (5, 512, 264)])
+def test_binding_equals_ctypes_path(gpu, m, k, n):
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=m + k + n)
+    X, QW, QZ, S = (_t(a, gpu) for a in (x, qw, qz, s))
+    p = _native.plan_for(m, n, k)
+    print(f"binding M={m} K={k} N={n} path={_native.PATH_NAMES[p.path]} v{p.variant} split={p.split_k}", flush=True)
+    y = awq_gemm_forward(X, QW, QZ, S)
+    y2 = awq_gemm_forward_ex(X, QW, QZ, S, 128)
+    torch.cuda.synchronize()
+    assert y.shape == (m, n) and y.dtype == torch.float16
+    assert torch.equal(y, y2)
+    if m <= 64:
+        err = O.max_rel_err(y.cpu().numpy(), O.awq_gemm_oracle(x, qw, qz, s))
+        assert err <= 1e-2, err
+
+
+def test_binding_shapes_views_and_alignment(gpu):
+    k, n = 3584, 4608
+    x, qw, qz, s = O.make_inputs(6, k, n, seed=9)
+    X, QW, QZ, S = (_t(a, gpu) for a in (x, qw, qz, s))
+    want = awq_gemm_forward_ex(X, QW, QZ, S, 128)
+    y3 = awq_gemm_forward(X.view(2, 3, k), QW, QZ, S)
+    assert y3.shape == (2, 3, n) and torch.equal(y3.reshape(6, n), want)
+    wide = torch.zeros((6, 2 * k), dtype=torch.float16, device=gpu)
+    wide[:, :k] = X
+    assert torch.equal(awq_gemm_forward(wide[:, :k], QW, QZ, S), want)       # non-contiguous x
+    buf = torch.empty(6 * k + 1, dtype=torch.float16, device=gpu)
+    xo = buf[1:].view(6, k)
+    xo.copy_(X)
+    assert xo.data_ptr() % 16
+    assert torch.equal(awq_gemm_forward(xo, QW, QZ, S), want)                 # misaligned x
+    qw_t = QW.t().contiguous().t()
+    assert torch.equal(awq_gemm_forward(X, qw_t, QZ, S), want)                # non-contiguous qweight
+    empty = awq_gemm_forward(X[:0], QW, QZ, S)
+    assert empty.shape == (0, n)
+    empty3 = awq_gemm_forward(torch.empty((2, 0, k), dtype=torch.float16, device=gpu), QW, QZ, S)
+    assert empty3.shape == (2, 0, n)
+    with pytest.raises(ValueError):
+        awq_gemm_forward(X, QW, QZ, S, group_size=64)
+    with pytest.raises(ValueError):
+        awq_gemm_forward(X.cpu(), QW, QZ, S)
+
+
+def test_binding_workspace_registry_and_capture(gpu):
+    """One workspace registry for both entry points; a graph captured after an
+    eager warm-up of the same shape replays bit-identically with eager work
+    between replays; growing the workspace under capture is refused."""
+    k, n, m = 3584, 4608, 16
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=12)
+    X, QW, QZ, S = (_t(a, gpu) for a in (x, qw, qz, s))
+    ref = awq_gemm_forward(X, QW, QZ, S)
+    bufs = _workspace_buffers(gpu)
+    assert bufs and bufs[-1].numel() * 4 >= _native.plan_for(m, n, k).workspace_bytes
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        out = awq_gemm_forward(X, QW, QZ, S)
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}"
+        assert torch.equal(awq_gemm_forward(X[:4], QW, QZ, S), awq_gemm_forward_ex(X[:4], QW, QZ, S, 128))
+    # a shape needing more workspace than the registry holds: refused under capture
+    have = _workspace_buffers(gpu)[-1].numel() * 4
+    big_m, big_k, big_n = 2048, 18944, 3584
+    assert _native.plan_for(big_m, big_n, big_k).workspace_bytes > have
+    xb = torch.zeros((big_m, big_k), dtype=torch.float16, device=gpu)
+    qwb = torch.zeros((big_k, big_n // 8), dtype=torch.int32, device=gpu)
+    qzb = torch.zeros((big_k // 128, big_n // 8), dtype=torch.int32, device=gpu)
+    sb = torch.zeros((big_k // 128, big_n), dtype=torch.float16, device=gpu)
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="during graph capture"):
+        with torch.cuda.graph(g2, stream=side):
+            awq_gemm_forward(xb, qwb, qzb, sb)
+    torch.cuda.synchronize()
+    assert _workspace_buffers(gpu)[-1].numel() * 4 == have
