@@ -496,16 +496,27 @@ const TileModel* tile_model(int variant) {
 // unsplit grid leaves CUs idle or some CUs a whole tile more than others.
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t groups = K / kGroup;
+    // Deep weights (K >= 8192) up to M = 1024: a split grid with more than
+    // one workgroup per CU measured slower than the model predicts (the second
+    // workgroup of a CU competes for its load bandwidth through a short run
+    // while the partials grow).  down_proj 18944 x 3584 at M = 24 .. 1024, tiles
+    // of 128, 64 and 32 rows x splits 1 .. 30: the best plan fits one workgroup
+    // per CU at every M (M = 64: 23.5 us at split 17 against 30.5 at split 25;
+    // M = 512: 80.2 us at split 4 against 83.2 at split 9; M = 1024: 147.6 us
+    // at split 2 against 150.2 at split 4).  At M = 2048 split 2 on 448
+    // workgroups is best (256.1 us against 270.1 unsplit), hence the bound.
+    const bool one_per_cu = K >= 8192 && M <= 1024;
     double best = 0.0;
     int64_t best_v = 0, best_s = 0;
     for (const TileModel& t : kTileModels) {
-        // On deep weights (K >= 8192) the 32-row tile measured slower than
-        // the model predicts above 24 rows.
-        if (t.variant == 9 && M > 24 && K >= 8192) continue;
+        // On deep weights the 32-row tile measured slower than the model
+        // predicts above 32 rows (and was the best plan at 24 and 32).
+        if (t.variant == 9 && M > 32 && K >= 8192) continue;
         for (int64_t sp = 1; sp <= groups && sp <= 32; ++sp) {
             awq_w4a16_plan q;
             if (fill_tile(M, N, K, t.variant, sp, &q) != AWQ_OK) continue;
             if (sp > 1 && q.grid > 2 * (int64_t)cus()) continue;
+            if (one_per_cu && sp > 1 && q.grid > (int64_t)cus()) continue;
             const double time = tile_cost_busiest(t, M, N, K, sp);
             if (best_v == 0 || time < best) {
                 best = time;

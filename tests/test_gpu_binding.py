@@ -4,6 +4,10 @@ bit-identical outputs on every decode and prefill route, leading batch
 dimensions, M = 0, non-contiguous and misaligned operands; the binding's
 workspace registry is the one the ctypes path uses; growing it under graph
 capture is refused, and a capture after an eager warm-up replays correctly."""
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -86,17 +90,70 @@ def test_binding_workspace_registry_and_capture(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {i}"
         assert torch.equal(awq_gemm_forward(X[:4], QW, QZ, S), awq_gemm_forward_ex(X[:4], QW, QZ, S, 128))
-    # a shape needing more workspace than the registry holds: refused under capture
+    # growing the registry under capture is refused (what earlier tests left in
+    # it is unknown here, so ask for one byte more than it holds)
     have = _workspace_buffers(gpu)[-1].numel() * 4
-    big_m, big_k, big_n = 2048, 18944, 3584
-    assert _native.plan_for(big_m, big_n, big_k).workspace_bytes > have
-    xb = torch.zeros((big_m, big_k), dtype=torch.float16, device=gpu)
-    qwb = torch.zeros((big_k, big_n // 8), dtype=torch.int32, device=gpu)
-    qzb = torch.zeros((big_k // 128, big_n // 8), dtype=torch.int32, device=gpu)
-    sb = torch.zeros((big_k // 128, big_n), dtype=torch.float16, device=gpu)
     g2 = torch.cuda.CUDAGraph()
     with pytest.raises(RuntimeError, match="during graph capture"):
         with torch.cuda.graph(g2, stream=side):
-            awq_gemm_forward(xb, qwb, qzb, sb)
+            _native.binding().workspace(gpu.index, have + 1)
     torch.cuda.synchronize()
     assert _workspace_buffers(gpu)[-1].numel() * 4 == have
+
+
+_FRESH_REGISTRY = r"""
+import sys
+sys.path[:0] = sys.argv[1:3]
+import torch
+from kernels import _native
+from kernels.awq_gemm import _workspace_buffers, awq_gemm_forward
+
+dev = torch.device("cuda:0")
+g = torch.Generator(device=dev)
+g.manual_seed(5)
+def operands(m, k, n):
+    return (torch.randn((m, k), generator=g, device=dev).half(),
+            torch.randint(-2**31, 2**31 - 1, (k, n // 8), generator=g, device=dev, dtype=torch.int32),
+            torch.randint(-2**31, 2**31 - 1, (k // 128, n // 8), generator=g, device=dev, dtype=torch.int32),
+            (torch.rand((k // 128, n), generator=g, device=dev) * 0.018 + 0.002).half())
+small, big = (16, 3584, 4608), (16, 18944, 3584)
+ws_small = _native.plan_for(small[0], small[2], small[1]).workspace_bytes
+ws_big = _native.plan_for(big[0], big[2], big[1]).workspace_bytes
+print("workspace bytes: small", ws_small, "big", ws_big, flush=True)
+assert 0 < ws_small and ws_big > ((ws_small + (1 << 20) - 1) >> 20 << 20)
+a = operands(*small)
+ref = awq_gemm_forward(*a)
+have = _workspace_buffers(dev)[-1].numel() * 4
+assert len(_workspace_buffers(dev)) == 1 and ws_small <= have < ws_big
+b = operands(*big)
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+try:
+    with torch.cuda.graph(graph, stream=side):
+        awq_gemm_forward(*b)
+    raise SystemExit("growth under capture was not refused")
+except RuntimeError as e:
+    assert "during graph capture" in str(e), str(e)
+torch.cuda.synchronize()
+assert len(_workspace_buffers(dev)) == 1 and _workspace_buffers(dev)[-1].numel() * 4 == have
+assert torch.equal(awq_gemm_forward(*a), ref)
+y = awq_gemm_forward(*b)   # eagerly: grows the registry
+torch.cuda.synchronize()
+assert len(_workspace_buffers(dev)) == 2 and _workspace_buffers(dev)[-1].numel() * 4 >= ws_big
+print("ok", flush=True)
+"""
+
+
+def test_binding_growth_under_capture_is_refused(gpu):
+    """In a fresh process (registry empty): after an eager call that needs a
+    small workspace, a shape needing a larger one is refused under capture
+    with a RuntimeError and the registry is left as it was; the same call
+    eagerly grows it."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "qwen2-7b-triton_engine_amd")
+    print("binding growth under capture: fresh process", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FRESH_REGISTRY, pkg, root], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
