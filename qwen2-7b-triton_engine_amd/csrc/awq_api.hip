@@ -424,6 +424,26 @@ constexpr TileModel kTileModels[] = {
     {9, 32, 4, 0.768, 0.219, 1},
 };
 
+// 9 <= M <= 16 on deep, narrow weights (K >= 8192, fewer than 16 strips of
+// 512 columns): the 32-row tile (variant 9) with five 128-row groups per
+// split, where that grid covers every CU and fits two workgroups per CU;
+// else AWQ_ERR_PATH.
+// 18944 x 3584 (down_proj): 16.9 / 17.4 / 17.6 us at M = 9 / 12 / 16
+// against 17.2 / 17.9 / 18.8 for the half-strip stream kernel with its
+// reduce launch; at M = 5 - 8 the stream row kernel stays ahead (16.2 - 16.6
+// against 16.6 - 16.8).  Other splits of the same tile measured slower at
+// every M (17 splits 18.3 - 18.9, 25 splits 18.4 - 19.1, 37 splits 18.6 -
+// 20.0).
+int deep_small_m_tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    if (M < 9 || M > 16 || K < 8192 || gemv_strips((int)N) >= 16) return AWQ_ERR_PATH;
+    const int64_t groups = K / kGroup;
+    const int64_t split = (groups + 4) / 5;
+    awq_w4a16_plan q;
+    if (fill_tile(M, N, K, 9, split, &q) != AWQ_OK || q.grid < cus() || q.grid > 2 * cus()) return AWQ_ERR_PATH;
+    *p = q;
+    return AWQ_OK;
+}
+
 // 5 <= M <= 16 on weights the stream path does not take (narrow and
 // shallow: fewer than 16 strips of 512 columns, K < 8192): the 32-row
 // register-dequant tile (variant 9) split 14 ways along K (in whole 128-row
@@ -813,6 +833,7 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
     switch (path) {
         case AWQ_PATH_AUTO:
             if (M == 1 || (M <= kGemvMaxM && N % 32 != 0)) return gemv_plan(M, N, K, plan);
+            if (deep_small_m_tile_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (auto_stream(M, N, K) && stream_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (small_m_tile_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             return auto_skinny(M, N) ? skinny_plan(M, N, K, plan) : tile_plan(M, N, K, plan);

@@ -198,13 +198,16 @@ def test_auto_vocab_wide(gpu, m):
 
 def test_decode_plans_sized_by_the_device(gpu):
     """The planner sizes its grids by the current device's compute units (read
-    once per device): the decode plans of the Qwen2-7B shapes put at most one
-    workgroup on each CU and keep more than half of them busy."""
+    once per device): the GEMV and stream plans of the Qwen2-7B shapes put at
+    most one workgroup on each CU and keep more than half of them busy; the
+    32-row tile on down_proj at M = 16 covers every CU with at most two."""
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     print(f"device compute units: {cus}", flush=True)
-    for m, k, n in [(1, 3584, 4608), (1, 3584, 37888), (4, 3584, 4608), (4, 18944, 3584), (16, 18944, 3584)]:
+    for m, k, n in [(1, 3584, 4608), (1, 3584, 37888), (4, 3584, 4608), (4, 18944, 3584), (8, 18944, 3584)]:
         p = _native.plan_for(m, n, k)
         assert cus // 2 < p.grid <= cus, (m, k, n, p.grid, cus)
+    p = _native.plan_for(16, 3584, 18944)
+    assert p.path == _native.PATH_TILE and cus <= p.grid <= 2 * cus, (p.path, p.grid, cus)
 
 
 @pytest.mark.parametrize("m", [1, 8, 64, 512, 2048])

@@ -81,8 +81,14 @@ def test_auto_plan_invariants(L, m, k, n):
     p = _native.plan_for(m, n, k)
     strips = -(-(n // 8) // 64)            # 512-column strips of the stream path
     stream = n % 32 == 0 and m <= 16 and (m <= 4 or strips >= 16 or k >= 8192)
+    # 9 <= M <= 16 on deep, narrow weights: the 32-row tile with five groups per
+    # split where that grid covers every CU and fits two workgroups per CU
+    deep_split = -(-(k // 128) // 5)
+    deep_tile = 9 <= m <= 16 and k >= 8192 and strips < 16 and 256 <= -(-n // 256) * deep_split <= 512
     if m == 1 or (m == 2 and n % 32 != 0):
         assert p.path == _native.PATH_GEMV
+    elif deep_tile:
+        assert p.path == _native.PATH_TILE and p.variant == 9 and p.split_k == deep_split
     elif stream:
         assert p.path == _native.PATH_STREAM
         assert p.tile_m >= m
