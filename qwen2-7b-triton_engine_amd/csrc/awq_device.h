@@ -266,7 +266,11 @@ __device__ __forceinline__ half_t epi_round(float y, const half_t* bias_n, const
     return h;
 }
 // V consecutive outputs out[m, n .. n+V-1] (V = 4 or 8, n % V == 0) as one
-// vector store, with the epilogue above.
+// vector store, with the epilogue above.  Device-scope (write-through)
+// stores: the output leaves L2 while the kernel still runs instead of in the
+// write-back at its end (measured 0.5 - 4 % faster on the reduce launches
+// and whole tiles).  Output byte offsets stay below 2^31 (the host checks
+// M N 2 < 2^31), so one buffer resource from `out` covers every store.
 template <int V>
 __device__ __forceinline__ void store_out(half_t* out, const half_t* bias, const half_t* residual, int N, int m,
                                           int n, const float (&y)[V]) {
@@ -280,7 +284,14 @@ __device__ __forceinline__ void store_out(half_t* out, const half_t* bias, const
 #pragma unroll
         for (int i = 0; i < V; ++i) h[i] = epi_round(y[i], bias ? bias + n + i : nullptr, residual ? residual + o + i : nullptr);
     }
-    *reinterpret_cast<hv_t*>(out + o) = h;
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, 0x7FFFFFFFu);
+    if constexpr (V == 8) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, h), ro, (uint32_t)(o * 2), 0, kCpolSC1);
+    } else {
+        static_assert(V == 4, "4 or 8 outputs");
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, h), ro, (uint32_t)(o * 2), 0, kCpolSC1);
+    }
 }
 // epi_round with the bias / residual values already loaded (has_* says
 // which of them apply).

@@ -166,8 +166,7 @@ __device__ __forceinline__ void stream_finish(const GemmArgs& a, int split_k, ui
             floatx4 v = {0.f, 0.f, 0.f, 0.f};
             for (int w = 0; w < nred; ++w) v += *reinterpret_cast<const floatx4*>(&red[(w * MP + m) * 512 + 4 * q]);
             const uint32_t off = (uint32_t)((((size_t)split * a.M + m) * a.N + strip * 512 + 4 * q) * 4);
-            if (FIN == 1) buf_store_f4_device(v, rp, off);
-            else __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp, off, 0, 0);
+            buf_store_f4_device(v, rp, off);
         }
         if (FIN == 2) return;
         __shared__ int last_flag;

@@ -427,17 +427,40 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     }
     const int qcol = 64 * wn + 8 * (ekb >> 1) + 4 * (ekb & 1);  // + 16 c: the quad's first column in the tile
     if (ks == 1) {
+        // The fp16 tile goes through LDS and leaves as whole rows: each
+        // thread stores 16 bytes, 32 threads a 512-byte row, instead of every
+        // store instruction writing 32 bytes into each of 16 rows.  Staged
+        // rows are 544 bytes apart, so the 16 rows of a wave's 8-byte writes
+        // start 8 banks apart.  The ring is free: every wave has passed the
+        // last step's barrier, after which no load is in flight.
+        constexpr int ROW = T5_BN * 2 + 32;
+        static_assert(BM * ROW <= S * L::STAGE, "the staged tile fits in the ring");
+        typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+        typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 #pragma unroll
-        for (int f = 0; f < FM; ++f) {
-            const int m = m0 + 16 * f + e16;
-            if (m >= a.M) continue;
+        for (int f = 0; f < FM; ++f)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int col = qcol + 16 * c;
-                if (n0 + col >= a.N) continue;
-                const float v[4] = {acc[c][f][0], acc[c][f][1], acc[c][f][2], acc[c][f][3]};
-                store_out<4>(a.out, a.bias, a.residual, a.N, m, n0 + col, v);
+                const h4_t h = {(half_t)acc[c][f][0], (half_t)acc[c][f][1], (half_t)acc[c][f][2], (half_t)acc[c][f][3]};
+                *reinterpret_cast<h4_t*>(smem + (16 * f + e16) * ROW + 2 * (qcol + 16 * c)) = h;
             }
+        __syncthreads();
+        const bool epi = a.bias || a.residual;
+        const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.out, (uint32_t)((size_t)a.M * a.N * 2));
+#pragma unroll
+        for (int p = tid; p < BM * (T5_BN / 8); p += 256) {
+            const int r = p >> 5, c8 = 8 * (p & 31);
+            const int m = m0 + r, n = n0 + c8;
+            if (m >= a.M || n >= a.N) continue;
+            h8_t h = *reinterpret_cast<const h8_t*>(smem + r * ROW + 2 * c8);
+            const size_t o = (size_t)m * a.N + n;
+            if (epi) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    h[i] = epi_round_vals((float)h[i], a.bias != nullptr, a.bias ? a.bias[n + i] : (half_t)0,
+                                          a.residual != nullptr, a.residual ? a.residual[o + i] : (half_t)0);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, h), ro, (uint32_t)(o * 2), 0, kCpolSC1);
         }
         return;
     }
