@@ -214,6 +214,10 @@ __device__ __forceinline__ void wait_batches(int n) {
 // Device-scope (cache policy SC1) 16-byte store and load: coherent across
 // the XCDs of the device without whole-L2 maintenance.
 constexpr int kCpolSC1 = 16;
+// Non-temporal (streaming) load hint, used for the decode kernels' weight
+// loads when a workgroup streams a long K range: at most this many splits.
+constexpr int kCpolNT = 2;
+constexpr int kNonTemporalMaxSplit = 4;
 __device__ __forceinline__ void buf_store_f4_device(floatx4 v, __amdgpu_buffer_rsrc_t r, uint32_t voff) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, 0, kCpolSC1);
 }
@@ -301,16 +305,14 @@ __device__ __forceinline__ half_t epi_round_vals(float y, bool has_bias, half_t 
     if (has_res) h = (half_t)((float)res_v + (float)h);
     return h;
 }
+// out[o] = h as a device-scope (write-through) store, like store_out's.
+__device__ __forceinline__ void store_half_device(half_t* out, size_t o, half_t h) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, h), make_rsrc(out, 0x7FFFFFFFu),
+                                          (uint32_t)(o * 2), 0, kCpolSC1);
+}
 // The sum held by a fixed-point slot value.
 __device__ __forceinline__ float fixed_point_sum(unsigned long long now) {
     return (float)((long long)now >> 8) * (1.0f / 16777216.0f);
-}
-__device__ __forceinline__ void fixed_point_complete(unsigned long long now, unsigned long long* slot, half_t* out,
-                                                     int split_k, const half_t* bias_n, const half_t* res) {
-    if ((int)(now & 0xFFull) == split_k) {
-        *out = epi_round(fixed_point_sum(now), bias_n, res);
-        __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
 }
 // The last step of B outputs of one thread (out[m[b], n[b]] for the b with
 // ok[b]): a direct store of the fp32 sum when split_k == 1, else the
@@ -342,8 +344,8 @@ __device__ __forceinline__ void finish_batch(unsigned long long* fix, half_t* ou
 #pragma unroll
         for (int b = 0; b < B; ++b)
             if (ok[b])
-                out[(size_t)m[b] * N + n[b]] =
-                    epi_round_vals(sum[b], bias != nullptr, bv[b], residual != nullptr, rv[b]);
+                store_half_device(out, (size_t)m[b] * N + n[b],
+                                  epi_round_vals(sum[b], bias != nullptr, bv[b], residual != nullptr, rv[b]));
         return;
     }
     unsigned long long word[B], old[B];
@@ -360,7 +362,7 @@ __device__ __forceinline__ void finish_batch(unsigned long long* fix, half_t* ou
         const unsigned long long now = old[b] + word[b];
         if (ok[b] && (int)(now & 0xFFull) == split_k) {
             const size_t o = (size_t)m[b] * N + n[b];
-            out[o] = epi_round_vals(fixed_point_sum(now), bias != nullptr, bv[b], residual != nullptr, rv[b]);
+            store_half_device(out, o, epi_round_vals(fixed_point_sum(now), bias != nullptr, bv[b], residual != nullptr, rv[b]));
             __hip_atomic_store(fix + o, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }

@@ -40,13 +40,13 @@
 // one MFMA.
 //
 // Split-K finish (FIN): 0 -- fixed-point slots, one 64-bit atomic per output
-// element per workgroup (fixed_point_word / fixed_point_complete:
-// deterministic, one round trip; direct fp16 store when split_k == 1); 1 --
-// fp32 partials [split, M, N] with device-scope stores and an arrival counter
-// per strip, the last workgroup of a strip adds the partials in split order;
-// 2 -- fp32 partials with plain stores, added by awq_splitk_reduce_kernel in
-// a second launch (spreads the additions over the whole device when a strip
-// has many splits).
+// element per workgroup (fixed_point_word / finish_batch: deterministic, one
+// round trip; direct fp16 store when split_k == 1); 1 -- fp32 partials
+// [split, M, N] with device-scope stores and an arrival counter per strip,
+// the last workgroup of a strip adds the partials in split order; 2 -- fp32
+// partials, also with device-scope (write-through) stores, added by
+// awq_splitk_reduce_kernel in a second launch (spreads the additions over
+// the whole device when a strip has many splits).
 #include "awq_kernels.h"
 
 namespace awq {
@@ -212,7 +212,7 @@ __device__ __forceinline__ void stream_finish(const GemmArgs& a, int split_k, ui
 // together -- wave w its chunks w*CPG .. w*CPG+CPG-1 -- so they all have the
 // same work and stream adjacent rows; each folds its part of a group once.
 // x rows of the workgroup's K range are staged in LDS with the constants.
-template <int FIN, int CPG, int R>
+template <int FIN, int CPG, int R, bool NT>
 __global__ __launch_bounds__(512) void awq_stream_row_kernel(GemmArgs a, int split_k, uint32_t* counters) {
     constexpr int MH = 1;  // blocks of 8 x rows
     constexpr int XI = 4;  // x prologue loads per thread
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(512) void awq_stream_row_kernel(GemmArgs a, int spl
 #pragma unroll
         for (int u = 0; u < 8; ++u)
             w[u] = __builtin_bit_cast(u32x2,
-                                      __builtin_amdgcn_raw_buffer_load_b64(rw, voff_w + oob, (r0 + u) * row_bytes, 0));
+                                      __builtin_amdgcn_raw_buffer_load_b64(rw, voff_w + oob, (r0 + u) * row_bytes, NT ? kCpolNT : 0));
     };
     u32x2 ring[R][8];
 #pragma unroll
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(512) void awq_stream_row_kernel(GemmArgs a, int spl
 // Half-strip layout, M <= 16.  MP: rows of x covered by the finish (4 or 16,
 // >= M); R: chunk buffers per wave (2: two waves per SIMD, up to 512
 // threads; 4 or 6: one wave per SIMD, up to 256 threads).
-template <int MP, int FIN, int R>
+template <int MP, int FIN, int R, bool NT>
 __global__ __launch_bounds__(R == 2 ? 512 : 256) void awq_stream_kernel(GemmArgs a, int split_k, uint32_t* counters) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int lane = threadIdx.x & 63;
@@ -396,7 +396,7 @@ __global__ __launch_bounds__(R == 2 ? 512 : 256) void awq_stream_kernel(GemmArgs
 #pragma unroll
         for (int u = 0; u < 8; ++u)
             ck.w[u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                    rw, voff_w + oob, (r0 + (u & 3) + 16 * (u >> 2)) * row_bytes, 0));
+                                                    rw, voff_w + oob, (r0 + (u & 3) + 16 * (u >> 2)) * row_bytes, NT ? kCpolNT : 0));
 #pragma unroll
         for (int t = 0; t < 2; ++t)
             ck.xa[t] = __builtin_bit_cast(u32x2,
@@ -536,8 +536,11 @@ hipError_t reduce_launch(const GemmArgs& a, int split_k, hipStream_t stream) { r
 template <int MP, int FIN, int R>
 hipError_t half_launch(const GemmArgs& a, int split_k, int k_waves, uint32_t* counters, hipStream_t stream) {
     const size_t lds = stream_lds_bytes(a.M, a.K, split_k, k_waves, kStreamHalfLayout);
-    hipLaunchKernelGGL((awq_stream_kernel<MP, FIN, R>), dim3((unsigned)(gemv_strips(a.N) * split_k)),
-                       dim3((unsigned)stream_threads(kStreamHalfLayout, k_waves)), lds, stream, a, split_k, counters);
+    const dim3 grid((unsigned)(gemv_strips(a.N) * split_k)), block((unsigned)stream_threads(kStreamHalfLayout, k_waves));
+    if (split_k <= kNonTemporalMaxSplit)
+        hipLaunchKernelGGL((awq_stream_kernel<MP, FIN, R, true>), grid, block, lds, stream, a, split_k, counters);
+    else
+        hipLaunchKernelGGL((awq_stream_kernel<MP, FIN, R, false>), grid, block, lds, stream, a, split_k, counters);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || FIN != 2 || split_k <= 1) return e;
     return reduce_launch(a, split_k, stream);
@@ -546,8 +549,11 @@ hipError_t half_launch(const GemmArgs& a, int split_k, int k_waves, uint32_t* co
 template <int FIN, int CPG, int R>
 hipError_t row_launch(const GemmArgs& a, int split_k, uint32_t* counters, hipStream_t stream) {
     const size_t lds = stream_lds_bytes(a.M, a.K, split_k, 8 / CPG, kStreamRowLayout);
-    hipLaunchKernelGGL((awq_stream_row_kernel<FIN, CPG, R>), dim3((unsigned)(gemv_strips(a.N) * split_k)),
-                       dim3((unsigned)stream_threads(kStreamRowLayout, 8 / CPG)), lds, stream, a, split_k, counters);
+    const dim3 grid((unsigned)(gemv_strips(a.N) * split_k)), block((unsigned)stream_threads(kStreamRowLayout, 8 / CPG));
+    if (split_k <= kNonTemporalMaxSplit)
+        hipLaunchKernelGGL((awq_stream_row_kernel<FIN, CPG, R, true>), grid, block, lds, stream, a, split_k, counters);
+    else
+        hipLaunchKernelGGL((awq_stream_row_kernel<FIN, CPG, R, false>), grid, block, lds, stream, a, split_k, counters);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || FIN != 2 || split_k <= 1) return e;
     return reduce_launch(a, split_k, stream);
