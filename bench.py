@@ -359,8 +359,129 @@ def summarize(argv):
             md.append(f"| `{k}` | {g} | {w} | {len(v)} | {statistics.median(v):.2f} | {statistics.mean(v):.2f} |")
         open(os.path.join(prof, out_name), "w").write("\n".join(md) + "\n")
         print(f"kernel-trace: {len(groups)} launch configurations -> profiles/{out_name}")
+    elif kind == "prefill-trace":
+        _summarize_prefill_trace(dirs[0], prof, cmd_head)
     else:
         raise SystemExit(f"unknown summary kind {kind!r}")
+
+
+def _plan_kernel_key(_native, m, n, k):
+    """(kernel name prefix, workgroups, threads) that AUTO's plan for (m, n, k) launches first."""
+    p = _native.plan_for(m, n, k)
+    path = _native.PATH_NAMES[p.path]
+    if path == "tile":
+        fin = 0 if p.variant in (6, 13, 14) else 1
+        name = f"awq_tile_kernel<{p.tile_m // 16}, {fin}, {'true' if p.variant in (13, 14) else 'false'}>"
+    else:
+        name = FAMILY_KERNELS[path][0]
+    return name, int(p.grid), int(p.block_threads), p
+
+
+def _summarize_prefill_trace(d, prof, cmd_head):
+    """profiles/prefill_tile_kernel_trace.md and lm_head_gemv_kernel_trace.md from one
+    rocprofv3 --kernel-trace run of `bench.py --no-cpu-baseline --no-e2e --steps 1 --warmup 0`.
+    Each measurement of the bench (an eager launch, then graph replays) is a run of AWQ launches
+    of one kernel and grid; the runs are matched, in the bench's order, to the M = 2048
+    engine shapes, the down_proj M-sweep and the lm_head GEMV at M = 1 and 4 by the kernel and
+    grid of each one's AUTO plan."""
+    import csv
+    import glob
+    import statistics
+
+    from kernels import _native
+    from kernels.awq_roofline import MFMA_F16_DENSE_PEAK_FLOPS, flops
+    trace_path = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))[0]
+    rows = sorted(csv.DictReader(open(trace_path)), key=lambda r: int(r["Start_Timestamp"]))
+    # run: {"key": (name, wgs, threads), "main": [rows], "reduce": [rows]}; a measurement's
+    # eager launch and its graph replays are parted by two or three small torch kernels (fills),
+    # two measurements by more (operand set-up, or torch's own GEMM timed in between).
+    runs, cur, gap = [], None, 0
+    for r in rows:
+        name = _short_kernel(r["Kernel_Name"])
+        if "awq" not in name:
+            gap += 1
+            if gap > 3:
+                cur = None
+            continue
+        gap = 0
+        wgs = int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"])
+        if name == "awq_splitk_reduce_kernel":
+            if cur is not None:
+                cur["reduce"].append(r)
+            continue
+        key = (name, wgs, int(r["Workgroup_Size_X"]))
+        if cur is None or cur["key"] != key:
+            cur = {"key": key, "main": [], "reduce": []}
+            runs.append(cur)
+        cur["main"].append(r)
+
+    def us(r):
+        return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+    items = [(name, 2048, k, n) for name, k, n in ENGINE_SHAPES]
+    items += [("down_proj", m, INTER, HIDDEN) for m in (1, 8, 64, 512, 2048)]
+    pos, found = 0, []
+    for name, m, k, n in items:
+        kname, wgs, threads, p = _plan_kernel_key(_native, m, n, k)
+        while pos < len(runs) and not (runs[pos]["key"][0].startswith(kname) and runs[pos]["key"][1:] == (wgs, threads)):
+            pos += 1
+        if pos == len(runs):
+            raise SystemExit(f"no run of {kname} x {wgs} for {name} M={m}")
+        found.append((name, m, k, n, p, runs[pos]))
+        pos += 1
+    lm = []
+    for m in (1, 4):
+        while pos < len(runs) and "fp16_mfma_kernel" not in runs[pos]["key"][0]:
+            pos += 1
+        if pos == len(runs):
+            raise SystemExit(f"no lm_head run for M={m}")
+        lm.append((m, runs[pos]))
+        pos += 1
+
+    command = ("rocprofv3 --kernel-trace --stats -d " + d + " -o prefill --output-format csv -- "
+               "python3 bench.py --no-cpu-baseline --no-e2e --steps 1 --warmup 0")
+    head = ["Commands (from the repository root on the MI355X box):", "", "```", cmd_head, command,
+            f"python3 bench.py --summarize prefill-trace {d}", "```", ""]
+    md = ["# Prefill tile kernels and the down_proj M-sweep: rocprofv3 kernel trace", ""] + head + [
+        "Each row is one measurement of `bench.py` (an eager launch, then HIP-graph replays over",
+        ">= 640 MB of distinct random-init weight copies), found in the trace as a run of launches of",
+        "the kernel and grid AUTO plans for the shape.  The first replays run while the clocks are",
+        "still rising, so the median and the minimum are the figures to read.  Plans with the",
+        "reduce-launch finish are followed by one `awq_splitk_reduce_kernel` launch each (its median in",
+        "the reduce column).  TFLOP/s = 2 M N K / (median launch + median reduce launch); the",
+        f"percentage is of the dense fp16 MFMA peak ({MFMA_F16_DENSE_PEAK_FLOPS / 1e12:.1f} TFLOP/s).", "",
+        "| GEMM | kernel | variant, split | workgroups x threads | LDS B | VGPR+AGPR / scratch | launches "
+        "| avg us | median us | min us | reduce us | TFLOP/s |", "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for name, m, k, n, p, run in found:
+        t = [us(r) for r in run["main"]]
+        red = statistics.median([us(r) for r in run["reduce"]]) if run["reduce"] else 0.0
+        r0 = run["main"][0]
+        med = statistics.median(t)
+        tf = flops(m, n, k) / ((med + red) * 1e-6) / 1e12
+        md.append(f"| {name} M={m} K={k} N={n} | `{run['key'][0]}` | {p.variant}, {p.split_k} | "
+                  f"{run['key'][1]} x {run['key'][2]} | {r0['LDS_Block_Size']} | "
+                  f"{r0['VGPR_Count']}+{r0['Accum_VGPR_Count']} / {r0['Scratch_Size']} | {len(t)} | "
+                  f"{statistics.mean(t):.1f} | {med:.1f} | {min(t):.1f} | {red:.1f} | "
+                  f"{tf:.0f} ({100 * tf * 1e12 / MFMA_F16_DENSE_PEAK_FLOPS:.1f} %) |")
+    open(os.path.join(prof, "prefill_tile_kernel_trace.md"), "w").write("\n".join(md) + "\n")
+
+    wbytes = VOCAB * HIDDEN * 2
+    md = ["# lm_head fp16 GEMV: rocprofv3 kernel trace", ""] + head + [
+        f"`bench.py` times the projection {VOCAB} x {HIDDEN} (fp16 weight, {wbytes / 1e9:.3f} GB) at M = 1 and 4",
+        "over three weight copies in HIP graphs (torch's own `F.linear` on the same operands is timed",
+        "beside it and does not appear here).  GB/s = weight bytes / median launch.", "",
+        "| M | kernel | workgroups x threads | VGPR+AGPR / scratch | launches | avg us | median us | min us | GB/s |",
+        "|---|---|---|---|---|---|---|---|---|"]
+    for m, run in lm:
+        t = [us(r) for r in run["main"]]
+        r0 = run["main"][0]
+        med = statistics.median(t)
+        md.append(f"| {m} | `awq_fp16_mfma_kernel` | {run['key'][1]} x {run['key'][2]} | "
+                  f"{r0['VGPR_Count']}+{r0['Accum_VGPR_Count']} / {r0['Scratch_Size']} | {len(t)} | "
+                  f"{statistics.mean(t):.1f} | {med:.1f} | {min(t):.1f} | {wbytes / med / 1e3:.0f} |")
+    open(os.path.join(prof, "lm_head_gemv_kernel_trace.md"), "w").write("\n".join(md) + "\n")
+    print(f"prefill-trace: {len(found)} GEMMs, {len(lm)} lm_head points -> profiles/prefill_tile_kernel_trace.md, "
+          "profiles/lm_head_gemv_kernel_trace.md")
 
 
 def main():
@@ -382,7 +503,8 @@ def main():
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="host only: turn rocprofv3 CSV output into the profiles/ summaries. "
                          "'decode-pmc FETCH_DIR WRITE_DIR', 'prefill-pmc SQ_DIR FETCH_DIR WRITE_DIR' "
-                         "(directories of --counter-pass runs) or 'kernel-trace DIR' (a --kernel-trace --stats run)")
+                         "(directories of --counter-pass runs), 'kernel-trace DIR' (a --kernel-trace --stats run of the "
+                         "headline) or 'prefill-trace DIR' (one of --no-cpu-baseline --no-e2e --steps 1 --warmup 0)")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize)
