@@ -359,10 +359,60 @@ def summarize(argv):
             md.append(f"| `{k}` | {g} | {w} | {len(v)} | {statistics.median(v):.2f} | {statistics.mean(v):.2f} |")
         open(os.path.join(prof, out_name), "w").write("\n".join(md) + "\n")
         print(f"kernel-trace: {len(groups)} launch configurations -> profiles/{out_name}")
+    elif kind == "prefill-issue":
+        _summarize_prefill_issue(dirs[:2], prof, cmd_head)
     elif kind == "prefill-trace":
         _summarize_prefill_trace(dirs[0], prof, cmd_head)
     else:
         raise SystemExit(f"unknown summary kind {kind!r}")
+
+
+PREFILL_ISSUE_COUNTERS = (
+    "SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY SQ_ACTIVE_INST_VALU "
+    "SQ_ACTIVE_INST_LDS SQ_VALU_MFMA_COEXEC_CYCLES GRBM_GUI_ACTIVE",
+    "SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_WAIT_INST_LDS SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_SCA "
+    "SQ_INSTS_SALU SQ_ACTIVE_INST_VALU2 GRBM_GUI_ACTIVE")
+
+
+def _summarize_prefill_issue(dirs, prof, cmd_head):
+    """profiles/prefill_tile_issue.md: where the SIMD cycles of the prefill tile kernels go, from
+    two counter passes of `bench.py --counter-pass prefill` (the warm launch of each shape)."""
+    a_runs, b_runs = (_gemm_groups(_dispatches(_counter_csv(d))) for d in dirs)
+    want = len(ENGINE_SHAPES) * PREFILL_LAUNCHES
+    assert len(a_runs) == len(b_runs) == want, (len(a_runs), len(b_runs), want)
+    simds = 256 * 4
+    cmds = [f"timeout -s KILL 120 rocprofv3 --pmc {c} -d {d} -o {t} --output-format csv -- "
+            "python3 bench.py --counter-pass prefill" for c, d, t in zip(PREFILL_ISSUE_COUNTERS, dirs, "ab")]
+    cmds.append(f"python3 bench.py --summarize prefill-issue {' '.join(dirs)}")
+    md = ["# Prefill tile kernels (M = 2048): where the SIMD cycles go", "",
+          "Commands (two counter passes, then the summary; from the repository root on the MI355X box):", "",
+          "```", cmd_head, *cmds, "```", "",
+          f"The warm (last of {PREFILL_LAUNCHES}) launch of each engine shape; counters summed over the device.",
+          "SIMD cycles = 1024 SIMDs x `GRBM_GUI_ACTIVE` / 8 XCDs.  The SQ per-wave counters are in quad",
+          "cycles (x 4 below) and are divided by the waves' own cycles (`SQ_WAVE_CYCLES` x 4).", "",
+          "* MFMA busy: `SQ_VALU_MFMA_BUSY_CYCLES` / SIMD cycles (equal to MFMA count x 16 cycles /",
+          "  SIMD cycles: the matrix core is busy exactly while its instructions run).",
+          "* VALU issue: non-MFMA VALU instructions x 4 cycles / SIMD cycles (a wave64 VALU instruction",
+          "  takes 4 cycles); co-executed: `SQ_VALU_MFMA_COEXEC_CYCLES` / SIMD cycles, the cycles in which",
+          "  a VALU instruction issued while the matrix core was busy.",
+          "* Waves per SIMD: `SQ_WAVE_CYCLES` x 4 / SIMD cycles.", "",
+          "| shape | kernel | waves / SIMD | MFMA busy | VALU issue | VALU co-executed | VALU per MFMA | LDS per MFMA "
+          "| SALU per MFMA | wave: active | wave: waiting to issue | wave: waiting (deps, barrier) |",
+          "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for i, (name, k, n) in enumerate(ENGINE_SHAPES):
+        last = (i + 1) * PREFILL_LAUNCHES - 1
+        a, b = a_runs[last][0][2], b_runs[last][0][2]
+        cyc = simds * a["GRBM_GUI_ACTIVE"] / 8
+        wave = a["SQ_WAVE_CYCLES"] * 4
+        mf = b["SQ_INSTS_MFMA"]
+        valu = b["SQ_INSTS_VALU"] - mf
+        md.append(f"| {name} | `{_short_kernel(a_runs[last][0][1])}` | {wave / cyc:.2f} | "
+                  f"{b['SQ_VALU_MFMA_BUSY_CYCLES'] / cyc:.3f} | {valu * 4 / cyc:.3f} | "
+                  f"{a['SQ_VALU_MFMA_COEXEC_CYCLES'] / cyc:.3f} | {valu / mf:.2f} | {b['SQ_INSTS_LDS'] / mf:.2f} | "
+                  f"{b['SQ_INSTS_SALU'] / mf:.2f} | {a['SQ_ACTIVE_INST_ANY'] * 4 / wave:.3f} | "
+                  f"{a['SQ_WAIT_INST_ANY'] * 4 / wave:.3f} | {a['SQ_WAIT_ANY'] * 4 / wave:.3f} |")
+    open(os.path.join(prof, "prefill_tile_issue.md"), "w").write("\n".join(md) + "\n")
+    print("prefill-issue: 4 shapes -> profiles/prefill_tile_issue.md")
 
 
 def _plan_kernel_key(_native, m, n, k):
@@ -504,7 +554,8 @@ def main():
                     help="host only: turn rocprofv3 CSV output into the profiles/ summaries. "
                          "'decode-pmc FETCH_DIR WRITE_DIR', 'prefill-pmc SQ_DIR FETCH_DIR WRITE_DIR' "
                          "(directories of --counter-pass runs), 'kernel-trace DIR' (a --kernel-trace --stats run of the "
-                         "headline) or 'prefill-trace DIR' (one of --no-cpu-baseline --no-e2e --steps 1 --warmup 0)")
+                         "headline), 'prefill-trace DIR' (one of --no-cpu-baseline --no-e2e --steps 1 --warmup 0) or "
+                         "'prefill-issue A_DIR B_DIR' (the two issue-counter passes of --counter-pass prefill)")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize)
