@@ -137,6 +137,7 @@ bool auto_skinny(int64_t M, int64_t /*N*/) { return M <= 16; }
 
 // Largest M the GEMV path serves.
 constexpr int64_t kGemvMaxM = 2;
+constexpr int64_t kGemvPairMaxM = 4;
 // LDS the column-quad GEMV may stage per workgroup.
 constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 
@@ -146,34 +147,38 @@ constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 // see below.
 int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, int64_t rows_per_wave,
               int64_t k_waves, int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
-    if (M > kGemvMaxM) return AWQ_ERR_PATH;
+    // Column pairs (variant 5 with 256-column strips) carry up to 4 rows of x.
+    const bool pairs = variant == 5 && tile_n == 256;
+    if (M > (pairs ? kGemvPairMaxM : kGemvMaxM)) return AWQ_ERR_PATH;
     p->path = AWQ_PATH_GEMV;
     p->variant = (int32_t)variant;
-    p->tile_m = (int32_t)kGemvMaxM;
-    p->tile_n = 512;
+    p->tile_m = (int32_t)(pairs ? kGemvPairMaxM : kGemvMaxM);
+    p->tile_n = (int32_t)tile_n;
     p->rows_per_wave = (int32_t)rows_per_wave;
     p->k_waves = (int32_t)k_waves;
     p->block_threads = (int32_t)(64 * k_waves);
     p->factored_scale = 1;
     p->depth = 0;
-    if (tile_n != 512) return AWQ_ERR_PATH;
+    if (tile_n != 512 && !pairs) return AWQ_ERR_PATH;
     if (variant == 5) {
-        // Column quads with MFMA column sums: N % 32 == 0; rows_per_wave 0;
-        // depth 2 .. 4 chunk buffers per wave (each
-        // strip's K/32 chunks are divided evenly over split_k workgroups of
-        // k_waves waves); split_k <= min(K/32, kFixMaxSplit); the groups and
-        // x rows a workgroup stages must fit its prologue loads, and the
-        // staged data its LDS.
-        if (N % 32 != 0 || rows_per_wave != 0 || depth < 2 || depth > 4) return AWQ_ERR_PATH;
+        // Column quads (512-column strips, M <= 2) or column pairs (256-column
+        // strips, M <= 4) with MFMA column sums: N % 32 == 0; rows_per_wave 0;
+        // depth 2 .. 4 chunk buffers per wave (2 .. 3 for pairs; each strip's
+        // K/32 chunks are divided evenly over split_k workgroups of k_waves
+        // waves); split_k <= min(K/32, kFixMaxSplit); the groups and x rows a
+        // workgroup stages must fit its prologue loads, and the staged data
+        // its LDS.
+        const int cw = pairs ? 2 : 4;
+        if (N % 32 != 0 || rows_per_wave != 0 || depth < 2 || depth > (pairs ? 3 : 4)) return AWQ_ERR_PATH;
         if (k_waves < 1 || k_waves > 8 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
             return AWQ_ERR_PATH;
-        if (!gemv_quad_fits((int)M, (int)K, (int)split_k, (int)k_waves)) return AWQ_ERR_PATH;
+        if (!gemv_quad_fits((int)M, (int)K, (int)split_k, (int)k_waves, cw)) return AWQ_ERR_PATH;
         p->split_k = (int32_t)split_k;
         p->depth = (int32_t)depth;
-        p->grid = gemv_strips((int)N) * split_k;
+        p->grid = gemv_strips_cw((int)N, cw) * split_k;
         if (split_k > 1 && (uint64_t)M * (uint64_t)N * 8u > kSlotBytes) return AWQ_ERR_PATH;
         p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
-        p->lds_bytes = gemv_quad_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves);
+        p->lds_bytes = gemv_quad_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves, cw);
         if (p->lds_bytes > kQuadLdsBudget) return AWQ_ERR_PATH;
         if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
         return AWQ_OK;
@@ -221,13 +226,48 @@ int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     int64_t w = (C + split - 1) / split;
     if (w > 4) w = 4;
     if (w < 1) w = 1;
-    while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w) ||
-           gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w) > kQuadLdsBudget) {
+    while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w, 4) ||
+           gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w, 4) > kQuadLdsBudget) {
         if (w < 8) ++w;
         else if (split < C && split < kFixMaxSplit) ++split;
         else break;
     }
     return fill_gemv(M, N, K, 5, 512, 0, w, split, 2, p);
+}
+
+// Column pairs (256-column strips, up to 4 rows of x) on narrow weights
+// (fewer than 16 strips of 512 columns): twice the strips of the quads, so
+// one workgroup per CU needs half the K splits and the fixed-point finish
+// half the atomics.  Four waves, two chunk buffers.  Measured against the
+// previous AUTO plans (graphs over >= 640 MB of weights): 3584 x 4608 at
+// M = 1 / 2 / 3 / 4 5.96 / 6.95 / 8.59 / 9.00 us against 7.47 / 8.13 / 9.06 /
+// 9.51; 3584 x 3584 5.66 / 6.71 / 8.55 / 8.92 against 6.79 / 7.96 / 8.82 /
+// 9.22; 18944 x 3584 at M = 1 / 2 11.12 / 12.27 against 12.28 / 12.92 (at
+// M = 3 the stream row kernel stays ahead, 13.8 against 14.3-14.7, so deep
+// weights take pairs only for M <= 2); on 3584 x 37888 the quads (M = 1) and
+// the stream kernels (M >= 2) stay within 2 % of the pairs or ahead.
+bool auto_pairs(int64_t M, int64_t N, int64_t K) {
+    // Measured on 3584 - 4608 columns (14 - 18 strips of 256); narrower
+    // weights keep the plans measured for them.
+    if (N % 32 != 0 || gemv_strips((int)N) >= 16 || gemv_strips_cw((int)N, 2) < 8) return false;
+    return M <= 2 || (M <= kGemvPairMaxM && K < 8192);
+}
+
+int pair_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    const int64_t strips = gemv_strips_cw((int)N, 2);
+    const int64_t C = K / 32;
+    int64_t split = cus() / strips;
+    if (split > C) split = C;
+    if (split > kFixMaxSplit) split = kFixMaxSplit;
+    if (split < 1) split = 1;
+    int64_t w = 4;
+    while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w, 2) ||
+           gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w, 2) > kQuadLdsBudget) {
+        if (w < 8) ++w;
+        else if (split < C && split < kFixMaxSplit) ++split;
+        else return AWQ_ERR_PATH;
+    }
+    return fill_gemv(M, N, K, 5, 256, 0, w, split, 2, p);
 }
 
 // Column quads while their fixed-point slots (M x N x 8 bytes) fit the slot
@@ -648,6 +688,7 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         const int64_t groups = K / kGroup;
         cfg.chunks_per_split = (int)((groups + p.split_k - 1) / p.split_k);
         cfg.depth = p.depth;
+        cfg.cw = p.tile_n == 256 ? 2 : 4;
         a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kPartialsOffset)
                                    : nullptr;
         e = launch_gemv(a, cfg, static_cast<uint32_t*>(workspace), s);
@@ -832,6 +873,7 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
     if (d != AWQ_OK) return d;
     switch (path) {
         case AWQ_PATH_AUTO:
+            if (auto_pairs(M, N, K) && pair_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (M == 1 || (M <= kGemvMaxM && N % 32 != 0)) return gemv_plan(M, N, K, plan);
             if (deep_small_m_tile_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (auto_stream(M, N, K) && stream_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;

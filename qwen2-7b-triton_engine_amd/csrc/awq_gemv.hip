@@ -198,11 +198,16 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 // ---------------------------------------------------------------------------
 // Variant 5: column-quad GEMV, interleaved 32-row chunks, fixed-point split-K.
 //
-// Lane l: c4 = l % 16 owns packed columns 4*c4 .. 4*c4+3 of the workgroup's
-// 64-column strip (32 outputs) and reads them with one 16-byte load per row,
-// so the 16 lanes of a row cover one 256-byte row segment; rq = l / 16 picks
-// rows 4*rq .. 4*rq+3 of each 16-row half of a 32-row chunk (one load
-// instruction = four row segments, eight per chunk).
+// Lane l: c4 = l % 16 owns packed columns CW*c4 .. CW*c4+CW-1 of the
+// workgroup's 16 CW-column strip (8 CW outputs) and reads them with one
+// 4 CW-byte load per row, so the 16 lanes of a row cover one 64 CW-byte row
+// segment; rq = l / 16 picks rows 4*rq .. 4*rq+3 of each 16-row half of a
+// 32-row chunk (one load instruction = four row segments, eight per chunk).
+// CW = 4 (column quads): 512-column strips, 256-byte segments, M <= 2.
+// CW = 2 (column pairs): 256-column strips, 128-byte segments, M <= 4 (the
+// accumulators are 8 CW per row of x): twice the strips of the quads, so the
+// same grid needs half the K splits, and the fixed-point finish half the
+// atomics.
 //
 // Work split: the K/32 chunks of a strip are divided evenly among split_k
 // workgroups (the planner keeps split_k * strips within one workgroup per
@@ -226,14 +231,14 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 // one column are its B fragment as they are (lane n = c4, k-block = rq: the
 // MFMA operand layout), x rows m = c4 < M supply A in the same k order, and
 // an MFMA against ones gives sum_r x[r]; the MFMA sums the 32 rows inside the
-// chunk, so lane (c4, rq = 0) holds row m of its 32 columns in register m
+// chunk, so lane (c4, rq = 0) holds row m of its 8 CW columns in register m
 // and no cross-lane reduction is needed.  After each chunk acc += s * sum -
 // s(b + z) * sum_x for the M live rows.  At the end the waves are added
 // through LDS and each output's partial is stored (split_k == 1) or goes
 // through the fixed-point finish.  Needs N % 32 == 0 (whole quads).
 constexpr int kQuadItemsPerThread = 4;  // prologue loads per thread (consts and x each)
 
-template <int MR, int D, bool NT>
+template <int MR, int D, bool NT, int CW>
 __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int split_k, unsigned long long* fix) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int lane = threadIdx.x & 63;
@@ -241,11 +246,13 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     const int nw = blockDim.x >> 6;
     const int c4 = lane & 15;
     const int rq = lane >> 4;
+    constexpr int SP = 16 * CW;  // packed columns of a strip
+    constexpr int SC = 8 * SP;   // output columns of a strip
     const int pn = a.N >> 3;
-    const int n_strips = (pn + 63) / 64;
+    const int n_strips = (pn + SP - 1) / SP;
     const int strip = blockIdx.x % n_strips;
     const int split = blockIdx.x / n_strips;
-    const int jl = min(strip * 64 + 4 * c4, pn - 4);  // in-range quad; lanes past pn drop their results
+    const int jl = min(strip * SP + CW * c4, pn - CW);  // in-range columns; lanes past pn drop their results
     const int C = a.K / 32;
     const int c0 = (int)((int64_t)C * split / split_k);
     const int c1 = (int)((int64_t)C * (split + 1) / split_k);
@@ -261,11 +268,11 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     const uint32_t row_bytes = (uint32_t)pn * 4u;
     const uint32_t voff_w = (uint32_t)(4 * rq) * row_bytes + (uint32_t)jl * 4u;
 
-    // LDS: consts float4 [n_g][16][16] ((s', s'(1024+z')) of two columns, indexed
-    // [group][column pair i][lane quad c4]: one wave-wide read is 256
-    // consecutive bytes), then x [MR][nc * 32] fp16.
+    // LDS: consts float4 [n_g][4 CW][16] ((s', s'(1024+z')) of two columns,
+    // indexed [group][column pair i of the lane][lane c4]: one wave-wide read
+    // is 256 consecutive bytes), then x [MR][nc * 32] fp16.
     floatx4* lc = reinterpret_cast<floatx4*>(lds);
-    half_t* lx = reinterpret_cast<half_t*>(lds + n_g * 16 * 16 * 4);
+    half_t* lx = reinterpret_cast<half_t*>(lds + n_g * (4 * CW) * 16 * 4);
 
     // Prologue loads: item (g, j) = zero word and 8 scales of packed column j
     // of group g_lo + g; x in 16-byte pieces.  Issued before the weights.
@@ -276,9 +283,9 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
 #pragma unroll
     for (int i = 0; i < kQuadItemsPerThread; ++i) {
-        const int item = min((int)threadIdx.x + i * nt, max(n_g * 64 - 1, 0));
-        const int g = g_lo + item / 64;
-        const int j = min(strip * 64 + item % 64, pn - 1);
+        const int item = min((int)threadIdx.x + i * nt, max(n_g * SP - 1, 0));
+        const int g = g_lo + item / SP;
+        const int j = min(strip * SP + item % SP, pn - 1);
         zv[i] = buf_load_b32(rz, (uint32_t)(g * pn + j) * 4u, 0u);
         sv[i] = buf_load_u4(rs, (uint32_t)(((size_t)g * a.N + 8 * j) * 2), 0u);
         const int xi = (int)threadIdx.x + i * nt;  // x piece: row m, 8 rows at c0*32 + 8 * (xi % (nc * 4))
@@ -287,8 +294,9 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         xv[i] = buf_load_u4(rx, m < MR ? xoff : 0x80000000u, 0u);
     }
 
+    typedef uint32_t cw_t __attribute__((ext_vector_type(CW)));
     struct Chunk {
-        u32x4 w[8];
+        cw_t w[8];
     };
     // Chunk c (rows 32c .. 32c+31); chunks past the wave's range read zeros.
     auto load_chunk = [&](int c, Chunk& ck) {
@@ -297,7 +305,13 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         const uint32_t r0 = live ? (uint32_t)c * 32u : 0u;
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-            ck.w[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + oob, (r0 + (u & 3) + 16 * (u >> 2)) * row_bytes, NT ? kCpolNT : 0));
+        {
+            const uint32_t so = (r0 + (u & 3) + 16 * (u >> 2)) * row_bytes;
+            if constexpr (CW == 4)
+                ck.w[u] = __builtin_bit_cast(cw_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + oob, so, NT ? kCpolNT : 0));
+            else
+                ck.w[u] = __builtin_bit_cast(cw_t, __builtin_amdgcn_raw_buffer_load_b64(rw, voff_w + oob, so, NT ? kCpolNT : 0));
+        }
     };
     // Ring of D chunk buffers: the wave's chunks i = 0, 1, ... (chunk c0 + wave
     // + i * nw) go to buffer i % D; chunk i + D is loaded right after chunk i
@@ -313,9 +327,9 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
 #pragma unroll
     for (int i = 0; i < kQuadItemsPerThread; ++i) {
         const int item = (int)threadIdx.x + i * nt;
-        if (item < n_g * 64) {
-            const int g = item / 64;
-            const int j = item % 64;  // packed column of the strip: lane quad j / 4, columns 8 (j % 4) + c
+        if (item < n_g * SP) {
+            const int g = item / SP;
+            const int j = item % SP;  // packed column of the strip: lane j / CW, its columns 8 (j % CW) + c
             const half8_t s8 = __builtin_bit_cast(half8_t, sv[i]);
 #pragma unroll
             for (int c = 0; c < 8; c += 2) {
@@ -329,19 +343,19 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
                     v[2 * h] = sc;
                     v[2 * h + 1] = sc * zz;
                 }
-                const int col = 8 * (j % 4) + c;  // column of the lane quad: pair index col / 2
-                lc[(g * 16 + col / 2) * 16 + j / 4] = v;
+                const int col = 8 * (j % CW) + c;  // column of the lane: pair index col / 2
+                lc[(g * (4 * CW) + col / 2) * 16 + j / CW] = v;
             }
         }
         if (item < MR * nc * 4) *reinterpret_cast<u32x4*>(lx + 8 * item) = xv[i];
     }
     __syncthreads();
 
-    float acc[MR][32];
+    float acc[MR][8 * CW];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc[m][i] = 0.f;
+        for (int i = 0; i < 8 * CW; ++i) acc[m][i] = 0.f;
     const uint32_t ones = 0x3C003C00u;  // fp16 (1, 1)
 
     // A = x rows (zero for lanes c4 >= M), S = row sums of x.
@@ -358,7 +372,7 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         const floatx4 S = mfma16x16x32(xa, __builtin_bit_cast(half8_t, u32x4{ones, ones, ones, ones}), zero4);
         const int gi = c / 4 - g_lo;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
+        for (int p = 0; p < CW; ++p) {
             uint32_t kp[4][8];
 #pragma unroll
             for (int h = 0; h < 2; ++h)
@@ -366,7 +380,7 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
                 for (int i = 0; i < 2; ++i) kpairs_magic_inplace(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp[2 * h + i]);
 #pragma unroll
             for (int cc = 0; cc < 8; cc += 2) {
-                const floatx4 v = lc[(gi * 16 + (8 * p + cc) / 2) * 16 + c4];
+                const floatx4 v = lc[(gi * (4 * CW) + (8 * p + cc) / 2) * 16 + c4];
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     const int col = 8 * p + cc + e;
@@ -398,14 +412,14 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
-            for (int i = 0; i < 32; i += 4)
-                *reinterpret_cast<floatx4*>(&red[(wave * MR + m) * 512 + 32 * c4 + i]) =
+            for (int i = 0; i < 8 * CW; i += 4)
+                *reinterpret_cast<floatx4*>(&red[(wave * MR + m) * SC + 8 * CW * c4 + i]) =
                     floatx4{acc[m][i], acc[m][i + 1], acc[m][i + 2], acc[m][i + 3]};
     }
     __syncthreads();
-    // Thread t finishes outputs t, t + nt, ... of the strip (at most 512 / 64
-    // = 8 per row of x) in one batch: one memory round trip per thread.
-    constexpr int kOwn = 512 / 64;
+    // Thread t finishes outputs t, t + nt, ... of the strip (at most SC / 64
+    // per row of x) in one batch: one memory round trip per thread.
+    constexpr int kOwn = SC / 64;
     float fs[kOwn * MR];
     int fm[kOwn * MR], fn[kOwn * MR];
     bool fok[kOwn * MR];
@@ -415,12 +429,12 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         for (int m = 0; m < MR; ++m) {
             const int t = threadIdx.x + i * nt;
             float s = 0.f;
-            if (t < 512)
-                for (int w = 0; w < nw; ++w) s += red[(w * MR + m) * 512 + t];
+            if (t < SC)
+                for (int w = 0; w < nw; ++w) s += red[(w * MR + m) * SC + t];
             fs[i * MR + m] = s;
             fm[i * MR + m] = m;
-            fn[i * MR + m] = strip * 512 + t;
-            fok[i * MR + m] = t < 512 && strip * 512 + t < a.N && m < a.M;
+            fn[i * MR + m] = strip * SC + t;
+            fok[i * MR + m] = t < SC && strip * SC + t < a.N && m < a.M;
         }
     finish_batch<kOwn * MR>(fix, a.out, a.bias, a.residual, a.M, a.N, split_k, fs, fm, fn, fok);
 }
@@ -432,28 +446,33 @@ int64_t gemv_quad_max_groups(int K, int split_k) {
     return (per + 2) / 4 + 1;
 }
 
-// LDS of the column-quad GEMV: staged consts (4 KiB per group) and x rows,
-// or the cross-wave reduction buffer, whichever is larger.
-size_t gemv_quad_lds_bytes(int M, int K, int split_k, int k_waves) {
+// Rows of x a column-quad / column-pair GEMV instance carries for M rows.
+static int gemv_quad_mr(int M) { return M <= 1 ? 1 : (M <= 2 ? 2 : 4); }
+
+// LDS of the column-quad (cw 4) or column-pair (cw 2) GEMV: staged consts
+// (1 KiB x cw per group) and x rows, or the cross-wave reduction buffer,
+// whichever is larger.
+size_t gemv_quad_lds_bytes(int M, int K, int split_k, int k_waves, int cw) {
     const int64_t C = K / 32;
     const int64_t per = (C + split_k - 1) / split_k;
-    const int mr = M <= 1 ? 1 : 2;
-    const size_t staged = (size_t)gemv_quad_max_groups(K, split_k) * 4096 + (size_t)mr * per * 64;
-    const size_t red = (size_t)k_waves * mr * 512 * 4;
+    const int mr = gemv_quad_mr(M);
+    const size_t staged = (size_t)gemv_quad_max_groups(K, split_k) * 1024 * cw + (size_t)mr * per * 64;
+    const size_t red = (size_t)k_waves * mr * 128 * cw * 4;
     return staged > red ? staged : red;
 }
 
 // Whether the prologue's fixed number of loads per thread covers the shape.
-bool gemv_quad_fits(int M, int K, int split_k, int k_waves) {
+bool gemv_quad_fits(int M, int K, int split_k, int k_waves, int cw) {
     const int64_t C = K / 32;
     const int64_t per = (C + split_k - 1) / split_k;
     const int64_t threads = 64 * (int64_t)k_waves;
-    const int mr = M <= 1 ? 1 : 2;
-    return gemv_quad_max_groups(K, split_k) * 64 <= kQuadItemsPerThread * threads &&
+    const int mr = gemv_quad_mr(M);
+    return gemv_quad_max_groups(K, split_k) * 16 * cw <= kQuadItemsPerThread * threads &&
            mr * per * 4 <= kQuadItemsPerThread * threads;
 }
 
 int64_t gemv_strips(int N) { return ((N >> 3) + 63) / 64; }
+int64_t gemv_strips_cw(int N, int cw) { return ((N >> 3) + 16 * cw - 1) / (16 * cw); }
 
 template <int MR, int R, int D>
 static hipError_t gemv_stream_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
@@ -464,33 +483,44 @@ static hipError_t gemv_stream_launch(const GemmArgs& a, const GemvConfig& cfg, u
     return hipGetLastError();
 }
 
-template <int MR, int D>
+template <int MR, int D, int CW>
 static hipError_t gemv_quad_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
                                    hipStream_t stream) {
     unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
-    const size_t lds = gemv_quad_lds_bytes(a.M, a.K, cfg.split_k, cfg.kw_count);
+    const size_t lds = gemv_quad_lds_bytes(a.M, a.K, cfg.split_k, cfg.kw_count, CW);
+    const dim3 grid((unsigned)(gemv_strips_cw(a.N, CW) * cfg.split_k)), block(64 * cfg.kw_count);
     // Weight loads marked non-temporal where each workgroup streams a long
     // K range (few splits): 3584 x 37888 at split 3 measured 2.7 - 4.7 %
     // faster with them at M = 1 - 16, the 100 - 500-row ranges of 18 - 36
     // splits up to 3 % slower.
     if (cfg.split_k <= kNonTemporalMaxSplit)
-        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, true>), dim3((unsigned)(gemv_strips(a.N) * cfg.split_k)),
-                           dim3(64 * cfg.kw_count), lds, stream, a, cfg.split_k, fix);
+        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, true, CW>), grid, block, lds, stream, a, cfg.split_k, fix);
     else
-        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, false>), dim3((unsigned)(gemv_strips(a.N) * cfg.split_k)),
-                           dim3(64 * cfg.kw_count), lds, stream, a, cfg.split_k, fix);
+        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, false, CW>), grid, block, lds, stream, a, cfg.split_k, fix);
     return hipGetLastError();
 }
 
 static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
                                      hipStream_t stream) {
+    if (cfg.cw == 2) {
+        switch (gemv_quad_mr(a.M) * 10 + cfg.depth) {
+            case 12: return gemv_quad_launch<1, 2, 2>(a, cfg, counters, stream);
+            case 13: return gemv_quad_launch<1, 3, 2>(a, cfg, counters, stream);
+            case 22: return gemv_quad_launch<2, 2, 2>(a, cfg, counters, stream);
+            case 23: return gemv_quad_launch<2, 3, 2>(a, cfg, counters, stream);
+            case 42: return gemv_quad_launch<4, 2, 2>(a, cfg, counters, stream);
+            case 43: return gemv_quad_launch<4, 3, 2>(a, cfg, counters, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    if (cfg.cw != 4 || a.M > 2) return hipErrorInvalidValue;
     switch ((a.M <= 1 ? 10 : 20) + cfg.depth) {
-        case 12: return gemv_quad_launch<1, 2>(a, cfg, counters, stream);
-        case 13: return gemv_quad_launch<1, 3>(a, cfg, counters, stream);
-        case 14: return gemv_quad_launch<1, 4>(a, cfg, counters, stream);
-        case 22: return gemv_quad_launch<2, 2>(a, cfg, counters, stream);
-        case 23: return gemv_quad_launch<2, 3>(a, cfg, counters, stream);
-        case 24: return gemv_quad_launch<2, 4>(a, cfg, counters, stream);
+        case 12: return gemv_quad_launch<1, 2, 4>(a, cfg, counters, stream);
+        case 13: return gemv_quad_launch<1, 3, 4>(a, cfg, counters, stream);
+        case 14: return gemv_quad_launch<1, 4, 4>(a, cfg, counters, stream);
+        case 22: return gemv_quad_launch<2, 2, 4>(a, cfg, counters, stream);
+        case 23: return gemv_quad_launch<2, 3, 4>(a, cfg, counters, stream);
+        case 24: return gemv_quad_launch<2, 4, 4>(a, cfg, counters, stream);
         default: return hipErrorInvalidValue;
     }
 }

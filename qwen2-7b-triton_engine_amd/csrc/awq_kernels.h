@@ -39,6 +39,7 @@ struct GemvConfig {
     int split_k;             // workgroups along K
     int chunks_per_split;    // variant 2: 128-row groups per workgroup
     int depth;               // variant 2: chunk buffers in flight (2, 3 or 4; 4 only for 16 rows per wave)
+    int cw;                  // variant 5: packed columns per lane, 4 (512-column strips) or 2 (256)
 };
 
 // Tile variants 6 .. 9, 13, 14: weights dequantised into MFMA registers,
@@ -91,9 +92,10 @@ size_t skinny_counter_bytes();
 // 64-bit fixed-point slots (left zero on return) instead of partials.
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream);
 int64_t gemv_strips(int N);
-size_t gemv_quad_lds_bytes(int M, int K, int split_k, int k_waves);
+int64_t gemv_strips_cw(int N, int cw);
+size_t gemv_quad_lds_bytes(int M, int K, int split_k, int k_waves, int cw);
 int64_t gemv_quad_max_groups(int K, int split_k);
-bool gemv_quad_fits(int M, int K, int split_k, int k_waves);
+bool gemv_quad_fits(int M, int K, int split_k, int k_waves, int cw);
 
 // Stream path (M <= 16, N % 32 == 0, split_k <= K / 128).  layout:
 // kStreamRowLayout (M <= 8; 16-row chunks, k_waves waves) or

@@ -85,7 +85,13 @@ def test_auto_plan_invariants(L, m, k, n):
     # split where that grid covers every CU and fits two workgroups per CU
     deep_split = -(-(k // 128) // 5)
     deep_tile = 9 <= m <= 16 and k >= 8192 and strips < 16 and 256 <= -(-n // 256) * deep_split <= 512
-    if m == 1 or (m == 2 and n % 32 != 0):
+    # column pairs (256-column strips) on narrow weights: M <= 2, or M <= 4 when K < 8192
+    strips256 = -(-(n // 8) // 32)
+    pairs = n % 32 == 0 and strips < 16 and strips256 >= 8 and (m <= 2 or (m <= 4 and k < 8192))
+    if pairs:
+        assert p.path == _native.PATH_GEMV and p.variant == 5 and p.tile_n == 256 and p.tile_m >= m
+        assert 0.5 * 256 < p.grid <= 256
+    elif m == 1 or (m == 2 and n % 32 != 0):
         assert p.path == _native.PATH_GEMV
     elif deep_tile:
         assert p.path == _native.PATH_TILE and p.variant == 9 and p.split_k == deep_split
@@ -147,17 +153,22 @@ def test_auto_plan_falls_back_when_slots_do_not_fit(L, m, n, k):
         assert p.workspace_bytes == _native.counter_bytes() + _native.SLOT_BYTES + p.split_k * m * n * 4
 
 
-def test_auto_stream_split_keeps_a_group_and_a_half_per_split(L):
-    """K = 3584 (28 groups) at M = 2 .. 4: 18 splits, the cap of 2 x groups / 3;
-    M = 2 takes the half-strip layout with two wave pairs there, the row layout
-    with four waves on deep weights (148 groups, 36 splits)."""
+def test_stream_split_keeps_a_group_and_a_half_per_split(L):
+    """The stream planner (AUTO's choice at M = 2 .. 4 on wide weights, and
+    the explicit stream path elsewhere): K = 3584 (28 groups) at M = 2 .. 4
+    gets 18 splits, the cap of 2 x groups / 3; M = 2 takes the half-strip
+    layout with two wave pairs there, the row layout with four waves on deep
+    weights (148 groups, 36 splits)."""
+    S = _native.PATH_STREAM
     for m in (2, 3, 4):
         for n in (4608, 3584):
-            p = _native.plan_for(m, n, 3584)
-            assert p.path == _native.PATH_STREAM and p.split_k == 18
-    p = _native.plan_for(2, 4608, 3584)
+            p = _native.plan_for(m, n, 3584, path=S)
+            assert p.path == S and p.split_k == 18
+        p = _native.plan_for(m, 37888, 3584)
+        assert p.path == S and p.split_k == 3
+    p = _native.plan_for(2, 4608, 3584, path=S)
     assert (p.rows_per_wave, p.k_waves, p.depth, p.variant) == (32, 2, 2, 1)
-    p = _native.plan_for(2, 3584, 18944)
+    p = _native.plan_for(2, 3584, 18944, path=S)
     assert (p.rows_per_wave, p.k_waves, p.depth, p.split_k) == (16, 4, 2, 36)
 
 
