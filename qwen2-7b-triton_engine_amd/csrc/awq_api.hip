@@ -147,8 +147,9 @@ constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 // see below.
 int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, int64_t rows_per_wave,
               int64_t k_waves, int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
-    // Column pairs (variant 5 with 256-column strips) carry up to 4 rows of x.
-    const bool pairs = variant == 5 && tile_n == 256;
+    // Column pairs and singles (variant 5 with 256- and 128-column strips)
+    // carry up to 4 rows of x.
+    const bool pairs = variant == 5 && (tile_n == 256 || tile_n == 128);
     if (M > (pairs ? kGemvPairMaxM : kGemvMaxM)) return AWQ_ERR_PATH;
     p->path = AWQ_PATH_GEMV;
     p->variant = (int32_t)variant;
@@ -168,7 +169,7 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
         // waves); split_k <= min(K/32, kFixMaxSplit); the groups and x rows a
         // workgroup stages must fit its prologue loads, and the staged data
         // its LDS.
-        const int cw = pairs ? 2 : 4;
+        const int cw = (int)(tile_n / 128);
         if (N % 32 != 0 || rows_per_wave != 0 || depth < 2 || depth > (pairs ? 3 : 4)) return AWQ_ERR_PATH;
         if (k_waves < 1 || k_waves > 8 || split_k < 1 || split_k > K / 32 || split_k > kFixMaxSplit)
             return AWQ_ERR_PATH;
@@ -235,17 +236,23 @@ int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_gemv(M, N, K, 5, 512, 0, w, split, 2, p);
 }
 
-// Column pairs (256-column strips, up to 4 rows of x) on narrow weights
-// (fewer than 16 strips of 512 columns): twice the strips of the quads, so
-// one workgroup per CU needs half the K splits and the fixed-point finish
-// half the atomics.  Four waves, two chunk buffers.  Measured against the
-// previous AUTO plans (graphs over >= 640 MB of weights): 3584 x 4608 at
-// M = 1 / 2 / 3 / 4 5.96 / 6.95 / 8.59 / 9.00 us against 7.47 / 8.13 / 9.06 /
-// 9.51; 3584 x 3584 5.66 / 6.71 / 8.55 / 8.92 against 6.79 / 7.96 / 8.82 /
-// 9.22; 18944 x 3584 at M = 1 / 2 11.12 / 12.27 against 12.28 / 12.92 (at
-// M = 3 the stream row kernel stays ahead, 13.8 against 14.3-14.7, so deep
-// weights take pairs only for M <= 2); on 3584 x 37888 the quads (M = 1) and
-// the stream kernels (M >= 2) stay within 2 % of the pairs or ahead.
+// Column pairs and singles (256- and 128-column strips, up to 4 rows of x)
+// on narrow weights (fewer than 16 strips of 512 columns): two and four
+// times the strips of the quads, so one workgroup per CU needs a half or a
+// quarter of the K splits, and the fixed-point finish as few atomics.
+// Measured against the previous AUTO plans (graphs over >= 640 MB of
+// weights; us):
+//   3584 x 4608, M = 1 / 2 / 3 / 4: pairs 5.86 / 6.87 / 8.64 / 8.93, singles
+//     6.18 / 6.70 / 7.60 / 7.78, before 7.47 / 8.13 / 9.06 / 9.51;
+//   3584 x 3584: pairs 5.66 / 6.68 / 8.57 / 8.92, singles 5.82 / 6.39 / 7.28 /
+//     7.44, before 6.79 / 7.96 / 8.82 / 9.22;
+//   18944 x 3584 (eight waves), M = 1 / 2: pairs 11.19 / 12.14, before 12.28 /
+//     12.92; at M = 3 / 4 the stream row kernel stays (13.8 / 14.8 against
+//     14.4 / 14.4 for pairs), singles are slower on these deep weights;
+//   3584 x 37888: the quads (M = 1) and stream kernels (M >= 2) stay within
+//     2 % of the pairs or ahead.
+// So: shallow weights take pairs at M = 1 and singles at M = 2 .. 4, deep
+// ones pairs at M <= 2.
 bool auto_pairs(int64_t M, int64_t N, int64_t K) {
     // Measured on 3584 - 4608 columns (14 - 18 strips of 256); narrower
     // weights keep the plans measured for them.
@@ -254,20 +261,21 @@ bool auto_pairs(int64_t M, int64_t N, int64_t K) {
 }
 
 int pair_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    const int64_t strips = gemv_strips_cw((int)N, 2);
+    const int cw = (K < 8192 && M >= 2) ? 1 : 2;
+    const int64_t strips = gemv_strips_cw((int)N, cw);
     const int64_t C = K / 32;
     int64_t split = cus() / strips;
     if (split > C) split = C;
     if (split > kFixMaxSplit) split = kFixMaxSplit;
     if (split < 1) split = 1;
-    int64_t w = 4;
-    while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w, 2) ||
-           gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w, 2) > kQuadLdsBudget) {
+    int64_t w = K >= 8192 ? 8 : 4;
+    while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w, cw) ||
+           gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w, cw) > kQuadLdsBudget) {
         if (w < 8) ++w;
         else if (split < C && split < kFixMaxSplit) ++split;
         else return AWQ_ERR_PATH;
     }
-    return fill_gemv(M, N, K, 5, 256, 0, w, split, 2, p);
+    return fill_gemv(M, N, K, 5, 128 * cw, 0, w, split, 2, p);
 }
 
 // Column quads while their fixed-point slots (M x N x 8 bytes) fit the slot
@@ -688,7 +696,7 @@ int run_plan(const void* x, const int32_t* qweight, const int32_t* qzeros, const
         const int64_t groups = K / kGroup;
         cfg.chunks_per_split = (int)((groups + p.split_k - 1) / p.split_k);
         cfg.depth = p.depth;
-        cfg.cw = p.tile_n == 256 ? 2 : 4;
+        cfg.cw = p.tile_n / 128;
         a.partials = p.split_k > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kPartialsOffset)
                                    : nullptr;
         e = launch_gemv(a, cfg, static_cast<uint32_t*>(workspace), s);

@@ -13,6 +13,8 @@
 // cut in place, see awq_device.h), the lanes accumulate
 // sum_r x[r] * (b + q[r]) and sum_r x[r], and each group folds
 // s * (that - (b + z) * sum_r x[r]) in fp32 once.
+#include <type_traits>
+
 #include "awq_kernels.h"
 
 namespace awq {
@@ -294,9 +296,17 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         xv[i] = buf_load_u4(rx, m < MR ? xoff : 0x80000000u, 0u);
     }
 
-    typedef uint32_t cw_t __attribute__((ext_vector_type(CW)));
+    typedef uint32_t cwv_t __attribute__((ext_vector_type(CW < 2 ? 2 : CW)));
+    using cw_t = std::conditional_t<CW == 1, uint32_t, cwv_t>;
     struct Chunk {
         cw_t w[8];
+    };
+    // Packed column p of the lane's words.
+    auto word = [](const cw_t& v, int p) -> uint32_t {
+        if constexpr (CW == 1)
+            return v;
+        else
+            return v[p];
     };
     // Chunk c (rows 32c .. 32c+31); chunks past the wave's range read zeros.
     auto load_chunk = [&](int c, Chunk& ck) {
@@ -309,8 +319,10 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
             const uint32_t so = (r0 + (u & 3) + 16 * (u >> 2)) * row_bytes;
             if constexpr (CW == 4)
                 ck.w[u] = __builtin_bit_cast(cw_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + oob, so, NT ? kCpolNT : 0));
-            else
+            else if constexpr (CW == 2)
                 ck.w[u] = __builtin_bit_cast(cw_t, __builtin_amdgcn_raw_buffer_load_b64(rw, voff_w + oob, so, NT ? kCpolNT : 0));
+            else
+                ck.w[u] = __builtin_amdgcn_raw_buffer_load_b32(rw, voff_w + oob, so, NT ? kCpolNT : 0);
         }
     };
     // Ring of D chunk buffers: the wave's chunks i = 0, 1, ... (chunk c0 + wave
@@ -377,7 +389,8 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int i = 0; i < 2; ++i) kpairs_magic_inplace(ck.w[4 * h + 2 * i][p], ck.w[4 * h + 2 * i + 1][p], kp[2 * h + i]);
+                for (int i = 0; i < 2; ++i)
+                    kpairs_magic_inplace(word(ck.w[4 * h + 2 * i], p), word(ck.w[4 * h + 2 * i + 1], p), kp[2 * h + i]);
 #pragma unroll
             for (int cc = 0; cc < 8; cc += 2) {
                 const floatx4 v = lc[(gi * (4 * CW) + (8 * p + cc) / 2) * 16 + c4];
@@ -502,6 +515,17 @@ static hipError_t gemv_quad_launch(const GemmArgs& a, const GemvConfig& cfg, uin
 
 static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
                                      hipStream_t stream) {
+    if (cfg.cw == 1) {
+        switch (gemv_quad_mr(a.M) * 10 + cfg.depth) {
+            case 12: return gemv_quad_launch<1, 2, 1>(a, cfg, counters, stream);
+            case 13: return gemv_quad_launch<1, 3, 1>(a, cfg, counters, stream);
+            case 22: return gemv_quad_launch<2, 2, 1>(a, cfg, counters, stream);
+            case 23: return gemv_quad_launch<2, 3, 1>(a, cfg, counters, stream);
+            case 42: return gemv_quad_launch<4, 2, 1>(a, cfg, counters, stream);
+            case 43: return gemv_quad_launch<4, 3, 1>(a, cfg, counters, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
     if (cfg.cw == 2) {
         switch (gemv_quad_mr(a.M) * 10 + cfg.depth) {
             case 12: return gemv_quad_launch<1, 2, 2>(a, cfg, counters, stream);

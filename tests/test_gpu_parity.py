@@ -388,12 +388,13 @@ def test_gemv_quad_plans_agree(gpu, m):
     assert tried >= 80
 
 
+@pytest.mark.parametrize("tile_n", [256, 128])
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
-def test_gemv_pair_plans_agree(gpu, m):
-    """Column-pair GEMV (256-column strips, up to 4 rows of x, fixed-point
-    split-K finish): split counts from 1 up to one 32-row chunk per workgroup,
-    wave counts 1 - 8, ring depths 2 and 3, on an N whose last 256-column
-    strip holds two lanes' columns."""
+def test_gemv_pair_plans_agree(gpu, m, tile_n):
+    """Column-pair and column-single GEMV (256- and 128-column strips, up to 4
+    rows of x, fixed-point split-K finish): split counts from 1 up to one
+    32-row chunk per workgroup, wave counts 1 - 8, ring depths 2 and 3, on an
+    N whose last strip is partly filled (1056 = 4 x 256 + 32 = 8 x 128 + 32)."""
     k, n = 3584, 1056
     x, qw, qz, s = O.make_inputs(m, k, n, seed=25 + m)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)
@@ -402,12 +403,12 @@ def test_gemv_pair_plans_agree(gpu, m):
         for kw in (1, 2, 4, 8):
             for depth in (2, 3):
                 try:
-                    p = _native.plan_gemv(m, n, k, 0, kw, variant=5, split_k=split, depth=depth, tile_n=256)
+                    p = _native.plan_gemv(m, n, k, 0, kw, variant=5, split_k=split, depth=depth, tile_n=tile_n)
                 except _native.AwqNativeError:
                     continue
-                print(f"gemv pair plan M={m} split={split} k_waves={kw} depth={depth}", flush=True)
+                print(f"gemv {tile_n}-column strips M={m} split={split} k_waves={kw} depth={depth}", flush=True)
                 y = _run(gpu, x, qw, qz, s, plan_obj=p)
-                _assert_close(y, y_ref, f"gemv pair M={m} split={split} kw={kw} d={depth}")
+                _assert_close(y, y_ref, f"gemv {tile_n} M={m} split={split} kw={kw} d={depth}")
                 tried += 1
     assert tried >= 40
 
