@@ -252,8 +252,17 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     constexpr int SC = 8 * SP;   // output columns of a strip
     const int pn = a.N >> 3;
     const int n_strips = (pn + SP - 1) / SP;
-    const int strip = blockIdx.x % n_strips;
-    const int split = blockIdx.x / n_strips;
+    // Work item w = (split, strip), strip fastest, numbered in XCD order:
+    // workgroups are dispatched round-robin over the 8 XCDs (workgroup b on
+    // XCD b % 8), and the workgroups one XCD runs get consecutive items, so
+    // neighbouring strips run on one XCD -- with 128-column strips (64-byte
+    // row segments) two strips share each 128-byte line, which one L2 then
+    // fetches once.  Any numbering is correct; this one is about traffic.
+    const int total = (int)gridDim.x;
+    const int xb = (int)blockIdx.x & 7, xi = (int)blockIdx.x >> 3, per_x = (total + 7) >> 3, rem_x = total & 7;
+    const int w_item = (rem_x == 0 || xb < rem_x) ? xb * per_x + xi : rem_x * per_x + (xb - rem_x) * (per_x - 1) + xi;
+    const int strip = w_item % n_strips;
+    const int split = w_item / n_strips;
     const int jl = min(strip * SP + CW * c4, pn - CW);  // in-range columns; lanes past pn drop their results
     const int C = a.K / 32;
     const int c0 = (int)((int64_t)C * split / split_k);
