@@ -138,6 +138,7 @@ bool auto_skinny(int64_t M, int64_t /*N*/) { return M <= 16; }
 // Largest M the GEMV path serves.
 constexpr int64_t kGemvMaxM = 2;
 constexpr int64_t kGemvPairMaxM = 4;
+constexpr int64_t kGemvSingleMaxM = 4;
 // LDS the column-quad GEMV may stage per workgroup.
 constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 
@@ -236,32 +237,30 @@ int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_gemv(M, N, K, 5, 512, 0, w, split, 2, p);
 }
 
-// Column pairs and singles (256- and 128-column strips, up to 4 rows of x)
-// on narrow weights (fewer than 16 strips of 512 columns): two and four
-// times the strips of the quads, so one workgroup per CU needs a half or a
-// quarter of the K splits, and the fixed-point finish as few atomics.
+// Column singles (128-column strips, up to 4 rows of x) on narrow weights
+// (fewer than 16 strips of 512 columns): four times the strips of the
+// quads, so one workgroup per CU needs a quarter of the K splits, and the
+// fixed-point finish a quarter of the atomics.  Two strips share each
+// 128-byte line; the kernel's XCD-ordered work items keep them on one L2.
 // Measured against the previous AUTO plans (graphs over >= 640 MB of
-// weights; us):
-//   3584 x 4608, M = 1 / 2 / 3 / 4: pairs 5.86 / 6.87 / 8.64 / 8.93, singles
-//     6.18 / 6.70 / 7.60 / 7.78, before 7.47 / 8.13 / 9.06 / 9.51;
-//   3584 x 3584: pairs 5.66 / 6.68 / 8.57 / 8.92, singles 5.82 / 6.39 / 7.28 /
-//     7.44, before 6.79 / 7.96 / 8.82 / 9.22;
-//   18944 x 3584 (eight waves), M = 1 / 2: pairs 11.19 / 12.14, before 12.28 /
-//     12.92; at M = 3 / 4 the stream row kernel stays (13.8 / 14.8 against
-//     14.4 / 14.4 for pairs), singles are slower on these deep weights;
-//   3584 x 37888: the quads (M = 1) and stream kernels (M >= 2) stay within
-//     2 % of the pairs or ahead.
-// So: shallow weights take pairs at M = 1 and singles at M = 2 .. 4, deep
-// ones pairs at M <= 2.
+// weights; us), M = 1 / 2 / 3 / 4:
+//   3584 x 4608 (four waves): singles 5.77 / 6.44 / 7.36 / 7.56, pairs (256
+//     columns) 5.89 / - / - / -, before 7.47 / 8.13 / 9.06 / 9.51;
+//   3584 x 3584 (four waves): singles 5.59 / 6.26 / 7.18 / 7.31, pairs 5.72,
+//     before 6.79 / 7.96 / 8.82 / 9.22;
+//   18944 x 3584 (eight waves): singles 10.98 / 11.50 / 12.46 / 12.56, pairs
+//     11.03 / 12.12, before 12.28 / 12.92 / 13.75 / 14.67;
+//   3584 x 37888: the quads (M = 1) and stream kernels (M >= 2) stay ahead
+//     (unsplit singles and pairs stream too long a K range per workgroup).
 bool auto_pairs(int64_t M, int64_t N, int64_t K) {
-    // Measured on 3584 - 4608 columns (14 - 18 strips of 256); narrower
+    // Measured on 3584 - 4608 columns (28 - 36 strips of 128); narrower
     // weights keep the plans measured for them.
     if (N % 32 != 0 || gemv_strips((int)N) >= 16 || gemv_strips_cw((int)N, 2) < 8) return false;
-    return M <= 2 || (M <= kGemvPairMaxM && K < 8192);
+    return M <= kGemvSingleMaxM;
 }
 
 int pair_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
-    const int cw = (K < 8192 && M >= 2) ? 1 : 2;
+    const int cw = 1;
     const int64_t strips = gemv_strips_cw((int)N, cw);
     const int64_t C = K / 32;
     int64_t split = cus() / strips;

@@ -85,12 +85,11 @@ def test_auto_plan_invariants(L, m, k, n):
     # split where that grid covers every CU and fits two workgroups per CU
     deep_split = -(-(k // 128) // 5)
     deep_tile = 9 <= m <= 16 and k >= 8192 and strips < 16 and 256 <= -(-n // 256) * deep_split <= 512
-    # column pairs (256-column strips) on narrow weights: M <= 2, or M <= 4 when K < 8192
+    # column singles (128-column strips) on narrow weights at M <= 4
     strips256 = -(-(n // 8) // 32)
-    pairs = n % 32 == 0 and strips < 16 and strips256 >= 8 and (m <= 2 or (m <= 4 and k < 8192))
+    pairs = n % 32 == 0 and strips < 16 and strips256 >= 8 and m <= 4
     if pairs:
-        assert p.path == _native.PATH_GEMV and p.variant == 5 and p.tile_m >= m
-        assert p.tile_n == (128 if (k < 8192 and m >= 2) else 256)
+        assert p.path == _native.PATH_GEMV and p.variant == 5 and p.tile_m >= m and p.tile_n == 128
         assert 0.5 * 256 < p.grid <= 256
     elif m == 1 or (m == 2 and n % 32 != 0):
         assert p.path == _native.PATH_GEMV
