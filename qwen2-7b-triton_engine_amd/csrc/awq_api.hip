@@ -595,7 +595,14 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (best_v != 0 && best_s == 1 && M >= 512) {
         double hbest = 0.0;
         int64_t hv = 0, hs = 0;
+        // The 64-row hybrid only where the 128-row one has no whole tile per
+        // CU: with its finish by helpers (the whole-tile workgroups add the
+        // leftover tiles' partials after their own tiles) the 128-row hybrid
+        // measured ahead wherever both apply (3584 x 4608 at M = 2048: 69.9 us
+        // at split 3 against 72.6 - 80.3 for the 64-row one at splits 2 - 4).
+        const bool v13_whole = tile_tiles((int)M, (int)N, 7) >= cus();
         for (int64_t v = 13; v <= 14; ++v) {
+            if (v == 14 && v13_whole) continue;
             const TileModel* t = tile_model(v == 13 ? 7 : 8);
             for (int64_t sp = 2; sp <= 8; ++sp) {
                 awq_w4a16_plan q;

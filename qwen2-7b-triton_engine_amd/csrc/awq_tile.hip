@@ -70,6 +70,15 @@ struct Parity {
 };
 }  // namespace
 
+// Hybrid tiles: bands per leftover tile whose partials are added by helpers
+// -- the largest power of two up to 8 with n_sk x bands whole-tile
+// workgroups to help (d of them) and bands of at least 16 rows.
+__device__ __forceinline__ int hy_bands(int n_sk, int d, int bm) {
+    int h = 1;
+    while (h < 8 && n_sk * 2 * h <= d && bm / (2 * h) >= 16) h *= 2;
+    return h;
+}
+
 // FIN (split_k > 1): 0 -- the last workgroup of a tile to arrive adds the
 // partials; 1 -- partials with plain stores, summed by a second launch of
 // awq_splitk_reduce_kernel over the whole device (for small tiles, whose
@@ -95,6 +104,7 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     static_assert(L::PER_CU >= 1 && L::PER_CU * S * L::STAGE <= 160 * 1024, "LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char smem[S * L::STAGE];
     __shared__ int last_flag;
+    __shared__ int last_band[8];
     floatx4* fin = reinterpret_cast<floatx4*>(smem);  // split-K finish, after the main loop
 
     const int tid = threadIdx.x;
@@ -134,12 +144,15 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         split = w - tile * split_k;
     }
     const int in_group = T5_GM * n_tiles;
-    const int first_m = (tile / in_group) * T5_GM;
-    const int gm = min(m_tiles - first_m, T5_GM);
-    const int tm = first_m + (tile % in_group) % gm;
-    const int tn = (tile % in_group) / gm;
-    const int m0 = tm * BM;
-    const int n0 = tn * T5_BN;
+    // Tile t's first row and column (tiles in groups of T5_GM row tiles).
+    auto tile_origin = [&](int t, int& tm0, int& tn0) {
+        const int first_m = (t / in_group) * T5_GM;
+        const int gm = min(m_tiles - first_m, T5_GM);
+        tm0 = (first_m + (t % in_group) % gm) * BM;
+        tn0 = ((t % in_group) / gm) * T5_BN;
+    };
+    int m0, n0;
+    tile_origin(tile, m0, n0);
     const int pn = a.N >> 3;
     const int k_begin = ks == 1 ? 0 : split * k_per_split;
     const int k_end = ks == 1 ? a.K : min(a.K, k_begin + k_per_split);
@@ -426,6 +439,27 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
             }
     }
     const int qcol = 64 * wn + 8 * (ekb >> 1) + 4 * (ekb & 1);  // + 16 c: the quad's first column in the tile
+    // Hybrids: add the split_k pieces' partials of band h (of hb) of leftover
+    // tile t ([split_k][n_sk][BM][256] fp32), write fp16, reset the band's
+    // counter.  Called by the whole workgroup.
+    auto hy_finish_band = [&](int t, int h, int hb) {
+        if constexpr (HY) {
+            int tm0, tn0;
+            tile_origin(n_tiles * m_tiles - n_sk + t, tm0, tn0);
+            const int br = BM / hb;
+            const int row0 = tm0 + h * br;
+            const uint32_t tile_bytes = (uint32_t)(BM * T5_BN * 4);
+            const PartLayout bp{(uint32_t)t * tile_bytes + (uint32_t)(h * br) * (uint32_t)(T5_BN * 4),
+                                (uint32_t)(T5_BN * 4), (uint32_t)n_sk * tile_bytes};
+            const __amdgpu_buffer_rsrc_t rpb = make_rsrc(a.partials, (uint32_t)split_k * bp.split_stride);
+            const int rows = min(br, a.M - row0);
+            if (rows > 0)
+                splitk_finish<(FM >= 8 ? 16 : 8)>(rpb, a.out, a.bias, a.residual, a.M, a.N, row0, rows, tn0,
+                                                  min(T5_BN, a.N - tn0), split_k, fin, bp);
+            if (tid == 0)
+                __hip_atomic_store(&counters[t * hb + h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
     if (ks == 1) {
         // The fp16 tile goes through LDS and leaves as whole rows: each
         // thread stores 16 bytes, 32 threads a 512-byte row, instead of every
@@ -462,6 +496,19 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
             }
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, h), ro, (uint32_t)(o * 2), 0, kCpolSC1);
         }
+        if constexpr (HY) {
+            // Whole-tile workgroup b < n_sk * H helps finish band b % H of
+            // leftover tile b / H (below).
+            const int hb = hy_bands(n_sk, (int)gridDim.x - n_sk * split_k, BM);
+            if ((int)blockIdx.x < n_sk * hb) {
+                __syncthreads();  // the staged tile's reads are done: the LDS becomes `fin`
+                if (tid == 0)
+                    last_flag = __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)split_k;
+                __syncthreads();
+                if (last_flag) hy_finish_band((int)blockIdx.x / hb, (int)blockIdx.x % hb, hb);
+            }
+        }
         return;
     }
 
@@ -489,6 +536,21 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     if constexpr (FIN == 1) return;
     wait_vm_stores();
     __syncthreads();
+    if constexpr (HY) {
+        // Band h of this leftover tile has a counter of its own that its
+        // split_k pieces and one helper (a whole-tile workgroup, after its
+        // own tile) each add 1 to; whoever brings it to split_k + 1 adds the
+        // band's partials.  The helpers run late, so usually they do, spread
+        // over many workgroups instead of one last piece per tile.
+        const int hb = hy_bands(n_sk, (int)gridDim.x - n_sk * split_k, BM);
+        if (tid < hb)
+            last_band[tid] = __hip_atomic_fetch_add(&counters[sk_tile * hb + tid], 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)split_k;
+        __syncthreads();
+        for (int h = 0; h < hb; ++h)
+            if (last_band[h]) hy_finish_band(sk_tile, h, hb);
+        return;
+    }
     if (tid == 0)
         last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                     (uint32_t)(split_k - 1);
