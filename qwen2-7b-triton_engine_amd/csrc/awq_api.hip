@@ -137,8 +137,8 @@ bool auto_skinny(int64_t M, int64_t /*N*/) { return M <= 16; }
 
 // Largest M the GEMV path serves.
 constexpr int64_t kGemvMaxM = 2;
-constexpr int64_t kGemvPairMaxM = 4;
-constexpr int64_t kGemvSingleMaxM = 4;
+constexpr int64_t kGemvPairMaxM = 8;
+constexpr int64_t kGemvSingleMaxM = 8;
 // LDS the column-quad GEMV may stage per workgroup.
 constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 
@@ -149,12 +149,14 @@ constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, int64_t rows_per_wave,
               int64_t k_waves, int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
     // Column pairs and singles (variant 5 with 256- and 128-column strips)
-    // carry up to 4 rows of x.
+    // carry up to 4 and 8 rows of x.
     const bool pairs = variant == 5 && (tile_n == 256 || tile_n == 128);
-    if (M > (pairs ? kGemvPairMaxM : kGemvMaxM)) return AWQ_ERR_PATH;
+    // Rows of x: 2 for the quads, 4 for pairs, 8 for singles.
+    const int64_t max_m = pairs ? (tile_n == 128 ? kGemvPairMaxM : 4) : kGemvMaxM;
+    if (M > max_m) return AWQ_ERR_PATH;
     p->path = AWQ_PATH_GEMV;
     p->variant = (int32_t)variant;
-    p->tile_m = (int32_t)(pairs ? kGemvPairMaxM : kGemvMaxM);
+    p->tile_m = (int32_t)max_m;
     p->tile_n = (int32_t)tile_n;
     p->rows_per_wave = (int32_t)rows_per_wave;
     p->k_waves = (int32_t)k_waves;
@@ -252,6 +254,10 @@ int quad_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
 //     11.03 / 12.12, before 12.28 / 12.92 / 13.75 / 14.67;
 //   3584 x 37888: the quads (M = 1) and stream kernels (M >= 2) stay ahead
 //     (unsplit singles and pairs stream too long a K range per workgroup).
+// At M = 5 .. 8 (eight rows of x, eight waves): 3584 x 4608 9.07 / 9.14 /
+// 9.34 us at M = 5 / 6 / 8 against 9.4 - 9.5 for the 32-row tile; 3584 x 3584
+// 8.83 / 8.91 / 9.12 against 9.3 - 9.45; 18944 x 3584 14.5 / 14.2 / 14.45
+// against 15.9 - 16.1 for the stream kernel with its reduce launch.
 bool auto_pairs(int64_t M, int64_t N, int64_t K) {
     // Measured on 3584 - 4608 columns (28 - 36 strips of 128); narrower
     // weights keep the plans measured for them.
@@ -267,7 +273,7 @@ int pair_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (split > C) split = C;
     if (split > kFixMaxSplit) split = kFixMaxSplit;
     if (split < 1) split = 1;
-    int64_t w = K >= 8192 ? 8 : 4;
+    int64_t w = (K >= 8192 || M > 4) ? 8 : 4;
     while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w, cw) ||
            gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w, cw) > kQuadLdsBudget) {
         if (w < 8) ++w;

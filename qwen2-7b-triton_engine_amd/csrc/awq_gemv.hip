@@ -250,6 +250,10 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     const int rq = lane >> 4;
     constexpr int SP = 16 * CW;  // packed columns of a strip
     constexpr int SC = 8 * SP;   // output columns of a strip
+    // D rows live per lane: MR <= 4, rows 0 .. MR - 1 in the lanes of k-block
+    // 0; MR = 8, rows 4 rq .. 4 rq + 3 in the lanes of k-blocks 0 and 1.
+    constexpr int NR = MR > 4 ? 4 : MR;
+    constexpr int XI = MR > 4 ? 8 : kQuadItemsPerThread;  // x prologue loads per thread
     const int pn = a.N >> 3;
     const int n_strips = (pn + SP - 1) / SP;
     // Work item w = (split, strip), strip fastest, numbered in XCD order:
@@ -290,7 +294,7 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     const int nt = blockDim.x;
     u32x4 sv[kQuadItemsPerThread];
     uint32_t zv[kQuadItemsPerThread];
-    u32x4 xv[kQuadItemsPerThread];
+    u32x4 xv[XI];
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
 #pragma unroll
     for (int i = 0; i < kQuadItemsPerThread; ++i) {
@@ -299,6 +303,9 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
         const int j = min(strip * SP + item % SP, pn - 1);
         zv[i] = buf_load_b32(rz, (uint32_t)(g * pn + j) * 4u, 0u);
         sv[i] = buf_load_u4(rs, (uint32_t)(((size_t)g * a.N + 8 * j) * 2), 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
         const int xi = (int)threadIdx.x + i * nt;  // x piece: row m, 8 rows at c0*32 + 8 * (xi % (nc * 4))
         const int m = xi / max(nc * 4, 1);
         const uint32_t xoff = (uint32_t)(((size_t)m * a.K + (size_t)c0 * 32 + 8 * (xi % max(nc * 4, 1))) * 2);
@@ -368,13 +375,17 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
                 lc[(g * (4 * CW) + col / 2) * 16 + j / CW] = v;
             }
         }
+    }
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const int item = (int)threadIdx.x + i * nt;
         if (item < MR * nc * 4) *reinterpret_cast<u32x4*>(lx + 8 * item) = xv[i];
     }
     __syncthreads();
 
-    float acc[MR][8 * CW];
+    float acc[NR][8 * CW];
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+    for (int m = 0; m < NR; ++m)
 #pragma unroll
         for (int i = 0; i < 8 * CW; ++i) acc[m][i] = 0.f;
     const uint32_t ones = 0x3C003C00u;  // fp16 (1, 1)
@@ -410,7 +421,7 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
                         xa, __builtin_bit_cast(half8_t, u32x4{kp[0][cc + e], kp[1][cc + e], kp[2][cc + e], kp[3][cc + e]}),
                         zero4);
 #pragma unroll
-                    for (int m = 0; m < MR; ++m)
+                    for (int m = 0; m < NR; ++m)
                         acc[m][col] = __builtin_fmaf(-v[2 * e + 1], S[m], __builtin_fmaf(v[2 * e], Cv[m], acc[m][col]));
                 }
             }
@@ -430,12 +441,13 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
 
     __syncthreads();  // every wave is done with the staged consts: the LDS becomes the reduction buffer
     float* red = reinterpret_cast<float*>(lds);
-    if (rq == 0) {
+    if (rq < (MR + 3) / 4) {
+        const int row0 = 4 * rq;
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
+        for (int m = 0; m < NR; ++m)
 #pragma unroll
             for (int i = 0; i < 8 * CW; i += 4)
-                *reinterpret_cast<floatx4*>(&red[(wave * MR + m) * SC + 8 * CW * c4 + i]) =
+                *reinterpret_cast<floatx4*>(&red[(wave * MR + row0 + m) * SC + 8 * CW * c4 + i]) =
                     floatx4{acc[m][i], acc[m][i + 1], acc[m][i + 2], acc[m][i + 3]};
     }
     __syncthreads();
@@ -469,7 +481,7 @@ int64_t gemv_quad_max_groups(int K, int split_k) {
 }
 
 // Rows of x a column-quad / column-pair GEMV instance carries for M rows.
-static int gemv_quad_mr(int M) { return M <= 1 ? 1 : (M <= 2 ? 2 : 4); }
+static int gemv_quad_mr(int M) { return M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8)); }
 
 // LDS of the column-quad (cw 4) or column-pair (cw 2) GEMV: staged consts
 // (1 KiB x cw per group) and x rows, or the cross-wave reduction buffer,
@@ -490,7 +502,7 @@ bool gemv_quad_fits(int M, int K, int split_k, int k_waves, int cw) {
     const int64_t threads = 64 * (int64_t)k_waves;
     const int mr = gemv_quad_mr(M);
     return gemv_quad_max_groups(K, split_k) * 16 * cw <= kQuadItemsPerThread * threads &&
-           mr * per * 4 <= kQuadItemsPerThread * threads;
+           mr * per * 4 <= (mr > 4 ? 8 : kQuadItemsPerThread) * threads;
 }
 
 int64_t gemv_strips(int N) { return ((N >> 3) + 63) / 64; }
@@ -532,6 +544,8 @@ static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, u
             case 23: return gemv_quad_launch<2, 3, 1>(a, cfg, counters, stream);
             case 42: return gemv_quad_launch<4, 2, 1>(a, cfg, counters, stream);
             case 43: return gemv_quad_launch<4, 3, 1>(a, cfg, counters, stream);
+            case 82: return gemv_quad_launch<8, 2, 1>(a, cfg, counters, stream);
+            case 83: return gemv_quad_launch<8, 3, 1>(a, cfg, counters, stream);
             default: return hipErrorInvalidValue;
         }
     }

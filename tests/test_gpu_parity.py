@@ -160,14 +160,16 @@ def test_gemm_decode_shapes(gpu, name, m):
 
 
 @pytest.mark.parametrize("m,k,n,path,variant,k_waves", [
-    (5, 3584, 4608, "tile", 9, None), (8, 3584, 3592, "tile", 9, None), (13, 2048, 4104, "tile", 9, None),
-    (16, 1152, 6144, "tile", 9, None),
+    (5, 3584, 4608, "gemv", 5, 8), (8, 18944, 3584, "gemv", 5, 8),
+    (8, 3584, 3592, "tile", 9, None), (13, 2048, 4104, "tile", 9, None), (16, 1152, 6144, "tile", 9, None),
     (9, 3584, 8224, "stream", 3, 3), (13, 8192, 1056, "stream", 3, 3), (12, 2048, 16384, "stream", 3, 2)])
 def test_auto_small_m_routes(gpu, m, k, n, path, variant, k_waves):
-    """The AUTO routes for 5 <= M <= 16: the 32-row tile split along K on
-    narrow shallow weights (N not a multiple of 256, splits that do not
-    divide K evenly), and the half-strip stream kernel with two or three
-    wave pairs on wide or deep ones; each against the oracle."""
+    """The AUTO routes for 5 <= M <= 16: the column-single GEMV (eight rows of
+    x, eight waves) up to M = 8 on narrow weights of 3584 - 4608 columns;
+    the 32-row tile split along K on other narrow shallow weights (N not a
+    multiple of 256, splits that do not divide K evenly) and above M = 8; the
+    half-strip stream kernel with two or three wave pairs on wide or deep
+    ones; each against the oracle."""
     p = _native.plan_for(m, n, k)
     assert _native.PATH_NAMES[p.path] == path and p.variant == variant
     if k_waves is not None:
@@ -388,13 +390,14 @@ def test_gemv_quad_plans_agree(gpu, m):
     assert tried >= 80
 
 
-@pytest.mark.parametrize("tile_n", [256, 128])
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("tile_n,m", [(256, 1), (256, 2), (256, 3), (256, 4), (128, 1), (128, 2), (128, 3), (128, 4),
+                                      (128, 5), (128, 7), (128, 8)])
 def test_gemv_pair_plans_agree(gpu, m, tile_n):
     """Column-pair and column-single GEMV (256- and 128-column strips, up to 4
-    rows of x, fixed-point split-K finish): split counts from 1 up to one
-    32-row chunk per workgroup, wave counts 1 - 8, ring depths 2 and 3, on an
-    N whose last strip is partly filled (1056 = 4 x 256 + 32 = 8 x 128 + 32)."""
+    and 8 rows of x -- above 4, lanes of two k-blocks hold the rows --,
+    fixed-point split-K finish): split counts from 1 up to one 32-row chunk
+    per workgroup, wave counts 1 - 8, ring depths 2 and 3, on an N whose last
+    strip is partly filled (1056 = 4 x 256 + 32 = 8 x 128 + 32)."""
     k, n = 3584, 1056
     x, qw, qz, s = O.make_inputs(m, k, n, seed=25 + m)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)

@@ -85,9 +85,9 @@ def test_auto_plan_invariants(L, m, k, n):
     # split where that grid covers every CU and fits two workgroups per CU
     deep_split = -(-(k // 128) // 5)
     deep_tile = 9 <= m <= 16 and k >= 8192 and strips < 16 and 256 <= -(-n // 256) * deep_split <= 512
-    # column singles (128-column strips) on narrow weights at M <= 4
+    # column singles (128-column strips) on narrow weights at M <= 8
     strips256 = -(-(n // 8) // 32)
-    pairs = n % 32 == 0 and strips < 16 and strips256 >= 8 and m <= 4
+    pairs = n % 32 == 0 and strips < 16 and strips256 >= 8 and m <= 8
     if pairs:
         assert p.path == _native.PATH_GEMV and p.variant == 5 and p.tile_m >= m and p.tile_n == 128
         assert 0.5 * 256 < p.grid <= 256
