@@ -150,12 +150,16 @@ int awq_w4a16_plan_tile(int64_t M, int64_t N, int64_t K, int32_t group_size,
 /* Host-only: a GEMV-path plan with explicit tuning values.
  * variant 5 (N % 32 == 0, column sums on v_mfma_f32_16x16x32_f16): tile_n
  * is the strip width -- 512 (column quads, M <= 2, depth 2 .. 4), 256
- * (column pairs) or 128 (column singles; both M <= 4, depth 2 .. 3);
+ * (column pairs, M <= 4) or 128 (column singles, M <= 8; pairs and singles
+ * depth 2 .. 3);
  * rows_per_wave 0; depth = chunk buffers per wavefront (depth - 1 chunks of
  * loads in flight while one is computed); k_waves 1 .. 8 wavefronts, which
  * take every k_waves-th 32-row chunk of the workgroup's share of K; split_k
  * 1 .. min(K/32, 255) workgroups share each strip's K evenly; split-K
  * partials meet in 64-bit fixed-point workspace slots.
+ * variant 6: column singles (tile_n 128) with 16 rows of x, 9 <= M <= 16,
+ * depth 2, k_waves and split_k as variant 5; split-K partials are fp32
+ * ([split_k, M, N] in the workspace) added by a second launch.
  * variant 2 (K-streaming, one 128-row group per step): tile_n 512;
  * rows_per_wave 16 or 32, k_waves = 128 / rows_per_wave, split_k in
  * 1 .. K/128 with every split a whole number of groups, depth = chunks in

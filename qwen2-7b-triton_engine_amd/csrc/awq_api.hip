@@ -149,10 +149,13 @@ constexpr uint64_t kQuadLdsBudget = 96 * 1024;
 int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, int64_t rows_per_wave,
               int64_t k_waves, int64_t split_k, int64_t depth, awq_w4a16_plan* p) {
     // Column pairs and singles (variant 5 with 256- and 128-column strips)
-    // carry up to 4 and 8 rows of x.
-    const bool pairs = variant == 5 && (tile_n == 256 || tile_n == 128);
-    // Rows of x: 2 for the quads, 4 for pairs, 8 for singles.
-    const int64_t max_m = pairs ? (tile_n == 128 ? kGemvPairMaxM : 4) : kGemvMaxM;
+    // carry up to 4 and 8 rows of x; variant 6 (singles with fp32 partials
+    // and the reduce launch) 9 .. 16.
+    const bool red = variant == 6;
+    const bool pairs = (variant == 5 || red) && (tile_n == 256 || tile_n == 128);
+    // Rows of x: 2 for the quads, 4 for pairs, 8 for singles, 16 for variant 6.
+    const int64_t max_m = red ? 16 : (pairs ? (tile_n == 128 ? kGemvPairMaxM : 4) : kGemvMaxM);
+    if (red && (tile_n != 128 || M < 9)) return AWQ_ERR_PATH;
     if (M > max_m) return AWQ_ERR_PATH;
     p->path = AWQ_PATH_GEMV;
     p->variant = (int32_t)variant;
@@ -164,7 +167,7 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
     p->factored_scale = 1;
     p->depth = 0;
     if (tile_n != 512 && !pairs) return AWQ_ERR_PATH;
-    if (variant == 5) {
+    if (variant == 5 || variant == 6) {
         // Column quads (512-column strips, M <= 2) or column pairs (256-column
         // strips, M <= 4) with MFMA column sums: N % 32 == 0; rows_per_wave 0;
         // depth 2 .. 4 chunk buffers per wave (2 .. 3 for pairs; each strip's
@@ -180,8 +183,13 @@ int fill_gemv(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t tile_n, 
         p->split_k = (int32_t)split_k;
         p->depth = (int32_t)depth;
         p->grid = gemv_strips_cw((int)N, cw) * split_k;
-        if (split_k > 1 && (uint64_t)M * (uint64_t)N * 8u > kSlotBytes) return AWQ_ERR_PATH;
-        p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
+        if (red) {
+            if (depth != 2) return AWQ_ERR_PATH;
+            p->workspace_bytes = split_k > 1 ? partials_workspace(split_k, M, N) : 0u;
+        } else {
+            if (split_k > 1 && (uint64_t)M * (uint64_t)N * 8u > kSlotBytes) return AWQ_ERR_PATH;
+            p->workspace_bytes = split_k > 1 ? kCounterBytes + (uint64_t)M * (uint64_t)N * 8u : 0u;
+        }
         p->lds_bytes = gemv_quad_lds_bytes((int)M, (int)K, (int)split_k, (int)k_waves, cw);
         if (p->lds_bytes > kQuadLdsBudget) return AWQ_ERR_PATH;
         if (p->workspace_bytes > (uint64_t)kBytesLimit) return AWQ_ERR_TOO_LARGE;
@@ -487,6 +495,22 @@ constexpr TileModel kTileModels[] = {
 // against 16.6 - 16.8).  Other splits of the same tile measured slower at
 // every M (17 splits 18.3 - 18.9, 25 splits 18.4 - 19.1, 37 splits 18.6 -
 // 20.0).
+// 9 <= M <= 16 on deep, narrow weights (K >= 8192; 2048 <= N < 8192, as
+// auto_pairs): column singles with all 16 rows of x (GEMV variant 6, fp32
+// partials added by the reduce launch), eight waves, one split fewer than
+// fills the CUs.  down_proj (18944 x 3584) at M = 9 / 12 / 16 measured 16.6
+// / 16.9 / 17.2 us against 17.2 / 17.7 / 18.2 for the 32-row tile below;
+// 8 splits (224 workgroups) 0.3 - 0.5 us faster than 9 (252) at M = 12 - 16,
+// as the partials the reduce launch reads shrink with the split.
+int deep_small_m_gemv_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    if (M < 9 || M > 16 || K < 8192 || N % 32 != 0 || !auto_pairs(1, N, K)) return AWQ_ERR_PATH;
+    const int64_t split = cus() / gemv_strips_cw((int)N, 1) - 1;
+    awq_w4a16_plan q;
+    if (split < 2 || fill_gemv(M, N, K, 6, 128, 0, 8, split, 2, &q) != AWQ_OK) return AWQ_ERR_PATH;
+    *p = q;
+    return AWQ_OK;
+}
+
 int deep_small_m_tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     if (M < 9 || M > 16 || K < 8192 || gemv_strips((int)N) >= 16) return AWQ_ERR_PATH;
     const int64_t groups = K / kGroup;
@@ -895,6 +919,7 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
         case AWQ_PATH_AUTO:
             if (auto_pairs(M, N, K) && pair_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (M == 1 || (M <= kGemvMaxM && N % 32 != 0)) return gemv_plan(M, N, K, plan);
+            if (deep_small_m_gemv_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (deep_small_m_tile_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (auto_stream(M, N, K) && stream_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (small_m_tile_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;

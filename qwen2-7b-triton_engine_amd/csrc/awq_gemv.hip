@@ -240,7 +240,7 @@ __global__ __launch_bounds__(512) void awq_gemv_stream_kernel(GemmArgs a, int ch
 // through the fixed-point finish.  Needs N % 32 == 0 (whole quads).
 constexpr int kQuadItemsPerThread = 4;  // prologue loads per thread (consts and x each)
 
-template <int MR, int D, bool NT, int CW>
+template <int MR, int D, bool NT, int CW, bool RED = false>
 __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int split_k, unsigned long long* fix) {
     extern __shared__ __align__(16) uint32_t lds[];
     const int lane = threadIdx.x & 63;
@@ -251,9 +251,10 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     constexpr int SP = 16 * CW;  // packed columns of a strip
     constexpr int SC = 8 * SP;   // output columns of a strip
     // D rows live per lane: MR <= 4, rows 0 .. MR - 1 in the lanes of k-block
-    // 0; MR = 8, rows 4 rq .. 4 rq + 3 in the lanes of k-blocks 0 and 1.
+    // 0; MR = 8 / 16, rows 4 rq .. 4 rq + 3 in the lanes of k-blocks 0 .. 1 / 0 .. 3.
     constexpr int NR = MR > 4 ? 4 : MR;
-    constexpr int XI = MR > 4 ? 8 : kQuadItemsPerThread;  // x prologue loads per thread
+    constexpr int XI = MR > 8 ? 16 : (MR > 4 ? 8 : kQuadItemsPerThread);  // x prologue loads per thread
+    static_assert(MR <= 8 || RED, "16 rows of x take the reduce-launch finish");
     const int pn = a.N >> 3;
     const int n_strips = (pn + SP - 1) / SP;
     // Work item w = (split, strip), strip fastest, numbered in XCD order:
@@ -451,26 +452,48 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
                     floatx4{acc[m][i], acc[m][i + 1], acc[m][i + 2], acc[m][i + 3]};
     }
     __syncthreads();
+    if constexpr (RED) {
+        if (split_k > 1) {
+            // fp32 partials [split_k, M, N] (write-through), added by a second
+            // launch of awq_splitk_reduce_kernel.
+            const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, (uint32_t)((size_t)split_k * a.M * a.N * 4));
+            for (int idx = threadIdx.x; idx < MR * SC; idx += nt) {
+                const int m = idx / SC, t = idx - m * SC, n = strip * SC + t;
+                if (m >= a.M || n >= a.N) continue;
+                float v = 0.f;
+                for (int w = 0; w < nw; ++w) v += red[(w * MR + m) * SC + t];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rp,
+                                                      (uint32_t)((((size_t)split * a.M + m) * a.N + n) * 4), 0,
+                                                      kCpolSC1);
+            }
+            return;
+        }
+    }
     // Thread t finishes outputs t, t + nt, ... of the strip (at most SC / 64
     // per row of x) in one batch: one memory round trip per thread.
     constexpr int kOwn = SC / 64;
-    float fs[kOwn * MR];
-    int fm[kOwn * MR], fn[kOwn * MR];
-    bool fok[kOwn * MR];
+    constexpr int FB = MR > 8 ? 8 : MR;  // rows per finish batch (16 rows: two, at split_k 1 only)
 #pragma unroll
-    for (int i = 0; i < kOwn; ++i)
+    for (int mb = 0; mb < MR; mb += FB) {
+        float fs[kOwn * FB];
+        int fm[kOwn * FB], fn[kOwn * FB];
+        bool fok[kOwn * FB];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const int t = threadIdx.x + i * nt;
-            float s = 0.f;
-            if (t < SC)
-                for (int w = 0; w < nw; ++w) s += red[(w * MR + m) * SC + t];
-            fs[i * MR + m] = s;
-            fm[i * MR + m] = m;
-            fn[i * MR + m] = strip * SC + t;
-            fok[i * MR + m] = t < SC && strip * SC + t < a.N && m < a.M;
-        }
-    finish_batch<kOwn * MR>(fix, a.out, a.bias, a.residual, a.M, a.N, split_k, fs, fm, fn, fok);
+        for (int i = 0; i < kOwn; ++i)
+#pragma unroll
+            for (int mm = 0; mm < FB; ++mm) {
+                const int m = mb + mm;
+                const int t = threadIdx.x + i * nt;
+                float s = 0.f;
+                if (t < SC)
+                    for (int w = 0; w < nw; ++w) s += red[(w * MR + m) * SC + t];
+                fs[i * FB + mm] = s;
+                fm[i * FB + mm] = m;
+                fn[i * FB + mm] = strip * SC + t;
+                fok[i * FB + mm] = t < SC && strip * SC + t < a.N && m < a.M;
+            }
+        finish_batch<kOwn * FB>(fix, a.out, a.bias, a.residual, a.M, a.N, split_k, fs, fm, fn, fok);
+    }
 }
 
 // Groups a workgroup's chunk range can touch: at most ceil(per / 4) + 1.
@@ -481,7 +504,7 @@ int64_t gemv_quad_max_groups(int K, int split_k) {
 }
 
 // Rows of x a column-quad / column-pair GEMV instance carries for M rows.
-static int gemv_quad_mr(int M) { return M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8)); }
+static int gemv_quad_mr(int M) { return M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : (M <= 8 ? 8 : 16))); }
 
 // LDS of the column-quad (cw 4) or column-pair (cw 2) GEMV: staged consts
 // (1 KiB x cw per group) and x rows, or the cross-wave reduction buffer,
@@ -502,7 +525,7 @@ bool gemv_quad_fits(int M, int K, int split_k, int k_waves, int cw) {
     const int64_t threads = 64 * (int64_t)k_waves;
     const int mr = gemv_quad_mr(M);
     return gemv_quad_max_groups(K, split_k) * 16 * cw <= kQuadItemsPerThread * threads &&
-           mr * per * 4 <= (mr > 4 ? 8 : kQuadItemsPerThread) * threads;
+           mr * per * 4 <= (mr > 8 ? 16 : (mr > 4 ? 8 : kQuadItemsPerThread)) * threads;
 }
 
 int64_t gemv_strips(int N) { return ((N >> 3) + 63) / 64; }
@@ -517,7 +540,7 @@ static hipError_t gemv_stream_launch(const GemmArgs& a, const GemvConfig& cfg, u
     return hipGetLastError();
 }
 
-template <int MR, int D, int CW>
+template <int MR, int D, int CW, bool RED = false>
 static hipError_t gemv_quad_launch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
                                    hipStream_t stream) {
     unsigned long long* fix = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(counters) + kCounterBytes);
@@ -528,10 +551,12 @@ static hipError_t gemv_quad_launch(const GemmArgs& a, const GemvConfig& cfg, uin
     // faster with them at M = 1 - 16, the 100 - 500-row ranges of 18 - 36
     // splits up to 3 % slower.
     if (cfg.split_k <= kNonTemporalMaxSplit)
-        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, true, CW>), grid, block, lds, stream, a, cfg.split_k, fix);
+        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, true, CW, RED>), grid, block, lds, stream, a, cfg.split_k, fix);
     else
-        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, false, CW>), grid, block, lds, stream, a, cfg.split_k, fix);
-    return hipGetLastError();
+        hipLaunchKernelGGL((awq_gemv_quad_kernel<MR, D, false, CW, RED>), grid, block, lds, stream, a, cfg.split_k, fix);
+    const hipError_t e = hipGetLastError();
+    if (!RED || e != hipSuccess || cfg.split_k <= 1) return e;
+    return splitk_reduce_launch(a, cfg.split_k, stream);
 }
 
 static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters,
@@ -574,6 +599,11 @@ static hipError_t gemv_quad_dispatch(const GemmArgs& a, const GemvConfig& cfg, u
 
 hipError_t launch_gemv(const GemmArgs& a, const GemvConfig& cfg, uint32_t* counters, hipStream_t stream) {
     if (cfg.variant == 5) return gemv_quad_dispatch(a, cfg, counters, stream);
+    if (cfg.variant == 6) {
+        // Column singles with 16 rows of x, fp32 partials and the reduce launch.
+        if (cfg.cw != 1 || gemv_quad_mr(a.M) != 16 || cfg.depth != 2) return hipErrorInvalidValue;
+        return gemv_quad_launch<16, 2, 1, true>(a, cfg, counters, stream);
+    }
     if (cfg.variant == 2) {
         const int key2 = (a.M <= 1 ? 1 : 2) * 10000 + cfg.rows_per_wave * 10 + cfg.depth;
         switch (key2) {

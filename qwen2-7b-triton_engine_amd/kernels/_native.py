@@ -179,9 +179,10 @@ def plan_skinny(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, varian
 def plan_gemv(M: int, N: int, K: int, rows_per_wave: int, k_waves: int, variant: int = 5, split_k: int = 1,
               depth: int = 2, tile_n: int = 512, group_size: int = 128) -> Plan:
     """GEMV-path plan.  Variant 5 (MFMA column sums, fixed-point split-K):
-    ``tile_n`` is the strip width -- 512 (column quads, M <= 2), 256 (pairs)
-    or 128 (singles; both M <= 4); variant 2 (K-streaming): ``tile_n`` 512,
-    ``rows_per_wave`` 16 or 32."""
+    ``tile_n`` is the strip width -- 512 (column quads, M <= 2), 256 (pairs,
+    M <= 4) or 128 (singles, M <= 8); variant 6 (singles with 16 rows of x,
+    9 <= M <= 16, fp32 partials and a reduce launch): ``tile_n`` 128, depth 2;
+    variant 2 (K-streaming): ``tile_n`` 512, ``rows_per_wave`` 16 or 32."""
     p = Plan()
     check(lib().awq_w4a16_plan_gemv(M, N, K, group_size, variant, tile_n, rows_per_wave, k_waves, split_k, depth,
                                     ctypes.byref(p)), "awq_w4a16_plan_gemv")

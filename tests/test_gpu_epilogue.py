@@ -32,6 +32,10 @@ def _plans(m, n, k):
                    for v in (5,) for sp in (1, 3, 16)]
     if m <= 16:
         makers += [(f"stream v{v} s4", lambda v=v: _native.plan_stream(m, n, k, 2, 4, variant=v)) for v in (1, 2, 3)]
+    if 9 <= m <= 16:
+        makers += [(f"gemv singles reduce s{sp}",
+                    lambda sp=sp: _native.plan_gemv(m, n, k, 0, 8, variant=6, split_k=sp, tile_n=128))
+                   for sp in (4, 9)]
     if m > 16:
         makers += [(f"tile v{v} s{sp}", lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp))
                    for v, sp in ((6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (13, 2), (14, 3))]

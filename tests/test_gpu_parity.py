@@ -160,15 +160,18 @@ def test_gemm_decode_shapes(gpu, name, m):
 
 
 @pytest.mark.parametrize("m,k,n,path,variant,k_waves", [
-    (5, 3584, 4608, "gemv", 5, 8), (8, 18944, 3584, "gemv", 5, 8),
+    (5, 3584, 4608, "gemv", 5, 8), (8, 18944, 3584, "gemv", 5, 8), (9, 18944, 3584, "gemv", 6, 8),
+    (16, 8192, 2080, "gemv", 6, 8),
     (8, 3584, 3592, "tile", 9, None), (13, 2048, 4104, "tile", 9, None), (16, 1152, 6144, "tile", 9, None),
     (9, 3584, 8224, "stream", 3, 3), (13, 8192, 1056, "stream", 3, 3), (12, 2048, 16384, "stream", 3, 2)])
 def test_auto_small_m_routes(gpu, m, k, n, path, variant, k_waves):
     """The AUTO routes for 5 <= M <= 16: the column-single GEMV (eight rows of
     x, eight waves) up to M = 8 on narrow weights of 3584 - 4608 columns;
     the 32-row tile split along K on other narrow shallow weights (N not a
-    multiple of 256, splits that do not divide K evenly) and above M = 8; the
-    half-strip stream kernel with two or three wave pairs on wide or deep
+    multiple of 256, splits that do not divide K evenly) and above M = 8; on
+    deep narrow ones at M = 9 - 16 column singles with 16 rows of x and the
+    reduce launch (last strip partly filled at N = 2080); the half-strip
+    stream kernel with two or three wave pairs on wide or deep
     ones; each against the oracle."""
     p = _native.plan_for(m, n, k)
     assert _native.PATH_NAMES[p.path] == path and p.variant == variant
@@ -201,15 +204,17 @@ def test_auto_vocab_wide(gpu, m):
 def test_decode_plans_sized_by_the_device(gpu):
     """The planner sizes its grids by the current device's compute units (read
     once per device): the GEMV and stream plans of the Qwen2-7B shapes put at
-    most one workgroup on each CU and keep more than half of them busy; the
-    32-row tile on down_proj at M = 16 covers every CU with at most two."""
+    most one workgroup on each CU and keep more than half of them busy; on
+    down_proj at M = 16 the column singles with 16 rows of x take one split
+    fewer than fills the CUs."""
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     print(f"device compute units: {cus}", flush=True)
-    for m, k, n in [(1, 3584, 4608), (1, 3584, 37888), (4, 3584, 4608), (4, 18944, 3584), (8, 18944, 3584)]:
+    for m, k, n in [(1, 3584, 4608), (1, 3584, 37888), (4, 3584, 4608), (4, 18944, 3584), (8, 18944, 3584),
+                    (16, 18944, 3584)]:
         p = _native.plan_for(m, n, k)
         assert cus // 2 < p.grid <= cus, (m, k, n, p.grid, cus)
     p = _native.plan_for(16, 3584, 18944)
-    assert p.path == _native.PATH_TILE and cus <= p.grid <= 2 * cus, (p.path, p.grid, cus)
+    assert p.path == _native.PATH_GEMV and p.variant == 6 and p.split_k == cus // 28 - 1, (p.path, p.split_k, cus)
 
 
 @pytest.mark.parametrize("m", [1, 8, 64, 512, 2048])
@@ -414,6 +419,30 @@ def test_gemv_pair_plans_agree(gpu, m, tile_n):
                 _assert_close(y, y_ref, f"gemv {tile_n} M={m} split={split} kw={kw} d={depth}")
                 tried += 1
     assert tried >= 40
+
+
+@pytest.mark.parametrize("m", [9, 12, 16])
+def test_gemv_singles_reduce_plans_agree(gpu, m):
+    """Column singles with fp32 partials added by a second reduce launch
+    (GEMV variant 6, 128-column strips, 9 - 16 rows of x in the lanes of all
+    four k-blocks): split counts from 1 (direct finish, two row batches) up to
+    one 32-row chunk per workgroup, wave counts 1 - 8, on an N whose last
+    strip is partly filled."""
+    k, n = 2048, 1056
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=41 + m)
+    y_ref = O.awq_gemm_oracle(x, qw, qz, s)
+    tried = 0
+    for split in (1, 2, 3, 9, 37, 64):
+        for kw in (1, 2, 4, 8):
+            try:
+                p = _native.plan_gemv(m, n, k, 0, kw, variant=6, split_k=split, depth=2, tile_n=128)
+            except _native.AwqNativeError:
+                continue
+            print(f"gemv singles + reduce M={m} split={split} k_waves={kw}", flush=True)
+            y = _run(gpu, x, qw, qz, s, plan_obj=p)
+            _assert_close(y, y_ref, f"gemv singles reduce M={m} split={split} kw={kw}")
+            tried += 1
+    assert tried >= 12
 
 
 @pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 9, 16])

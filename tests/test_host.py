@@ -81,18 +81,26 @@ def test_auto_plan_invariants(L, m, k, n):
     p = _native.plan_for(m, n, k)
     strips = -(-(n // 8) // 64)            # 512-column strips of the stream path
     stream = n % 32 == 0 and m <= 16 and (m <= 4 or strips >= 16 or k >= 8192)
-    # 9 <= M <= 16 on deep, narrow weights: the 32-row tile with five groups per
-    # split where that grid covers every CU and fits two workgroups per CU
+    # 9 <= M <= 16 on deep, narrow weights: column singles with 16 rows of x
+    # and the reduce launch, one split fewer than fills the CUs (256 without
+    # a GPU); else the 32-row tile with five groups per split where that grid
+    # covers every CU and fits two workgroups per CU
+    strips128 = -(-(n // 8) // 16)
+    strips256 = -(-(n // 8) // 32)
+    deep_gemv = (9 <= m <= 16 and k >= 8192 and n % 32 == 0 and strips < 16 and strips256 >= 8
+                 and 256 // strips128 - 1 >= 2)
     deep_split = -(-(k // 128) // 5)
     deep_tile = 9 <= m <= 16 and k >= 8192 and strips < 16 and 256 <= -(-n // 256) * deep_split <= 512
     # column singles (128-column strips) on narrow weights at M <= 8
-    strips256 = -(-(n // 8) // 32)
     pairs = n % 32 == 0 and strips < 16 and strips256 >= 8 and m <= 8
     if pairs:
         assert p.path == _native.PATH_GEMV and p.variant == 5 and p.tile_m >= m and p.tile_n == 128
         assert 0.5 * 256 < p.grid <= 256
     elif m == 1 or (m == 2 and n % 32 != 0):
         assert p.path == _native.PATH_GEMV
+    elif deep_gemv:
+        assert p.path == _native.PATH_GEMV and p.variant == 6 and p.tile_n == 128 and p.k_waves == 8
+        assert p.split_k == 256 // strips128 - 1 and p.grid == strips128 * p.split_k <= 256
     elif deep_tile:
         assert p.path == _native.PATH_TILE and p.variant == 9 and p.split_k == deep_split
     elif stream:

@@ -51,7 +51,7 @@ def _noalloc(x, qw, qz, s):
 CASES = [
     ("qkv_proj", 3584, 4608, 16, 1),        # 32-row tile split 14 + reduce launch; GEMV fixed-point slots
     ("gate_up_proj", 3584, 37888, 4, 2),    # stream fixed-point slots, at M = 4 and 2
-    ("down_proj", 18944, 3584, 16, 8),      # 32-row tile split 30 + reduce launch; column-single GEMV at M = 8
+    ("down_proj", 18944, 3584, 16, 8),      # 16-row column singles split 8 + reduce launch; 8-row ones at M = 8
     ("o_proj", 3584, 3584, 300, 5),         # tile split-K (reduce launch); column-single GEMV at M = 5
     ("down_proj", 18944, 3584, 2048, 512),  # tile plan lowered to fit the scratch; tile split 4 (28 MB)
     ("qkv_proj", 3584, 4608, 2048, 1025),   # hybrid tiles (compact partials, last arrivers)
