@@ -116,7 +116,7 @@ def operands(m, k, n):
             torch.randint(-2**31, 2**31 - 1, (k, n // 8), generator=g, device=dev, dtype=torch.int32),
             torch.randint(-2**31, 2**31 - 1, (k // 128, n // 8), generator=g, device=dev, dtype=torch.int32),
             (torch.rand((k // 128, n), generator=g, device=dev) * 0.018 + 0.002).half())
-small, big = (16, 3584, 4608), (16, 18944, 3584)
+small, big = (16, 3584, 4608), (16, 3584, 37888)
 ws_small = _native.plan_for(small[0], small[2], small[1]).workspace_bytes
 ws_big = _native.plan_for(big[0], big[2], big[1]).workspace_bytes
 print("workspace bytes: small", ws_small, "big", ws_big, flush=True)
