@@ -291,6 +291,61 @@ int pair_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     return fill_gemv(M, N, K, 5, 128 * cw, 0, w, split, 2, p);
 }
 
+// Two more width classes for the column pairs and singles, from sweeps of
+// every strip width, split, wave count and depth against the previous AUTO
+// (graphs over >= 400 MB of weights; us):
+//  * slim weights (256 <= N < 2048: 1 - 7 strips of 256 columns; 2048 <= K <
+//    8192):
+//    singles with two waves, four 32-row chunks per workgroup, at M <= 8 --
+//    3584 x 512 at M = 1 / 2 / 4 / 8: 4.56 / 5.04 / 5.79 / 7.41 against 8.14 /
+//    7.63 / 8.67 / 10.36 for the quads split 112 ways (112 fixed-point atomics
+//    on each output) and the stream and skinny kernels on 18 and 14
+//    workgroups; at M = 9 .. 16 the 16-row singles (variant 6, eight waves)
+//    with one workgroup per CU: 9.51 against 12.84 at M = 16.
+//  * wide, shallow weights (>= 16 strips of 512 columns, K < 8192) whose
+//    256-column strips leave at least three splits per CU: pairs at M <= 2,
+//    singles at M = 3 .. 8, split CUs / strips of 256 -- 3584 x 18944 at M = 1
+//    / 2 / 4 / 8: 10.61 / 11.89 / 13.64 / 16.02 against 12.30 / 13.09 / 14.46 /
+//    16.88 for the quads and the stream kernel.  3584 x 37888 (1.7 splits per
+//    CU) keeps those: its best pair plans were 3 % faster at M <= 2 and 6 - 42 %
+//    slower at M = 4 - 8.
+constexpr int64_t kSlimMinN = 256;
+constexpr int64_t kSlimMinK = 2048;
+
+int strip_fit(int64_t M, int64_t N, int64_t K, int variant, int cw, int64_t split, int64_t w,
+              awq_w4a16_plan* p) {
+    const int64_t C = K / 32;
+    if (split > C) split = C;
+    if (split > kFixMaxSplit) split = kFixMaxSplit;
+    if (split < 1) split = 1;
+    while (!gemv_quad_fits((int)M, (int)K, (int)split, (int)w, cw) ||
+           gemv_quad_lds_bytes((int)M, (int)K, (int)split, (int)w, cw) > kQuadLdsBudget) {
+        if (w < 8) ++w;
+        else if (split < C && split < kFixMaxSplit) ++split;
+        else return AWQ_ERR_PATH;
+    }
+    awq_w4a16_plan q;
+    if (fill_gemv(M, N, K, variant, 128 * cw, 0, w, split, 2, &q) != AWQ_OK) return AWQ_ERR_PATH;
+    *p = q;
+    return AWQ_OK;
+}
+
+int strip_class_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
+    if (N % 32 != 0 || M > 16) return AWQ_ERR_PATH;
+    const int64_t s128 = gemv_strips_cw((int)N, 1), s256 = gemv_strips_cw((int)N, 2);
+    if (N >= kSlimMinN && s256 < 8 && K >= kSlimMinK && K < 8192) {
+        const int64_t four_chunks = (K / 32) / 4, fill = cus() / s128;
+        if (M <= kGemvSingleMaxM) return strip_fit(M, N, K, 5, 1, four_chunks < fill ? four_chunks : fill, 2, p);
+        if (M >= 9) return strip_fit(M, N, K, 6, 1, fill, 8, p);
+        return AWQ_ERR_PATH;
+    }
+    if (gemv_strips((int)N) >= 16 && K < 8192 && cus() / s256 >= 3 && M <= kGemvSingleMaxM) {
+        if (M <= 2) return strip_fit(M, N, K, 5, 2, cus() / s256, M == 1 ? 4 : 8, p);
+        return strip_fit(M, N, K, 5, 1, cus() / s256, 4, p);
+    }
+    return AWQ_ERR_PATH;
+}
+
 // Column quads while their fixed-point slots (M x N x 8 bytes) fit the slot
 // region; else (and for N % 32 != 0) the K-streaming variant 2, whose fp32
 // partials have no such limit.
@@ -918,6 +973,7 @@ int awq_w4a16_plan_for(int64_t M, int64_t N, int64_t K, int32_t group_size, int3
     switch (path) {
         case AWQ_PATH_AUTO:
             if (auto_pairs(M, N, K) && pair_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
+            if (strip_class_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (M == 1 || (M <= kGemvMaxM && N % 32 != 0)) return gemv_plan(M, N, K, plan);
             if (deep_small_m_gemv_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;
             if (deep_small_m_tile_plan(M, N, K, plan) == AWQ_OK) return AWQ_OK;

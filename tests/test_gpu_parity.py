@@ -183,6 +183,30 @@ def test_auto_small_m_routes(gpu, m, k, n, path, variant, k_waves):
     _assert_close(_run(gpu, x, qw, qz, s), y_ref, f"auto M={m} K={k} N={n}")
 
 
+@pytest.mark.parametrize("m,k,n,tile_n,variant", [
+    (1, 3584, 512, 128, 5), (3, 3584, 512, 128, 5), (8, 3584, 512, 128, 5), (12, 3584, 512, 128, 6),
+    (16, 3584, 512, 128, 6), (2, 2048, 1056, 128, 5), (9, 2048, 1056, 128, 6),
+    (1, 3584, 18944, 256, 5), (2, 3584, 18944, 256, 5), (3, 3584, 18944, 128, 5), (8, 3584, 18944, 128, 5),
+    (1, 3584, 8224, 256, 5), (5, 3584, 8224, 128, 5)])
+def test_auto_strip_class_routes(gpu, m, k, n, tile_n, variant):
+    """AUTO's column-strip GEMV on slim weights (1 - 7 strips of 256 columns:
+    k_proj / v_proj 3584 x 512, and 2048 x 1056 whose last strip is partly
+    filled) -- column singles, the 16-row singles above M = 8 -- and on wide
+    shallow ones (gate_proj / up_proj 3584 x 18944; 3584 x 8224) -- column
+    pairs at M <= 2, singles above; each against the oracle on three
+    512-column slices (first, middle, last)."""
+    p = _native.plan_for(m, n, k)
+    print(f"strip-class route M={m} K={k} N={n}: {_native.PATH_NAMES[p.path]} v{p.variant} "
+          f"tile_n={p.tile_n} split={p.split_k} k_waves={p.k_waves}", flush=True)
+    assert p.path == _native.PATH_GEMV and p.variant == variant and p.tile_n == tile_n
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=70 + m)
+    y = _run(gpu, x, qw, qz, s)
+    for c0 in sorted({0, n // 2 - 256, n - 512}):
+        w = O.dequant_awq_f32eval(qw[:, c0 // 8:(c0 + 512) // 8], qz[:, c0 // 8:(c0 + 512) // 8],
+                                  s[:, c0:c0 + 512]).astype(np.float64)
+        _assert_close(y[:, c0:c0 + 512], x.astype(np.float64) @ w, f"strip class M={m} N={n} columns {c0}..")
+
+
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_auto_vocab_wide(gpu, m):
     """AUTO on a vocab-wide weight (3584 x 152064, the Qwen2-7B LM head's
@@ -523,6 +547,7 @@ def test_split_k_workspace_left_zero(gpu):
               for m, v, sp, kw, d in ((3, 1, 28, 8, 1), (5, 2, 6, 8, 2), (8, 3, 28, 8, 1))]
     cases += [(m, _native.plan_stream(m, n, k, 3, 14, variant=3)) for m in (9, 16)]
     cases += [(m, _native.plan_gemv(m, n, k, 16, 8, variant=2, split_k=sp, depth=3)) for m, sp in ((1, 7), (2, 14))]
+    cases += [(m, _native.plan_gemv(m, n, k, 0, 8, variant=6, split_k=sp, tile_n=128)) for m, sp in ((9, 6), (16, 9))]
     cases += [(m, _native.plan_tile(m, n, k, v, sp)) for m, v, sp in
               ((100, 6, 4), (200, 7, 3), (100, 8, 4), (70, 9, 7), (2048, 13, 2), (2048, 14, 3))]
     ws = G._workspace(gpu, max(int(p.workspace_bytes) for _, p in cases))

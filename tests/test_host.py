@@ -93,9 +93,24 @@ def test_auto_plan_invariants(L, m, k, n):
     deep_tile = 9 <= m <= 16 and k >= 8192 and strips < 16 and 256 <= -(-n // 256) * deep_split <= 512
     # column singles (128-column strips) on narrow weights at M <= 8
     pairs = n % 32 == 0 and strips < 16 and strips256 >= 8 and m <= 8
+    # slim weights (1 - 7 strips of 256, 2048 <= K < 8192): singles with two
+    # waves and four chunks per workgroup at M <= 8, the 16-row singles with
+    # one workgroup per CU above; wide shallow ones with >= 3 splits of the
+    # 256-column strips per CU: pairs at M <= 2, singles to M = 8
+    slim = n % 32 == 0 and n >= 256 and strips256 < 8 and 2048 <= k < 8192 and m <= 16
+    wide = n % 32 == 0 and strips >= 16 and k < 8192 and 256 // strips256 >= 3 and m <= 8
     if pairs:
         assert p.path == _native.PATH_GEMV and p.variant == 5 and p.tile_m >= m and p.tile_n == 128
         assert 0.5 * 256 < p.grid <= 256
+    elif slim:
+        assert p.path == _native.PATH_GEMV and p.tile_n == 128
+        if m <= 8:
+            assert p.variant == 5 and p.k_waves == 2 and p.split_k == min((k // 32) // 4, 256 // strips128)
+        else:
+            assert p.variant == 6 and p.k_waves == 8 and p.split_k == 256 // strips128
+    elif wide:
+        assert p.path == _native.PATH_GEMV and p.variant == 5 and p.split_k == 256 // strips256
+        assert p.tile_n == (256 if m <= 2 else 128)
     elif m == 1 or (m == 2 and n % 32 != 0):
         assert p.path == _native.PATH_GEMV
     elif deep_gemv:
