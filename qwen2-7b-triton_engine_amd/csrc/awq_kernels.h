@@ -47,7 +47,6 @@ struct GemvConfig {
 // Variants 13, 14: the hybrid of variants 6 (128 rows) and 8 (64 rows) --
 // whole tiles on every CU, the leftover tiles split along K.  Numbers 10 - 12
 // (retired k-half pair tiles) name no kernel.
-constexpr int kTileVariants = 14;
 constexpr int tile5_rows(int variant) { return (variant == 8 || variant == 14) ? 64 : variant == 9 ? 32 : 128; }
 constexpr int tile5_threads(int) { return 256; }
 constexpr bool tile_hybrid(int variant) { return variant == 13 || variant == 14; }
