@@ -364,13 +364,22 @@ def _random_shapes(count, seed, kind="any"):
     and prefill routes, K any multiple of 128 up to 4992, N any multiple of 8
     up to 9592, at most 3e9 multiply-adds each; "decode": M <= 16 and N a
     multiple of 32 (the GEMV and stream routes); "prefill": M from 512 to
-    2100, K up to 4992, N up to 12800 (the tile routes and hybrids)."""
+    2100, K up to 4992, N up to 12800 (the tile routes and hybrids);
+    "strips": M <= 16, N a multiple of 32 from 256 to 8160, K from 2048 to
+    12800 (the column-strip GEMV classes, 16-row singles included), at most
+    40 M weights."""
     rng = np.random.default_rng(seed)
     ms = {"any": [1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 13, 16, 17, 20, 24, 31, 33, 48, 64, 65, 100, 129, 200, 257, 513,
                   1000],
-          "decode": list(range(1, 17)), "prefill": [512, 600, 1024, 1500, 2048, 2100]}[kind]
+          "decode": list(range(1, 17)), "prefill": [512, 600, 1024, 1500, 2048, 2100],
+          "strips": list(range(1, 17))}[kind]
     out = []
     while len(out) < count:
+        if kind == "strips":
+            m, k, n = int(rng.choice(ms)), 128 * int(rng.integers(16, 101)), 32 * int(rng.integers(8, 256))
+            if k * n <= 40e6:
+                out.append((m, k, n))
+            continue
         m, k = int(rng.choice(ms)), 128 * int(rng.integers(1, 40))
         n = 32 * int(rng.integers(1, 400)) if kind == "decode" else 8 * int(rng.integers(1, 1600 if kind == "prefill"
                                                                                            else 1200))
@@ -380,12 +389,13 @@ def _random_shapes(count, seed, kind="any"):
 
 
 @pytest.mark.parametrize("m,k,n", _random_shapes(40, 2027) + _random_shapes(16, 2028, "decode") +
-                         _random_shapes(6, 2029, "prefill"))
+                         _random_shapes(6, 2029, "prefill") + _random_shapes(12, 2030, "strips"))
 def test_auto_random_shapes(gpu, m, k, n):
     """AUTO on shapes no other test fixes, drawn at random: every output
     against the oracle's dequantised product, whichever route and split the
     dispatcher takes for the shape (N not a multiple of 32 or of a tile,
-    K of a few groups, M between the routes' bounds)."""
+    K of a few groups, M between the routes' bounds, strip widths and K of
+    the column-strip GEMV classes)."""
     x, qw, qz, s = O.make_inputs(m, k, n, seed=m + k + n)
     w = O.dequant_awq(qw, qz, s)
     y_ref = x.astype(np.float32) @ w.astype(np.float32)
