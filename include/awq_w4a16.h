@@ -78,7 +78,8 @@ typedef enum awq_w4a16_path {
     AWQ_PATH_AUTO = 0,
     AWQ_PATH_SKINNY = 1,         /* decode: MFMA skinny-M streaming kernel (M <= 64)         */
     AWQ_PATH_TILE = 2,           /* prefill: LDS-tiled MFMA GEMM                            */
-    AWQ_PATH_GEMV = 3,           /* decode: column-quad GEMV, MFMA or dot2 sums (M <= 2)    */
+    AWQ_PATH_GEMV = 3,           /* decode: column-strip GEMV (quads, pairs, singles), MFMA
+                                    or dot2 sums; M <= 2 when forced, to 16 under AUTO     */
     AWQ_PATH_STREAM = 5          /* decode: streaming 16x16x32 MFMA kernels (M <= 16)       */
 } awq_w4a16_path;
 
@@ -86,14 +87,16 @@ typedef enum awq_w4a16_path {
 typedef struct awq_w4a16_plan {
     int32_t path;                /* AWQ_PATH_SKINNY, _TILE, _GEMV or _STREAM                */
     int32_t variant;             /* kernel variant inside the path                          */
-    int32_t tile_m;              /* rows of x per work unit (skinny: 16, 32 or 64)          */
+    int32_t tile_m;              /* rows of x per work unit (skinny: 16, 32 or 64; gemv:
+                                    the rows of x its instance carries)                    */
     int32_t tile_n;              /* output columns per work unit                            */
     int32_t rows_per_wave;       /* skinny: K rows per wavefront (32, 64 or 128*q)          */
     int32_t k_waves;             /* skinny: wavefronts per workgroup along K (1, 2, 4)      */
     int32_t split_k;             /* workgroups along K; > 1 uses the fp32 workspace         */
     int32_t block_threads;       /* threads per workgroup                                   */
     int32_t factored_scale;      /* skinny: 1 = scale applied per group sum, 0 = per weight */
-    int32_t depth;               /* gemv variant 2: 128-row chunks in flight per wave; else 0 */
+    int32_t depth;               /* gemv, stream: chunk buffers per wave (gemv variant 2:
+                                    128-row groups in flight); else 0                      */
     int64_t grid;                /* workgroups in the one launch                            */
     uint64_t workspace_bytes;    /* split_k > 1: counter block + 64-bit fixed-point slots
                                     or counters + slot region + fp32 partials; else 0    */
