@@ -505,7 +505,11 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->split_k = (int32_t)split_k;
     p->rows_per_wave = (int32_t)(per * unit);  // K rows per split
     p->grid = tiles * split_k;
-    p->workspace_bytes = split_k > 1 ? partials_workspace(split_k, M, N) : 0u;
+    // Variant 6 (last-arriver finish): partials [split, M, N]; 7, 8, 9
+    // (reduce launch): fragment-native units of 16 rows x 256 columns.
+    p->workspace_bytes = split_k <= 1 ? 0u
+                         : variant == 6 ? partials_workspace(split_k, M, N)
+                                        : kPartialsOffset + tile_partials_bytes(split_k, M, N);
     if (tile_hybrid((int)variant)) {
         // Whole tiles: `full` per CU on every CU (fewer than the workgroups a
         // CU holds: 2 for 128 rows, 3 for 64); the L leftover tiles split

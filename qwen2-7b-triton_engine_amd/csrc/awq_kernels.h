@@ -116,10 +116,16 @@ bool stream_fits(int M, int K, int split_k, int k_waves, int layout);
 int64_t stream_threads(int layout, int k_waves);
 
 // split_k > 1 uses the same workspace contract as launch_skinny (counters:
-// one per tile; variants 7, 8, 9 add the partials in a second
-// launch of awq_splitk_reduce_kernel on the same stream).
+// one per tile).  Variants 7, 8, 9 keep fragment-native partials
+// (tile_partials_bytes of them at kPartialsOffset: one 16 KB unit per split,
+// 16-row block and 256-column tile) and add them in a second launch of
+// awq_tile_reduce_kernel on the same stream.
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream);
 int64_t tile_tiles(int M, int N, int variant);
+uint64_t tile_partials_bytes(int64_t split_k, int64_t M, int64_t N);
+// Threads that share one output piece in the reduce launches (enough that
+// each adds at most eight splits; eight from 12 splits up).
+int stream_reduce_parts(int split_k);
 
 // Output columns per skinny wave.
 constexpr int kSkinnyCols = 128;

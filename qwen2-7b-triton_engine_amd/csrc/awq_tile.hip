@@ -80,9 +80,10 @@ __device__ __forceinline__ int hy_bands(int n_sk, int d, int bm) {
 }
 
 // FIN (split_k > 1): 0 -- the last workgroup of a tile to arrive adds the
-// partials; 1 -- partials with plain stores, summed by a second launch of
-// awq_splitk_reduce_kernel over the whole device (for small tiles, whose
-// last arrivers would each read split x tile bytes alone).
+// partials; 1 -- fragment-native partials (whole-kilobyte stores of the
+// accumulator registers), summed by a second launch of
+// awq_tile_reduce_kernel over the whole device (for small tiles, whose last
+// arrivers would each read split x tile bytes alone).
 // HY (hybrid, FIN 0): workgroups 0 .. D-1 each take one whole tile, the last
 // L tiles of the order are split split_k ways along K, one piece per
 // remaining workgroup (grid = D + L split_k, so L = (grid - tiles) /
@@ -425,6 +426,30 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     // otherwise stay in registers across it.
     const uint32_t eln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
     const int e16 = (int)(eln & 15u), ekb = (int)(eln >> 4);
+    if constexpr (FIN == 1) {
+        if (ks > 1) {
+            // Split-K partials for the reduce launch, fragment-native: the
+            // accumulator registers as they are, each store one whole
+            // kilobyte (a wave's 64 lanes x 16 bytes), no exchange.  Unit
+            // (split, 16-row block rb, 256-column tile tn) is 16 KB at
+            // ((split x RB + rb) x NT + tn) x 16 KB, holding fragment (wave,
+            // c) at (4 wave + c) KB; lane l's value r is output (16 rb + l %
+            // 16, 256 tn + 64 wave + 16 c + 8 (kb >> 1) + 2 r + (kb & 1)), kb
+            // = l / 16.  Blocks of rows at or beyond M are not written (nor
+            // read by the reduce launch).
+            const int RB = (a.M + 15) >> 4, NT = (a.N + T5_BN - 1) / T5_BN;
+            const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, (uint32_t)((size_t)split_k * RB * NT * 16384));
+#pragma unroll
+            for (int f = 0; f < FM; ++f) {
+                if (m0 + 16 * f >= a.M) break;
+                const uint32_t unit = (uint32_t)(((split * RB + (m0 >> 4) + f) * NT + n0 / T5_BN));
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    buf_store_f4_device(acc[c][f], rp, unit * 16384u + (uint32_t)((4 * wn + c) * 1024) + eln * 16u);
+            }
+            return;
+        }
+    }
     {
         const bool odd = ekb & 1;
         const int src = (int)((eln ^ 16u) << 2);
@@ -512,9 +537,11 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         return;
     }
 
-    // Partials of this workgroup's split: [split_k, M, N], or for the hybrid's
-    // pieces [split_k][n_sk][BM][256] (PartLayout: byte base + r row_stride +
-    // 4 c + split split_stride for output (m0 + r, n0 + c)).
+    if constexpr (FIN == 1) return;  // split_k > 1 returned above
+    // FIN 0 (the last-arriver finish).  Partials of this workgroup's split:
+    // [split_k, M, N], or for the hybrid's pieces [split_k][n_sk][BM][256]
+    // (PartLayout: byte base + r row_stride + 4 c + split split_stride for
+    // output (m0 + r, n0 + c)).
     const PartLayout pl = HY ? PartLayout{(uint32_t)sk_tile * (uint32_t)(BM * T5_BN * 4), (uint32_t)(T5_BN * 4),
                                           (uint32_t)n_sk * (uint32_t)(BM * T5_BN * 4)}
                              : full_parts(a.M, a.N, m0, n0);
@@ -533,7 +560,6 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
             buf_store_f4_device(acc[c][f], rp_, off);
         }
     }
-    if constexpr (FIN == 1) return;
     wait_vm_stores();
     __syncthreads();
     if constexpr (HY) {
@@ -564,6 +590,63 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Second launch of tile variants 7, 8, 9 with split_k > 1: out = fp16(sum
+// over the splits of the fragment-native partials), each output summed in
+// split order (deterministic), with the bias / residual epilogue.  A thread
+// takes 8 consecutive columns of one output row: lanes 32 j + n and 32 j +
+// 16 + n of a fragment (k-blocks 2 j and 2 j + 1) hold them interleaved
+// (even and odd columns).  P threads share such a piece (splits p, p + P,
+// ...; at most eight splits each) and combine
+// through LDS in part order.  32 consecutive threads read one kilobyte.
+__global__ __launch_bounds__(256) void awq_tile_reduce_kernel(const float* __restrict__ partials, half_t* __restrict__ out,
+                                                             const half_t* bias, const half_t* residual, int M, int N,
+                                                             int split_k, int P) {
+    __shared__ floatx4 fin[2][256];
+    const int per_wg = 256 / P;  // pieces per workgroup
+    const int t = threadIdx.x;
+    const int part = t / per_wg;
+    const int RB = (M + 15) >> 4, NT = (N + T5_BN - 1) / T5_BN;
+    const int piece = blockIdx.x * per_wg + t % per_wg;
+    const int u = piece >> 9, in = piece & 511;     // unit rb x NT + tn; 512 pieces a unit
+    const int wc = in >> 5, j = (in >> 4) & 1, n16 = in & 15;
+    const int rb = u / NT, tn = u - rb * NT;
+    const int m = 16 * rb + n16;
+    const int n = T5_BN * tn + 64 * (wc >> 2) + 16 * (wc & 3) + 8 * j;
+    const bool valid = u < RB * NT && m < M && n < N;
+    floatx4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+        // In float4: a unit is 1024, a fragment 64, lane 32 j + n16.
+        const floatx4* p = reinterpret_cast<const floatx4*>(partials) + (size_t)u * 1024 + 64 * wc + 32 * j + n16;
+        const size_t step = (size_t)RB * NT * 1024;  // one split
+#pragma unroll 4
+        for (int sp = part; sp < split_k; sp += P) {
+            sa += __builtin_nontemporal_load(p + (size_t)sp * step);
+            sb += __builtin_nontemporal_load(p + (size_t)sp * step + 16);
+        }
+    }
+    fin[0][t] = sa;
+    fin[1][t] = sb;
+    __syncthreads();
+    if (valid && part == 0) {
+        for (int i = 1; i < P; ++i) {
+            sa += fin[0][i * per_wg + t];
+            sb += fin[1][i * per_wg + t];
+        }
+        const float y[8] = {sa[0], sb[0], sa[1], sb[1], sa[2], sb[2], sa[3], sb[3]};
+        store_out<8>(out, bias, residual, N, m, n, y);
+    }
+}
+
+int64_t tile_reduce_blocks(int M, int N, int split_k) {
+    const int64_t pieces = (int64_t)((M + 15) / 16) * ((N + T5_BN - 1) / T5_BN) * 512;
+    const int64_t per_wg = 256 / stream_reduce_parts(split_k);
+    return (pieces + per_wg - 1) / per_wg;
+}
+
+uint64_t tile_partials_bytes(int64_t split_k, int64_t M, int64_t N) {
+    return (uint64_t)split_k * (uint64_t)((M + 15) / 16) * (uint64_t)((N + T5_BN - 1) / T5_BN) * 16384u;
+}
+
 int64_t tile_tiles(int M, int N, int variant) {
     const int bm = tile5_rows(variant);
     return (int64_t)((M + bm - 1) / bm) * ((N + T5_BN - 1) / T5_BN);
@@ -586,7 +669,10 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess || !reduce || cfg.split_k <= 1) return e;
-        return splitk_reduce_launch(a, cfg.split_k, stream);
+        hipLaunchKernelGGL(awq_tile_reduce_kernel, dim3((unsigned)tile_reduce_blocks(a.M, a.N, cfg.split_k)), dim3(256),
+                           0, stream, a.partials, a.out, a.bias, a.residual, a.M, a.N, cfg.split_k,
+                           stream_reduce_parts(cfg.split_k));
+        return hipGetLastError();
     }
     return hipErrorInvalidValue;
 }

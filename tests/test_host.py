@@ -153,6 +153,10 @@ def test_auto_plan_invariants(L, m, k, n):
             assert p.grid == tiles - left + left * p.split_k
             assert p.workspace_bytes == (_native.counter_bytes() + _native.SLOT_BYTES +
                                          p.split_k * left * tm * 256 * 4)
+        elif p.path == _native.PATH_TILE and p.variant in (7, 8, 9):
+            # reduce launch: fragment-native units of 16 rows x 256 columns
+            assert p.workspace_bytes == (_native.counter_bytes() + _native.SLOT_BYTES +
+                                         p.split_k * -(-m // 16) * 16 * -(-n // 256) * 256 * 4)
         else:
             assert p.workspace_bytes == _native.counter_bytes() + _native.SLOT_BYTES + p.split_k * m * n * 4
     else:
