@@ -91,20 +91,21 @@ def kernel_family_kernel(_native, m, n, k, name):
     return name if name.startswith(prefixes) else None
 
 
-# Kernels each path family launches (a stream-path GEMM whose split-K partials
-# are added by a second launch runs awq_splitk_reduce_kernel after the main
-# kernel; both count as that GEMM's launch).
+# Kernels each path family launches (a GEMM whose split-K partials are added
+# by a second launch runs a reduce kernel after the main kernel --
+# awq_tile_reduce_kernel after the tile kernel, awq_splitk_reduce_kernel
+# after the others; both count as that GEMM's launch).
 FAMILY_KERNELS = {
     "gemv": ("awq_gemv",),
     "skinny": ("awq_skinny",),
     "stream": ("awq_stream", "awq_splitk_reduce"),
-    "tile": ("awq_tile", "awq_splitk_reduce"),
+    "tile": ("awq_tile",),
 }
 FAMILY_NAMES = {
     "gemv": "awq_gemv_quad_kernel",
     "skinny": "awq_skinny_kernel",
     "stream": "awq_stream_row_kernel / awq_stream_kernel (+ awq_splitk_reduce_kernel)",
-    "tile": "awq_tile_kernel (+ awq_splitk_reduce_kernel)",
+    "tile": "awq_tile_kernel (+ awq_tile_reduce_kernel)",
 }
 
 
@@ -145,8 +146,12 @@ def prefill_counter_pass(torch, dev):
 
 
 # ---- profile summaries (host only: rocprofv3 CSV -> profiles/) -------------
+# Second launches that add split-K partials.
+REDUCE_KERNELS = ("awq_splitk_reduce_kernel", "awq_tile_reduce_kernel")
+
+
 def _short_kernel(name):
-    for key in ("awq_splitk_reduce_kernel", "awq_zero_fill_kernel"):
+    for key in (*REDUCE_KERNELS, "awq_zero_fill_kernel"):
         if key in name:
             return key
     name = name.replace("void awq::", "")
@@ -181,14 +186,14 @@ def _copy_scale(rows, counter):
 
 def _gemm_groups(rows):
     """AWQ dispatches grouped per GEMM: a main kernel and, when its split-K
-    partials are added by a second launch, the awq_splitk_reduce_kernel that
-    follows it."""
+    partials are added by a second launch, the reduce kernel that follows
+    it."""
     groups = []
     for row in rows:
         k = _short_kernel(row[1])
         if not k.startswith("awq_") or k == "awq_zero_fill_kernel":
             continue
-        if k == "awq_splitk_reduce_kernel" and groups:
+        if k in REDUCE_KERNELS and groups:
             groups[-1].append(row)
         else:
             groups.append([row])
@@ -228,7 +233,8 @@ def summarize(argv):
               "`bench.py --counter-pass` makes the operands, runs one 64 MiB device-to-device copy",
               "(`torch.Tensor.copy_`, dispatched as `__amd_rocclr_copyBuffer`), then one eager launch of each",
               "engine shape at M = 1, 4, 16 on layer 0's weights (AUTO plans; a GEMM whose split-K partials are",
-              "added by a second launch shows two dispatches, the main kernel and `awq_splitk_reduce_kernel`).", "",
+              "added by a second launch shows two dispatches, the main kernel and its reduce kernel,",
+              "`awq_tile_reduce_kernel` after the tile kernel, `awq_splitk_reduce_kernel` after the others).", "",
               "## Calibration with the copy of known size (67,108,864 B read and written)", "",
               "| counter | reads for the copy (KiB) | expected (KiB) | scale factor |", "|---|---|---|---|",
               f"| FETCH_SIZE | {fcopy:.1f} | 65536 | {fs:.4f} |", f"| WRITE_SIZE | {wcopy:.1f} | 65536 | {ws:.4f} |",
@@ -455,7 +461,7 @@ def _summarize_prefill_trace(d, prof, cmd_head):
             continue
         gap = 0
         wgs = int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"])
-        if name == "awq_splitk_reduce_kernel":
+        if name in REDUCE_KERNELS:
             if cur is not None:
                 cur["reduce"].append(r)
             continue
@@ -497,7 +503,7 @@ def _summarize_prefill_trace(d, prof, cmd_head):
         ">= 640 MB of distinct random-init weight copies), found in the trace as a run of launches of",
         "the kernel and grid AUTO plans for the shape.  The first replays run while the clocks are",
         "still rising, so the median and the minimum are the figures to read.  Plans with the",
-        "reduce-launch finish are followed by one `awq_splitk_reduce_kernel` launch each (its median in",
+        "reduce-launch finish are followed by one `awq_tile_reduce_kernel` launch each (its median in",
         "the reduce column).  TFLOP/s = 2 M N K / (median launch + median reduce launch); the",
         f"percentage is of the dense fp16 MFMA peak ({MFMA_F16_DENSE_PEAK_FLOPS / 1e12:.1f} TFLOP/s).", "",
         "| GEMM | kernel | variant, split | workgroups x threads | LDS B | VGPR+AGPR / scratch | launches "
