@@ -39,6 +39,8 @@ VOCAB = 152064
 ENGINE_SHAPES = (("qkv_proj", HIDDEN, 4608), ("o_proj", HIDDEN, HIDDEN),
                  ("gate_up_proj", HIDDEN, 2 * INTER), ("down_proj", INTER, HIDDEN))
 DECODE_M = (1, 4, 16)
+# The down_proj M-sweep's HBM-bound points beyond the decode sweep, also in the decode counter pass.
+SWEEP_PMC_M = (8, 64)
 # Weight bytes every per-shape timing cycles through: 2.5x the 256 MB MALL,
 # so that each launch reads its weights from HBM.
 MIN_ROTATE_BYTES = 640e6
@@ -211,6 +213,7 @@ def summarize(argv):
         ws, wcopy = _copy_scale(write, "WRITE_SIZE")
         gf, gw = _gemm_groups(fetch), _gemm_groups(write)
         keys = [(m, name, k, n) for m in DECODE_M for name, k, n in ENGINE_SHAPES]
+        keys += [(m, "down_proj", INTER, HIDDEN) for m in SWEEP_PMC_M]
         assert len(gf) == len(gw) == len(keys), (len(gf), len(gw), len(keys))
         launches = []
         for (m, name, k, n), a, b in zip(keys, gf, gw):
@@ -232,7 +235,8 @@ def summarize(argv):
               "```", cmd_head, *cmds, "```", "",
               "`bench.py --counter-pass` makes the operands, runs one 64 MiB device-to-device copy",
               "(`torch.Tensor.copy_`, dispatched as `__amd_rocclr_copyBuffer`), then one eager launch of each",
-              "engine shape at M = 1, 4, 16 on layer 0's weights (AUTO plans; a GEMM whose split-K partials are",
+              "engine shape at M = 1, 4, 16 on layer 0's weights, then down_proj at M = 8 and 64 (the M-sweep's",
+              "HBM-bound points) on the same weights (AUTO plans; a GEMM whose split-K partials are",
               "added by a second launch shows two dispatches, the main kernel and its reduce kernel,",
               "`awq_tile_reduce_kernel` after the tile kernel, `awq_splitk_reduce_kernel` after the others).", "",
               "## Calibration with the copy of known size (67,108,864 B read and written)", "",
@@ -617,8 +621,12 @@ def main():
             for name, k, n in ENGINE_SHAPES:
                 awq_gemm_forward(xs[(m, k)], *layers[0][name])
                 torch.cuda.synchronize()
+        for m in SWEEP_PMC_M:
+            awq_gemm_forward(torch.randn((m, INTER), generator=gx, device=dev).half(), *layers[0]["down_proj"])
+            torch.cuda.synchronize()
         log("counter pass done: copy 67108864 B, then " + ", ".join(
-            f"M={m} {name} {kernel_family(_native, m, n, k)}" for m in DECODE_M for name, k, n in ENGINE_SHAPES))
+            [f"M={m} {name} {kernel_family(_native, m, n, k)}" for m in DECODE_M for name, k, n in ENGINE_SHAPES] +
+            [f"M={m} down_proj {kernel_family(_native, m, HIDDEN, INTER)}" for m in SWEEP_PMC_M]))
         return
 
     step()  # eager: sizes the shared workspace before capture
