@@ -235,6 +235,55 @@ def test_tile_plans_cover_k_exactly(L, k, n):
                     assert tiles * 4 <= _native.counter_bytes()
 
 
+@pytest.mark.parametrize("m,n,bm", [(16, 4608, 32), (64, 3584, 64), (70, 264, 64), (300, 1032, 128)])
+def test_tile_fragment_partials_layout_agrees(m, n, bm):
+    """The layout contract between the tile kernel's fragment-native partial
+    stores and the tile reduce kernel (both in csrc/awq_tile.hip), restated
+    from each side: the store side addresses lane l's value r of fragment
+    (wave, c, f) of a tile, the reduce side addresses the 8-column piece of a
+    thread.  Every output of every split must be read from exactly the bytes
+    written for it, and every written byte of a row below M read once."""
+    split = 3
+    rb_n, nt = -(-m // 16), -(-n // 256)
+    # Store side: (split, tile, wave, f, c, lane, r) -> byte offset, output (row, col).
+    store = {}
+    for s in range(split):
+        for m0 in range(0, m, bm):
+            for n0 in range(0, nt * 256, 256):
+                for f in range(bm // 16):
+                    if m0 + 16 * f >= m:
+                        break
+                    unit = (s * rb_n + m0 // 16 + f) * nt + n0 // 256
+                    for w in range(4):
+                        for c in range(4):
+                            for lane in range(64):
+                                kb = lane // 16
+                                for r in range(4):
+                                    row = m0 + 16 * f + lane % 16
+                                    col = n0 + 64 * w + 16 * c + 8 * (kb >> 1) + 2 * r + (kb & 1)
+                                    off = unit * 16384 + (4 * w + c) * 1024 + lane * 16 + 4 * r
+                                    store[(s, row, col)] = off
+    # Reduce side: piece -> its output row and 8 columns, the float4s it reads per split.
+    read = {}
+    for piece in range(rb_n * nt * 512):
+        u, rem = piece >> 9, piece & 511
+        wc, j, n16 = rem >> 5, (rem >> 4) & 1, rem & 15
+        rb, tn = u // nt, u % nt
+        row, col = 16 * rb + n16, 256 * tn + 64 * (wc >> 2) + 16 * (wc & 3) + 8 * j
+        if row >= m or col >= n:
+            continue
+        for s in range(split):
+            base = (s * rb_n * nt * 1024 + u * 1024 + 64 * wc + 32 * j + n16) * 16
+            for r in range(4):
+                read[(s, row, col + 2 * r)] = base + 4 * r
+                read[(s, row, col + 2 * r + 1)] = base + 16 * 16 + 4 * r
+    live = {k: v for k, v in store.items() if k[1] < m and k[2] < n}
+    assert len(read) == split * m * n
+    assert live == read
+    assert len(set(read.values())) == len(read)
+    assert max(store.values()) < split * rb_n * nt * 16384
+
+
 def test_build_rejects_register_spills():
     """build.py reads hipcc's per-kernel resource remarks and refuses kernels
     that spill registers to scratch memory."""
