@@ -404,6 +404,49 @@ def test_auto_random_shapes(gpu, m, k, n):
     _assert_close(_run(gpu, x, qw, qz, s), y_ref, f"random M={m} K={k} N={n}")
 
 
+def test_auto_many_random_shapes_against_fp32(gpu):
+    """AUTO on 300 seeded random shapes at once (M from 1 to 2100, K any
+    multiple of 128 up to 18944, N any multiple of 8 up to 40000, at most
+    1.5e11 multiply-adds): the output against a plain PyTorch fp32 product of
+    the same operands (x in fp32 times the weight dequantised by
+    awq_w4a16_dequant, which the tests above pin bit for bit to the oracle),
+    and the fused bias + residual epilogue bit-identical to torch's fp16 adds
+    on the GEMM's own output.  Covers every route, variant and split-K finish
+    AUTO takes over that range (the GEMV, skinny, stream and tile kernels and
+    the hybrids)."""
+    rng = np.random.default_rng(303)
+    ms = list(range(1, 17)) + [17, 20, 24, 31, 32, 33, 40, 48, 63, 64, 65, 80, 96, 100, 128, 129, 200, 256, 257,
+                               384, 500, 512, 513, 700, 1000, 1024, 1500, 2048, 2100]
+    routes, done = set(), 0
+    while done < 300:
+        m, k, n = int(rng.choice(ms)), 128 * int(rng.integers(1, 149)), 8 * int(rng.integers(1, 5000))
+        if m * k * n > 1.5e11 or k * n > 6e8:
+            continue
+        g = torch.Generator(device=gpu)
+        g.manual_seed(done)
+        x = torch.randn((m, k), generator=g, device=gpu).half()
+        qw = torch.randint(-2**31, 2**31 - 1, (k, n // 8), generator=g, device=gpu, dtype=torch.int32)
+        qz = torch.randint(-2**31, 2**31 - 1, (k // 128, n // 8), generator=g, device=gpu, dtype=torch.int32)
+        sc = (torch.rand((k // 128, n), generator=g, device=gpu) * 0.018 + 0.002).half()
+        bias = (torch.randn(n, generator=g, device=gpu) * 0.5).half()
+        res = (torch.randn((m, n), generator=g, device=gpu) * 4).half()
+        y = awq_gemm_forward(x, qw, qz, sc)
+        w = torch.empty((k, n), dtype=torch.float16, device=gpu)
+        _dequant_to_fp16(qw, qz, sc, w)
+        ref = torch.matmul(x.float(), w.float())
+        fused = awq_gemm_forward_ex(x, qw, qz, sc, bias=bias, residual=res)
+        unfused = res + (y + bias)
+        torch.cuda.synchronize()
+        p = _native.plan_for(m, n, k)
+        what = f"random M={m} K={k} N={n} ({_native.PATH_NAMES[p.path]} v{p.variant} split={p.split_k})"
+        _assert_close(y.float().cpu().numpy(), ref.cpu().numpy(), what)
+        assert torch.equal(fused.view(torch.int16), unfused.view(torch.int16)), what + ": epilogue"
+        routes.add((p.path, p.variant, p.split_k > 1))
+        done += 1
+    print(f"{done} random shapes over {len(routes)} routes", flush=True)
+    assert len(routes) >= 12, routes
+
+
 @pytest.mark.parametrize("m", [1, 2])
 def test_gemv_quad_plans_agree(gpu, m):
     """Column-quad GEMV (balanced K split, fixed-point split-K finish): split
