@@ -455,16 +455,16 @@ __global__ __launch_bounds__(512) void awq_gemv_quad_kernel(GemmArgs a, int spli
     if constexpr (RED) {
         if (split_k > 1) {
             // fp32 partials [split_k, M, N] (write-through), added by a second
-            // launch of awq_splitk_reduce_kernel.
+            // launch of awq_splitk_reduce_kernel.  A thread takes four
+            // consecutive columns (N % 32 == 0: all or none of them exist),
+            // so a wave's store covers 1 KB of a row.
             const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, (uint32_t)((size_t)split_k * a.M * a.N * 4));
-            for (int idx = threadIdx.x; idx < MR * SC; idx += nt) {
-                const int m = idx / SC, t = idx - m * SC, n = strip * SC + t;
+            for (int idx = threadIdx.x; idx < MR * SC / 4; idx += nt) {
+                const int m = idx / (SC / 4), t = 4 * (idx - m * (SC / 4)), n = strip * SC + t;
                 if (m >= a.M || n >= a.N) continue;
-                float v = 0.f;
-                for (int w = 0; w < nw; ++w) v += red[(w * MR + m) * SC + t];
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rp,
-                                                      (uint32_t)((((size_t)split * a.M + m) * a.N + n) * 4), 0,
-                                                      kCpolSC1);
+                floatx4 v = {0.f, 0.f, 0.f, 0.f};
+                for (int w = 0; w < nw; ++w) v += *reinterpret_cast<const floatx4*>(&red[(w * MR + m) * SC + t]);
+                buf_store_f4_device(v, rp, (uint32_t)((((size_t)split * a.M + m) * a.N + n) * 4));
             }
             return;
         }
