@@ -492,7 +492,7 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->lds_bytes = 0;
     if (!tile_variant_served((int)variant) || split_k < 1) return AWQ_ERR_PATH;
     p->tile_m = tile5_rows((int)variant);
-    p->tile_n = 256;
+    p->tile_n = tile5_cols((int)variant);
     p->block_threads = tile5_threads((int)variant);
     const int64_t tiles = tile_tiles((int)M, (int)N, (int)variant);
     // K range per split: whole 128-row groups (two 64-row k-steps).
@@ -505,7 +505,7 @@ int fill_tile(int64_t M, int64_t N, int64_t K, int64_t variant, int64_t split_k,
     p->split_k = (int32_t)split_k;
     p->rows_per_wave = (int32_t)(per * unit);  // K rows per split
     p->grid = tiles * split_k;
-    // Variant 6 (last-arriver finish): partials [split, M, N]; 7, 8, 9
+    // Variant 6 (last-arriver finish): partials [split, M, N]; 7, 8, 9, 15
     // (reduce launch): fragment-native units of 16 rows x 256 columns.
     p->workspace_bytes = split_k <= 1 ? 0u
                          : variant == 6 ? partials_workspace(split_k, M, N)
@@ -652,6 +652,25 @@ const TileModel* tile_model(int variant) {
 // unsplit grid leaves CUs idle or some CUs a whole tile more than others.
 int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     const int64_t groups = K / kGroup;
+    // Deep weights (K >= 8192) at M >= 512: the eight-wave 512-column tile
+    // (variant 15) at the largest split whose grid fits one workgroup per CU,
+    // where one does.  down_proj 18944 x 3584, A/B in one process against the
+    // 256-column tiles' AUTO plans (us): M = 512 80.7 (split 8) against 82.4;
+    // M = 1024 137.6 (split 4) against 149.1 (139.8 at that tile's best
+    // split); M = 1536 195.0 (split 3) against 195.2; M = 2048 255.6 (split 2)
+    // against 266.6; M = 4096 470.7 (split 1) against 490.5.  Splits that
+    // put a second workgroup on some CUs were slower (M = 2048 split 3 331.6,
+    // M = 4096 split 2 521.3), and at K = 3584 the 512-column tile lost to the
+    // 256-column one (o at M = 2048 66.7 against 59.1 us; gate||up even).
+    if (K >= 8192 && M >= 512) {
+        for (int64_t sp = groups < 32 ? groups : 32; sp >= 1; --sp) {
+            awq_w4a16_plan q;
+            if (fill_tile(M, N, K, 15, sp, &q) == AWQ_OK && q.grid <= (int64_t)cus()) {
+                *p = q;
+                return AWQ_OK;
+            }
+        }
+    }
     // Deep weights (K >= 8192) up to M = 1024: a split grid with more than
     // one workgroup per CU measured slower than the model predicts (the second
     // workgroup of a CU competes for its load bandwidth through a short run

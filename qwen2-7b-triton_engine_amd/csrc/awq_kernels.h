@@ -42,21 +42,23 @@ struct GemvConfig {
     int cw;                  // variant 5: packed columns per lane, 4 (512-column strips) or 2 (256)
 };
 
-// Tile variants 6 .. 9, 13, 14: weights dequantised into MFMA registers,
+// Tile variants 6 .. 9, 13, 14, 15: weights dequantised into MFMA registers,
 // every load a direct global->LDS load into a ring (x rows per tile, stages).
 // Variants 13, 14: the hybrid of variants 6 (128 rows) and 8 (64 rows) --
-// whole tiles on every CU, the leftover tiles split along K.  Numbers 10 - 12
-// (retired k-half pair tiles) name no kernel.
+// whole tiles on every CU, the leftover tiles split along K.  Variant 15:
+// variant 7 with eight waves on 512-column tiles, one workgroup per CU.
+// Numbers 10 - 12 (retired k-half pair tiles) name no kernel.
 constexpr int tile5_rows(int variant) { return (variant == 8 || variant == 14) ? 64 : variant == 9 ? 32 : 128; }
-constexpr int tile5_threads(int) { return 256; }
+constexpr int tile5_cols(int variant) { return variant == 15 ? 512 : 256; }
+constexpr int tile5_threads(int variant) { return variant == 15 ? 512 : 256; }
 constexpr bool tile_hybrid(int variant) { return variant == 13 || variant == 14; }
 // Whether a tile variant number names a kernel.
 constexpr bool tile_variant_served(int variant) {
-    return (variant >= 6 && variant <= 9) || variant == 13 || variant == 14;
+    return (variant >= 6 && variant <= 9) || variant == 13 || variant == 14 || variant == 15;
 }
 
 struct TileConfig {
-    int variant;             // 6 .. 9, 13, 14: register dequant, N tile 256
+    int variant;             // 6 .. 9, 13, 14, 15: register dequant, N tile 256 (15: 512)
     int tile_m, tile_n;
     int split_k;             // workgroups along K per tile (hybrid: per leftover tile)
     int k_per_split;         // K rows per split (a multiple of the 128-row group)

@@ -39,24 +39,27 @@ namespace awq {
 namespace {
 constexpr int T5_BK = 64;
 constexpr int T5_BN = 256;
-constexpr int T5_W_BYTES = 64 * 32 * 4;       // packed weights of one k-step
 constexpr int T5_ZS_WAVE = 160;               // one wave's 8 zero words + 64 scales
 constexpr int T5_GM = 4;
 constexpr int T5_STAGES = 3;
 
-template <int FM>
+template <int FM, int NW = 4>
 struct T5Layout {
     static constexpr int S = T5_STAGES;
     static constexpr int BM = 16 * FM;  // x rows per tile (every wave reads all of them)
+    static constexpr int BN = 64 * NW;  // columns per tile: 64 a wave
     static constexpr int X_BYTES = BM * T5_BK * 2;
-    static constexpr int ZS_BYTES = 4 * T5_ZS_WAVE;
-    static constexpr int STAGE = X_BYTES + T5_W_BYTES + ZS_BYTES;
-    static constexpr int WAVES = 4;
+    static constexpr int W_BYTES = 2048 * NW;  // packed weights of one k-step
+    static constexpr int ZS_BYTES = NW * T5_ZS_WAVE;
+    static constexpr int STAGE = X_BYTES + W_BYTES + ZS_BYTES;
+    static constexpr int WAVES = NW;
+    // The ring, or the staged fp16 tile (rows BN x 2 + 32 bytes apart) if larger.
+    static constexpr int SMEM = S * STAGE > BM * (BN * 2 + 32) ? S * STAGE : BM * (BN * 2 + 32);
     static constexpr int X_LOADS = X_BYTES / 1024 / WAVES;  // dwordx4 loads per wave per stage (FM / 2)
     // Workgroups per CU: by registers (accumulators 4 * FM float4 per lane)
     // and by LDS (S stages).
-    static constexpr int PER_CU_REG = FM >= 8 ? 2 : (FM >= 4 ? 3 : 4);
-    static constexpr int PER_CU_LDS = (160 * 1024) / (S * STAGE + 64);
+    static constexpr int PER_CU_REG = NW == 8 ? 1 : (FM >= 8 ? 2 : (FM >= 4 ? 3 : 4));
+    static constexpr int PER_CU_LDS = (160 * 1024) / (SMEM + 64);
     static constexpr int PER_CU = PER_CU_REG < PER_CU_LDS ? PER_CU_REG : PER_CU_LDS;
     static constexpr int W_LOADS = 2;  // dwordx4 packed-weight loads per wave per stage (its own 2 KB)
     // Loads a wave issues per stage: an even k-step's (the first of its
@@ -93,17 +96,24 @@ __device__ __forceinline__ int hy_bands(int n_sk, int d, int bm) {
 // pieces finish early, so their last arrivers add the partials while the
 // whole tiles still run.  The pieces' partials are compact: [split_k][L][BM
 // rows][256 columns] fp32.
-template <int FM, int FIN, bool HY = false>
-__global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(GemmArgs a, int split_k,
+//
+// NW: waves per workgroup, each owning 64 of the tile's 64 NW columns (4:
+// 256-column tiles, two workgroups per CU for 128 rows; 8: 512-column tiles,
+// one workgroup per CU, FIN 1 and no hybrid only -- variant 15).  The x rows
+// of a k-step are loaded once for all of the workgroup's columns.
+template <int FM, int FIN, bool HY = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, (T5Layout<FM, NW>::PER_CU)) void awq_tile_kernel(GemmArgs a, int split_k,
                                                                               int k_per_split,
                                                                               uint32_t* counters) {
-    using L = T5Layout<FM>;
+    using L = T5Layout<FM, NW>;
+    constexpr int BN = L::BN;
     constexpr int BM = L::BM;
     constexpr int S = L::S;
     static_assert((S - 2) * L::LOADS <= 63, "vmcnt holds 6 bits");
     static_assert(FM % 2 == 0 && L::X_LOADS >= 1, "a wave loads whole 8-row blocks of x");
-    static_assert(L::PER_CU >= 1 && L::PER_CU * S * L::STAGE <= 160 * 1024, "LDS per CU");
-    __shared__ __attribute__((aligned(16))) unsigned char smem[S * L::STAGE];
+    static_assert(L::PER_CU >= 1 && L::PER_CU * L::SMEM <= 160 * 1024, "LDS per CU");
+    static_assert(NW == 4 || (NW == 8 && FIN == 1 && !HY), "eight waves: reduce-launch finish only");
+    __shared__ __attribute__((aligned(16))) unsigned char smem[L::SMEM];
     __shared__ int last_flag;
     __shared__ int last_band[8];
     floatx4* fin = reinterpret_cast<floatx4*>(smem);  // split-K finish, after the main loop
@@ -117,7 +127,7 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
 
     // ---- work item: XCD-aware grouped tile order (groups of T5_GM row tiles) ----
     const int m_tiles = (a.M + BM - 1) / BM;
-    const int n_tiles = (a.N + T5_BN - 1) / T5_BN;
+    const int n_tiles = (a.N + BN - 1) / BN;
     // Position of workgroup b among `total` consecutive ones in XCD order:
     // the workgroups one XCD runs (b % 8 == x) get consecutive positions.
     auto xcd_order = [](int b, int total) {
@@ -163,7 +173,7 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         const int first_m = (t / in_group) * T5_GM;
         const int gm = min(m_tiles - first_m, T5_GM);
         tm0 = (first_m + (t % in_group) % gm) * BM;
-        tn0 = ((t % in_group) / gm) * T5_BN;
+        tn0 = ((t % in_group) / gm) * BN;
     };
     int m0, n0;
     tile_origin(tile, m0, n0);
@@ -222,7 +232,7 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         // group).  Partial-wave loads: the lanes left out write no LDS (never
         // all of them, so both loads issue and count in vmcnt).
         if ((kt & 1) == 0) {
-            const uint32_t zb = base + L::X_BYTES + T5_W_BYTES + (uint32_t)(T5_ZS_WAVE * wave);
+            const uint32_t zb = base + L::X_BYTES + L::W_BYTES + (uint32_t)(T5_ZS_WAVE * wave);
             if (lane >= 32 && lane < 40)
                 buffer_load_lds_x1(rz, zs_voff, __builtin_amdgcn_readfirstlane((uint32_t)g * (uint32_t)pn * 4u),
                                    zb - 128u);
@@ -291,7 +301,7 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         // column 2 c + n16 / 8 at z_rd + 8 c; its scale at s_rd + 32 c.
         const uint32_t w_rd = (uint32_t)L::X_BYTES + 2048u * (uint32_t)wn + 32u * (uint32_t)tr_row;
         const uint32_t tr_lo = w_rd + 16u * (uint32_t)tr_sw;  // w_rd is 32-aligned: tr_hi = tr_lo ^ 16
-        const uint32_t z_base = (uint32_t)(L::X_BYTES + T5_W_BYTES + T5_ZS_WAVE * wn);
+        const uint32_t z_base = (uint32_t)(L::X_BYTES + L::W_BYTES + T5_ZS_WAVE * wn);
         const uint32_t z_rd = z_base + 4u * (uint32_t)(n16 >> 3);
         const uint32_t s_rd = z_base + 32u + 16u * (uint32_t)(n16 >> 3) + 2u * (uint32_t)(2 * (sgi & 3) + (sgi >> 2));
         const uint32_t zsh = 4u * (uint32_t)sgi;
@@ -450,15 +460,20 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
             // 16, 256 tn + 64 wave + 16 c + 8 (kb >> 1) + 2 r + (kb & 1)), kb
             // = l / 16.  Blocks of rows at or beyond M are not written (nor
             // read by the reduce launch).
+            // A 512-column tile (eight waves) writes two such units, waves
+            // 4 .. 7 the second (none where it lies beyond N).
             const int RB = (a.M + 15) >> 4, NT = (a.N + T5_BN - 1) / T5_BN;
             const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partials, (uint32_t)((size_t)split_k * RB * NT * 16384));
+            const int tn = n0 / T5_BN + (NW == 8 ? (wn >> 2) : 0);
+            const int wq = NW == 8 ? (wn & 3) : wn;
+            if (NW == 8 && tn >= NT) return;
 #pragma unroll
             for (int f = 0; f < FM; ++f) {
                 if (m0 + 16 * f >= a.M) break;
-                const uint32_t unit = (uint32_t)(((split * RB + (m0 >> 4) + f) * NT + n0 / T5_BN));
+                const uint32_t unit = (uint32_t)(((split * RB + (m0 >> 4) + f) * NT + tn));
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    buf_store_f4_device(acc[c][f], rp, unit * 16384u + (uint32_t)((4 * wn + c) * 1024) + eln * 16u);
+                    buf_store_f4_device(acc[c][f], rp, unit * 16384u + (uint32_t)((4 * wq + c) * 1024) + eln * 16u);
             }
             return;
         }
@@ -486,14 +501,14 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
             tile_origin(n_tiles * m_tiles - n_sk + t, tm0, tn0);
             const int br = BM / hb;
             const int row0 = tm0 + h * br;
-            const uint32_t tile_bytes = (uint32_t)(BM * T5_BN * 4);
-            const PartLayout bp{(uint32_t)t * tile_bytes + (uint32_t)(h * br) * (uint32_t)(T5_BN * 4),
-                                (uint32_t)(T5_BN * 4), (uint32_t)n_sk * tile_bytes};
+            const uint32_t tile_bytes = (uint32_t)(BM * BN * 4);
+            const PartLayout bp{(uint32_t)t * tile_bytes + (uint32_t)(h * br) * (uint32_t)(BN * 4),
+                                (uint32_t)(BN * 4), (uint32_t)n_sk * tile_bytes};
             const __amdgpu_buffer_rsrc_t rpb = make_rsrc(a.partials, (uint32_t)split_k * bp.split_stride);
             const int rows = min(br, a.M - row0);
             if (rows > 0)
                 splitk_finish<(FM >= 8 ? 16 : 8)>(rpb, a.out, a.bias, a.residual, a.M, a.N, row0, rows, tn0,
-                                                  min(T5_BN, a.N - tn0), split_k, fin, bp);
+                                                  min(BN, a.N - tn0), split_k, fin, bp);
             if (tid == 0)
                 __hip_atomic_store(&counters[t * hb + h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -505,8 +520,8 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         // rows are 544 bytes apart, so the 16 rows of a wave's 8-byte writes
         // start 8 banks apart.  The ring is free: every wave has passed the
         // last step's barrier, after which no load is in flight.
-        constexpr int ROW = T5_BN * 2 + 32;
-        static_assert(BM * ROW <= S * L::STAGE, "the staged tile fits in the ring");
+        constexpr int ROW = BN * 2 + 32;
+        static_assert(BM * ROW <= L::SMEM, "the staged tile fits");
         typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
         typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 #pragma unroll
@@ -520,8 +535,8 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
         const bool epi = a.bias || a.residual;
         const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.out, (uint32_t)((size_t)a.M * a.N * 2));
 #pragma unroll
-        for (int p = tid; p < BM * (T5_BN / 8); p += 256) {
-            const int r = p >> 5, c8 = 8 * (p & 31);
+        for (int p = tid; p < BM * (BN / 8); p += 64 * NW) {
+            const int r = (int)((unsigned)p / (BN / 8)), c8 = 8 * (int)((unsigned)p % (BN / 8));
             const int m = m0 + r, n = n0 + c8;
             if (m >= a.M || n >= a.N) continue;
             h8_t h = *reinterpret_cast<const h8_t*>(smem + r * ROW + 2 * c8);
@@ -555,8 +570,8 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     // [split_k, M, N], or for the hybrid's pieces [split_k][n_sk][BM][256]
     // (PartLayout: byte base + r row_stride + 4 c + split split_stride for
     // output (m0 + r, n0 + c)).
-    const PartLayout pl = HY ? PartLayout{(uint32_t)sk_tile * (uint32_t)(BM * T5_BN * 4), (uint32_t)(T5_BN * 4),
-                                          (uint32_t)n_sk * (uint32_t)(BM * T5_BN * 4)}
+    const PartLayout pl = HY ? PartLayout{(uint32_t)sk_tile * (uint32_t)(BM * BN * 4), (uint32_t)(BN * 4),
+                                          (uint32_t)n_sk * (uint32_t)(BM * BN * 4)}
                              : full_parts(a.M, a.N, m0, n0);
     const uint32_t part_bytes = HY ? (uint32_t)split_k * pl.split_stride : (uint32_t)((size_t)split_k * a.M * a.N * 4);
     const __amdgpu_buffer_rsrc_t rp_ = make_rsrc(a.partials, part_bytes);
@@ -599,7 +614,7 @@ __global__ __launch_bounds__(256, (T5Layout<FM>::PER_CU)) void awq_tile_kernel(G
     // registers; the 64-row tile (three workgroups per CU, 168 VGPRs) takes
     // 8 so that nothing spills.
     splitk_finish<(FM >= 8 ? 16 : 8)>(rp_, a.out, a.bias, a.residual, a.M, a.N, m0, min(BM, a.M - m0), n0,
-                                      min(T5_BN, a.N - n0), split_k, fin, pl);
+                                      min(BN, a.N - n0), split_k, fin, pl);
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -661,8 +676,8 @@ uint64_t tile_partials_bytes(int64_t split_k, int64_t M, int64_t N) {
 }
 
 int64_t tile_tiles(int M, int N, int variant) {
-    const int bm = tile5_rows(variant);
-    return (int64_t)((M + bm - 1) / bm) * ((N + T5_BN - 1) / T5_BN);
+    const int bm = tile5_rows(variant), bn = tile5_cols(variant);
+    return (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
 }
 
 hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* counters, hipStream_t stream) {
@@ -676,6 +691,7 @@ hipError_t launch_tile(const GemmArgs& a, const TileConfig& cfg, uint32_t* count
             case 7: hipLaunchKernelGGL((awq_tile_kernel<8, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
             case 8: hipLaunchKernelGGL((awq_tile_kernel<4, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
             case 9: hipLaunchKernelGGL((awq_tile_kernel<2, 1>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
+            case 15: hipLaunchKernelGGL((awq_tile_kernel<8, 1, false, 8>), grid, dim3(512), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); reduce = true; break;
             case 13: hipLaunchKernelGGL((awq_tile_kernel<8, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
             case 14: hipLaunchKernelGGL((awq_tile_kernel<4, 0, true>), grid, dim3(256), 0, stream, a, cfg.split_k, cfg.k_per_split, counters); break;
             default: return hipErrorInvalidValue;

@@ -72,7 +72,7 @@ def _every_plan(m, n, k):
         makers += [lambda v=v, sp=sp: _native.plan_stream(m, n, k, 2, sp, variant=v) for v in (1, 2, 3)]
         makers += [lambda v=v, sp=sp: _native.plan_stream(m, n, k, 4, sp, variant=v, layout="row")
                    for v in (1, 2, 3)]
-        makers += [lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp) for v in (6, 7, 8, 9)]
+        makers += [lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp) for v in (6, 7, 8, 9, 15)]
     makers += [lambda f=f: _native.plan_skinny(m, n, k, 128, 2, 2, f) for f in (0, 1)]
     plans, seen = [], set()
     for make in makers:

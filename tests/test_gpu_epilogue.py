@@ -38,7 +38,7 @@ def _plans(m, n, k):
                    for sp in (4, 9)]
     if m > 16:
         makers += [(f"tile v{v} s{sp}", lambda v=v, sp=sp: _native.plan_tile(m, n, k, v, sp))
-                   for v, sp in ((6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (13, 2), (14, 3))]
+                   for v, sp in ((6, 1), (6, 2), (7, 3), (8, 2), (9, 4), (13, 2), (14, 3), (15, 1), (15, 2))]
     out = []
     for label, make in makers:
         try:

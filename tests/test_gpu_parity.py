@@ -319,7 +319,7 @@ def test_tile_plans_agree(gpu, m, k, n):
     """Every tile variant, and split-K counts from 1 up, give the same result."""
     x, qw, qz, s = O.make_inputs(m, k, n, seed=15)
     y_ref = O.awq_gemm_oracle(x, qw, qz, s)
-    plans = [(v, sk) for v in (6, 7, 8, 9) for sk in (1, 2, 3, 5, 8)]
+    plans = [(v, sk) for v in (6, 7, 8, 9, 15) for sk in (1, 2, 3, 5, 8)]
     for variant, sk in plans:
         try:
             p = _native.plan_tile(m, n, k, variant, sk)
@@ -328,6 +328,40 @@ def test_tile_plans_agree(gpu, m, k, n):
         print(f"tile plan M={m} K={k} N={n} variant={variant} split_k={sk}", flush=True)
         y = _run(gpu, x, qw, qz, s, plan_obj=p)
         _assert_close(y, y_ref, f"tile M={m} v={variant} split={sk}")
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 18944, 3584), (1000, 8192, 1000), (300, 3584, 2800), (513, 2048, 3000)])
+def test_512_column_tile_matches_256_column_tile(gpu, m, k, n):
+    """Variant 15 (eight waves on 512-column tiles) computes every output as
+    variant 7 does: one wave over the same K order within a split, the splits
+    summed in split order by the same reduce launch.  So at every split both
+    accept the two must be bit-identical -- with ragged M, and ragged N where a
+    512-column tile's second half starts at or beyond N (N = 1000, 2800, 3000)
+    -- and within tolerance of the oracle; one-hot rows of x give each weight
+    exactly."""
+    x, qw, qz, s = O.make_inputs(m, k, n, seed=18)
+    w = O.dequant_awq(qw, qz, s)
+    y_ref = x.astype(np.float32) @ w.astype(np.float32)
+    rows = np.random.default_rng(19).integers(0, k, size=m)
+    x1 = np.zeros((m, k), dtype=np.float16)
+    x1[np.arange(m), rows] = 1.0
+    want = (w[rows] + np.float16(0)).view(np.uint16)
+    tried = 0
+    for sk in (1, 2, 3, 4, 8):
+        try:
+            p15 = _native.plan_tile(m, n, k, 15, sk)
+            p7 = _native.plan_tile(m, n, k, 7, sk)
+        except _native.AwqNativeError:
+            continue
+        print(f"512-column tile M={m} K={k} N={n} split_k={sk} grid={p15.grid}", flush=True)
+        y15 = _run(gpu, x, qw, qz, s, plan_obj=p15)
+        _assert_close(y15, y_ref, f"tile v15 M={m} split={sk}")
+        y7 = _run(gpu, x, qw, qz, s, plan_obj=p7)
+        assert np.array_equal(y15.view(np.uint16), y7.view(np.uint16)), f"v15 != v7 M={m} N={n} split={sk}"
+        y1 = _run(gpu, x1, qw, qz, s, plan_obj=p15)
+        assert np.array_equal((y1 + np.float16(0)).view(np.uint16), want), f"one-hot v15 split={sk}"
+        tried += 1
+    assert tried >= 3
 
 
 @pytest.mark.parametrize("m,k,n", [(2048, 3584, 4608), (2100, 1024, 4104), (2600, 1280, 3584)])
@@ -574,7 +608,7 @@ def test_stream_and_quad_one_hot_bit_exact(gpu):
         if m <= 2:
             plans += [_native.plan_gemv(m, n, k, 0, 4, variant=5, split_k=sp) for sp in (1, 3, 16)]
         if m == 16:
-            plans += [_native.plan_tile(m, n, k, v, sp) for v in (6, 7, 8, 9) for sp in (1, 2, 4)]
+            plans += [_native.plan_tile(m, n, k, v, sp) for v in (6, 7, 8, 9, 15) for sp in (1, 2, 4)]
         for p in plans:
             print(f"one-hot M={m} path={_native.PATH_NAMES[p.path]} v={p.variant} split={p.split_k}", flush=True)
             y = _run(gpu, x, qw, qz, s, plan_obj=p)

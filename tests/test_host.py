@@ -138,7 +138,7 @@ def test_auto_plan_invariants(L, m, k, n):
         assert p.path == _native.PATH_TILE
         if m <= 1024 and -(-m // 128) * -(-n // 256) < 512:
             assert p.variant >= 6           # the register-dequant tiles, by the cost model
-            assert p.variant in (7, 8, 9, 13, 14)   # by the cost model; 6 = 7 with the one-launch finish
+            assert p.variant in (7, 8, 9, 13, 14, 15)   # by the cost model; 6 = 7 with the one-launch finish
     assert p.grid > 0 and p.block_threads % 64 == 0 and p.block_threads <= 1024
     if p.split_k > 1:
         if (p.path == _native.PATH_GEMV and p.variant in (4, 5)) or (p.path == _native.PATH_STREAM and p.variant == 1):
@@ -153,7 +153,7 @@ def test_auto_plan_invariants(L, m, k, n):
             assert p.grid == tiles - left + left * p.split_k
             assert p.workspace_bytes == (_native.counter_bytes() + _native.SLOT_BYTES +
                                          p.split_k * left * tm * 256 * 4)
-        elif p.path == _native.PATH_TILE and p.variant in (7, 8, 9):
+        elif p.path == _native.PATH_TILE and p.variant in (7, 8, 9, 15):
             # reduce launch: fragment-native units of 16 rows x 256 columns
             assert p.workspace_bytes == (_native.counter_bytes() + _native.SLOT_BYTES +
                                          p.split_k * -(-m // 16) * 16 * -(-n // 256) * 256 * 4)
@@ -202,13 +202,13 @@ def test_stream_split_keeps_a_group_and_a_half_per_split(L):
 @pytest.mark.parametrize("k,n", SHAPES)
 def test_tile_plans_cover_k_exactly(L, k, n):
     """Every split-K plan gives each split a whole number of 64-row k-steps
-    (variants 6..9, 13, 14: of 128-row groups) and covers K exactly; the tile count fits
+    (variants 6..9, 13, 14, 15: of 128-row groups) and covers K exactly; the tile count fits
     the arrival-counter block.  The hybrids (13, 14) put `full` whole tiles on
     each of the 256 CUs (fewer than a CU holds) and split the leftover tiles,
     at most one piece per CU, with compact partials.  Variant numbers without a
     kernel are refused."""
     for m in (512, 2048):
-        for variant in range(1, 16):
+        for variant in range(1, 17):
             for split in (1, 2, 3, 4, 5, 8):
                 try:
                     p = _native.plan_tile(m, n, k, variant, split)
@@ -216,12 +216,13 @@ def test_tile_plans_cover_k_exactly(L, k, n):
                     # no such kernel or split, or partials beyond 2^31 bytes (M = 2048, 8 splits)
                     assert e.status in (_native.AWQ_ERR_PATH, _native.AWQ_ERR_TOO_LARGE)
                     continue
-                assert variant in (6, 7, 8, 9, 13, 14)
+                assert variant in (6, 7, 8, 9, 13, 14, 15)
                 per = p.rows_per_wave
                 assert per % 128 == 0
                 assert (split - 1) * per < k <= split * per
                 tm = {6: 128, 7: 128, 8: 64, 9: 32, 14: 64}.get(variant, 128)
-                tn = 256
+                tn = 512 if variant == 15 else 256
+                assert (p.tile_m, p.tile_n, p.block_threads) == (tm, tn, 512 if variant == 15 else 256)
                 tiles = -(-m // tm) * -(-n // tn)
                 if variant in (13, 14):
                     full, left = tiles // 256, tiles % 256
@@ -235,34 +236,67 @@ def test_tile_plans_cover_k_exactly(L, k, n):
                     assert tiles * 4 <= _native.counter_bytes()
 
 
-@pytest.mark.parametrize("m,n,bm", [(16, 4608, 32), (64, 3584, 64), (70, 264, 64), (300, 1032, 128)])
-def test_tile_fragment_partials_layout_agrees(m, n, bm):
+def test_deep_weights_take_the_512_column_tile(L):
+    """On deep weights (K >= 8192) at M >= 512, AUTO takes the eight-wave
+    512-column tile (variant 15) at the largest split (of whole 128-row
+    groups, at most 32) whose grid fits one workgroup per CU, and otherwise
+    keeps the 256-column tiles: below M = 512, on shallow weights, and where
+    even one split needs more than 256 workgroups (M = 8192 on down_proj)."""
+    for k, n in ((18944, 3584), (8192, 1000), (18944, 3000)):
+        groups = k // 128
+        for m in (256, 511, 512, 768, 1000, 1024, 1536, 2048, 4096, 8192):
+            p = _native.plan_for(m, n, k)
+            tiles = -(-m // 128) * -(-n // 512)
+            valid = [s for s in range(1, min(groups, 32) + 1) if -(-groups // -(-groups // s)) == s]
+            fits = [s for s in valid if tiles * s <= 256]
+            if m >= 512 and fits:
+                assert (p.path, p.variant, p.split_k) == (_native.PATH_TILE, 15, max(fits)), (m, k, n)
+                assert p.grid == tiles * p.split_k <= 256 and p.block_threads == 512 and p.tile_n == 512
+            else:
+                assert not (p.path == _native.PATH_TILE and p.variant == 15), (m, k, n)
+    for m in (512, 2048, 4096):
+        for k, n in ((3584, 37888), (3584, 4608), (3584, 3584)):
+            assert _native.plan_for(m, n, k).variant != 15
+
+
+@pytest.mark.parametrize("m,n,bm,waves", [(16, 4608, 32, 4), (64, 3584, 64, 4), (70, 264, 64, 4), (300, 1032, 128, 4),
+                                         (64, 3584, 128, 8), (300, 1032, 128, 8), (70, 2800, 128, 8)])
+def test_tile_fragment_partials_layout_agrees(m, n, bm, waves):
     """The layout contract between the tile kernel's fragment-native partial
     stores and the tile reduce kernel (both in csrc/awq_tile.hip), restated
     from each side: the store side addresses lane l's value r of fragment
     (wave, c, f) of a tile, the reduce side addresses the 8-column piece of a
     thread.  Every output of every split must be read from exactly the bytes
-    written for it, and every written byte of a row below M read once."""
+    written for it, every written byte of a row below M read once, and no two
+    stores may write the same bytes.  Eight-wave tiles (512 columns) write two
+    256-column units, waves 4 .. 7 the second, and none where it starts at or
+    beyond N (N = 1032 and 2800 end inside a 512-column tile's first half)."""
     split = 3
     rb_n, nt = -(-m // 16), -(-n // 256)
+    bn = 64 * waves
     # Store side: (split, tile, wave, f, c, lane, r) -> byte offset, output (row, col).
-    store = {}
+    store, offsets = {}, []
     for s in range(split):
         for m0 in range(0, m, bm):
-            for n0 in range(0, nt * 256, 256):
+            for n0 in range(0, -(-n // bn) * bn, bn):
                 for f in range(bm // 16):
                     if m0 + 16 * f >= m:
                         break
-                    unit = (s * rb_n + m0 // 16 + f) * nt + n0 // 256
-                    for w in range(4):
+                    for w in range(waves):
+                        tn = n0 // 256 + (w >> 2)
+                        if tn >= nt:
+                            continue
+                        unit = (s * rb_n + m0 // 16 + f) * nt + tn
                         for c in range(4):
                             for lane in range(64):
                                 kb = lane // 16
                                 for r in range(4):
                                     row = m0 + 16 * f + lane % 16
                                     col = n0 + 64 * w + 16 * c + 8 * (kb >> 1) + 2 * r + (kb & 1)
-                                    off = unit * 16384 + (4 * w + c) * 1024 + lane * 16 + 4 * r
+                                    off = unit * 16384 + (4 * (w & 3) + c) * 1024 + lane * 16 + 4 * r
                                     store[(s, row, col)] = off
+                                    offsets.append(off)
+    assert len(set(offsets)) == len(offsets)
     # Reduce side: piece -> its output row and 8 columns, the float4s it reads per split.
     read = {}
     for piece in range(rb_n * nt * 512):
