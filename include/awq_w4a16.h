@@ -143,7 +143,10 @@ int awq_w4a16_plan_skinny(int64_t M, int64_t N, int64_t K, int32_t group_size,
  * tiles split split_k >= 2 ways along K, at most one piece per CU (grid =
  * full x CUs + L x split_k), the pieces' partials compact ([split_k, L,
  * rows, 256] fp32) and added by each leftover tile's last-arriving piece;
- * other shapes get AWQ_ERR_PATH.  Every variant takes split_k >= 1
+ * other shapes get AWQ_ERR_PATH; variant 15: variant 7 with eight
+ * wavefronts on 128 x 512 tiles (one workgroup per CU, x rows loaded once
+ * per 512 columns), bit-identical to variant 7 at the same split_k (plan
+ * tile_n 512, block_threads 512).  Every variant takes split_k >= 1
  * workgroups along K in whole 128-row groups; the plan's rows_per_wave holds
  * the K rows per split.  Other variant numbers (1 .. 5 and the retired
  * 10 .. 12 included): AWQ_ERR_PATH. */
