@@ -431,7 +431,8 @@ def _plan_kernel_key(_native, m, n, k):
     path = _native.PATH_NAMES[p.path]
     if path == "tile":
         fin = 0 if p.variant in (6, 13, 14) else 1
-        name = f"awq_tile_kernel<{p.tile_m // 16}, {fin}, {'true' if p.variant in (13, 14) else 'false'}>"
+        hy = "true" if p.variant in (13, 14) else "false"
+        name = f"awq_tile_kernel<{p.tile_m // 16}, {fin}, {hy}, {p.block_threads // 64}>"
     else:
         name = FAMILY_KERNELS[path][0]
     return name, int(p.grid), int(p.block_threads), p
