@@ -206,7 +206,7 @@ int awq_w4a16_plan_stream(int64_t M, int64_t N, int64_t K, int32_t group_size, i
  *   [64-bit fixed-point slots, one per output element [M, N]: at most
  *    AWQ_W4A16_SLOT_BYTES (GEMV variant 5 and stream variant 1)]
  *   [fp32 partial sums (every other split-K plan): [split_k, M, N]; for
- *    tile variants 7, 8 and 9 units of 16 rows x 256 columns in the MFMA
+ *    tile variants 7, 8, 9 and 15 units of 16 rows x 256 columns in the MFMA
  *    accumulators' lane order, [split_k, ceil(M/16), ceil(N/256), 16 KB];
  *    for the hybrid tile variants 13 and 14 only the leftover tiles',
  *    [split_k, leftover tiles, tile rows, 256]]
