@@ -662,12 +662,17 @@ int tile_plan(int64_t M, int64_t N, int64_t K, awq_w4a16_plan* p) {
     // put a second workgroup on some CUs were slower (M = 2048 split 3 331.6,
     // M = 4096 split 2 521.3), and at K = 3584 the 512-column tile lost to the
     // 256-column one (o at M = 2048 66.7 against 59.1 us; gate||up even).
+    // Every measured grid covered at least 7/8 of the CUs (224 - 252 of 256);
+    // where that split leaves more CUs idle the cost model below decides.
     if (K >= 8192 && M >= 512) {
         for (int64_t sp = groups < 32 ? groups : 32; sp >= 1; --sp) {
             awq_w4a16_plan q;
             if (fill_tile(M, N, K, 15, sp, &q) == AWQ_OK && q.grid <= (int64_t)cus()) {
-                *p = q;
-                return AWQ_OK;
+                if (q.grid * 8 >= (int64_t)cus() * 7) {
+                    *p = q;
+                    return AWQ_OK;
+                }
+                break;
             }
         }
     }

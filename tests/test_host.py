@@ -239,17 +239,19 @@ def test_tile_plans_cover_k_exactly(L, k, n):
 def test_deep_weights_take_the_512_column_tile(L):
     """On deep weights (K >= 8192) at M >= 512, AUTO takes the eight-wave
     512-column tile (variant 15) at the largest split (of whole 128-row
-    groups, at most 32) whose grid fits one workgroup per CU, and otherwise
-    keeps the 256-column tiles: below M = 512, on shallow weights, and where
-    even one split needs more than 256 workgroups (M = 8192 on down_proj)."""
-    for k, n in ((18944, 3584), (8192, 1000), (18944, 3000)):
+    groups, at most 32) whose grid fits one workgroup per CU, where that grid
+    covers at least 7/8 of the 256 CUs; otherwise it keeps the 256-column
+    tiles: below M = 512, on shallow weights, where even one split needs more
+    than 256 workgroups (M = 8192 on down_proj), and where the best fit leaves
+    CUs idle (M = 2760, N = 2896: 132 workgroups at split 1)."""
+    for k, n in ((18944, 3584), (8192, 1000), (18944, 3000), (11520, 2896)):
         groups = k // 128
-        for m in (256, 511, 512, 768, 1000, 1024, 1536, 2048, 4096, 8192):
+        for m in (256, 511, 512, 768, 1000, 1024, 1536, 2048, 2760, 4096, 8192):
             p = _native.plan_for(m, n, k)
             tiles = -(-m // 128) * -(-n // 512)
             valid = [s for s in range(1, min(groups, 32) + 1) if -(-groups // -(-groups // s)) == s]
             fits = [s for s in valid if tiles * s <= 256]
-            if m >= 512 and fits:
+            if m >= 512 and fits and tiles * max(fits) * 8 >= 256 * 7:
                 assert (p.path, p.variant, p.split_k) == (_native.PATH_TILE, 15, max(fits)), (m, k, n)
                 assert p.grid == tiles * p.split_k <= 256 and p.block_threads == 512 and p.tile_n == 512
             else:
