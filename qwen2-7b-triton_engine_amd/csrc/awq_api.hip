@@ -869,9 +869,13 @@ int noalloc_plan(int64_t M, int64_t N, int64_t K, int32_t group_size, awq_w4a16_
     const int st = awq_w4a16_plan_for(M, N, K, group_size, AWQ_PATH_AUTO, p);
     if (st != AWQ_OK || p->workspace_bytes <= kScratchBytes) return st;
     if (p->path != AWQ_PATH_TILE) return AWQ_ERR_SCRATCH;
+    // Fewer splits shrink the 512-column tile's grid below the CU count it
+    // was chosen for; the 256-column tile (variant 7) at the same split needs
+    // the same workspace and has twice the workgroups.
+    const int64_t v = p->variant == 15 ? 7 : p->variant;
     for (int64_t sp = p->split_k - 1; sp >= 1; --sp) {
         awq_w4a16_plan q;
-        if (fill_tile(M, N, K, p->variant, sp, &q) == AWQ_OK && q.workspace_bytes <= kScratchBytes) {
+        if (fill_tile(M, N, K, v, sp, &q) == AWQ_OK && q.workspace_bytes <= kScratchBytes) {
             *p = q;
             return AWQ_OK;
         }

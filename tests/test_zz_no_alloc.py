@@ -53,7 +53,7 @@ CASES = [
     ("gate_up_proj", 3584, 37888, 4, 2),    # stream fixed-point slots, at M = 4 and 2
     ("down_proj", 18944, 3584, 16, 8),      # 16-row column singles split 8 + reduce launch; 8-row ones at M = 8
     ("o_proj", 3584, 3584, 300, 5),         # tile split-K (reduce launch); column-single GEMV at M = 5
-    ("down_proj", 18944, 3584, 2048, 512),  # tile plan lowered to fit the scratch; tile split 4 (28 MB)
+    ("down_proj", 18944, 3584, 2048, 512),  # 512-column tile plans lowered to the 256-column tile: split 1, then 4 (28 MB)
     ("qkv_proj", 3584, 4608, 2048, 1025),   # hybrid tiles (compact partials, last arrivers)
     ("k_proj", 3584, 512, 16, 4),           # 16-row column singles split 64 + reduce; slim singles split 28
     ("gate_proj", 3584, 18944, 2, 1),       # column pairs split 3 (fixed-point slots), at M = 2 and 1
