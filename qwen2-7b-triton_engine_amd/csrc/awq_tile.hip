@@ -1,5 +1,6 @@
 // Prefill W4A16 AWQ GEMM (large M) for gfx950: LDS-tiled MFMA kernels
-// (awq_tile_kernel, tile variants 6 .. 9, 13, 14): 256 output columns per tile,
+// (awq_tile_kernel, tile variants 6 .. 9, 13, 14, 15): 256 output columns per
+// tile (512 for variant 15),
 // weights dequantised straight into MFMA operand registers, every operand
 // streamed into LDS rings by direct global->LDS loads, the reference's exact
 // fp16 weight fp16((q - z) * s) formed next to the load.
@@ -9,7 +10,8 @@ namespace awq {
 
 // ---------------------------------------------------------------------------
 // Tile variants 6 .. 9, 13, 14: 256 output columns per tile, four waves of 64
-// columns x 32, 64 or 128 x rows, weights dequantised straight into MFMA A
+// columns x 32, 64 or 128 x rows (variant 15: eight such waves, 512 columns
+// x 128 rows), weights dequantised straight into MFMA A
 // registers (never written back to LDS), every global load a direct
 // global->LDS load issued two k-steps ahead into a 3-stage ring.  No VGPR
 // holds data in flight and the compiler sees no global load inside the main
@@ -21,7 +23,7 @@ namespace awq {
 //     k-chunk p ^ (r & 7), so the MFMA fragment reads of 8 consecutive rows
 //     hit 8 distinct chunk positions (all banks once); rows beyond M read as
 //     zeros (buffer range check); a wave's dwordx4 load writes 8 rows.
-//   * packed weights, 64 rows x 32 packed columns: wave w's 2 KB holds its
+//   * packed weights, 64 rows x 8 packed columns a wave: wave w's 2 KB holds its
 //     packed columns 8 w .. + 7 row-major (32 B a row, the two 16-byte halves
 //     of row r swapped when bit 3 of r is set), loaded by two dwordx4 loads
 //     and read back column-wise with LDS transpose reads.
